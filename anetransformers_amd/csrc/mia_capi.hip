@@ -1,0 +1,453 @@
+// mia_capi.hip -- extern "C" shim of libmiattn.so (see include/miattn.h).
+// Host code only: validation, per-device context (stream, split-K scratch,
+// arrival counters, work buffers) and launch planning.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/miattn.h"
+#include "mia_kernels.h"
+
+namespace {
+
+constexpr int kMaxDevices = 16;
+constexpr int kG = 4;
+constexpr int kHD = 128;
+constexpr int kMaxSeq = 1 << 22;  // keeps 32-bit in-layer element offsets exact
+
+struct DevCtx {
+  bool ready = false;
+  hipStream_t stream = nullptr;
+  int num_cus = 256;
+  void *scratch = nullptr;  // split-K partials
+  size_t scratch_bytes = 0;
+  unsigned *counters = nullptr;  // arrival counters, zero between launches
+  size_t n_counters = 0;
+  void *work = nullptr;  // rotated Q + fp16 staging for mia_attention_step
+  size_t work_bytes = 0;
+};
+
+DevCtx g_ctx[kMaxDevices];
+std::mutex g_mu;
+thread_local char g_err[512] = "";
+
+int set_err(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+#define HIP_TRY(call)                                                                    \
+  do {                                                                                   \
+    hipError_t e_ = (call);                                                              \
+    if (e_ != hipSuccess)                                                                \
+      return set_err(MIA_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_));       \
+  } while (0)
+
+int current_ctx(DevCtx **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_err(MIA_ERR_NO_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return set_err(MIA_ERR_NO_DEVICE, "device %d out of range", dev);
+  if (!g_ctx[dev].ready) {
+    int rc = mia_init(dev);
+    if (rc) return rc;
+  }
+  *out = &g_ctx[dev];
+  return MIA_OK;
+}
+
+hipStream_t pick_stream(DevCtx *c, void *stream) {
+  return stream ? reinterpret_cast<hipStream_t>(stream) : c->stream;
+}
+
+// Grows the split-K scratch and the counters.  Growth synchronises the device
+// so that no queued kernel still uses the old buffers.
+int ensure_scratch(DevCtx *c, size_t bytes, size_t n_counters) {
+  if (bytes > c->scratch_bytes) {
+    HIP_TRY(hipDeviceSynchronize());
+    if (c->scratch) HIP_TRY(hipFree(c->scratch));
+    c->scratch = nullptr;
+    c->scratch_bytes = 0;
+    size_t sz = bytes + (bytes >> 2);
+    HIP_TRY(hipMalloc(&c->scratch, sz));
+    c->scratch_bytes = sz;
+  }
+  if (n_counters > c->n_counters) {
+    HIP_TRY(hipDeviceSynchronize());
+    if (c->counters) HIP_TRY(hipFree(c->counters));
+    c->counters = nullptr;
+    c->n_counters = 0;
+    size_t n = n_counters < 1024 ? 1024 : n_counters * 2;
+    HIP_TRY(hipMalloc(&c->counters, n * sizeof(unsigned)));
+    HIP_TRY(hipMemset(c->counters, 0, n * sizeof(unsigned)));
+    c->n_counters = n;
+  }
+  return MIA_OK;
+}
+
+int ensure_work(DevCtx *c, size_t bytes) {
+  if (bytes > c->work_bytes) {
+    HIP_TRY(hipDeviceSynchronize());
+    if (c->work) HIP_TRY(hipFree(c->work));
+    c->work = nullptr;
+    c->work_bytes = 0;
+    HIP_TRY(hipMalloc(&c->work, bytes));
+    c->work_bytes = bytes;
+  }
+  return MIA_OK;
+}
+
+int check_shape(int n_heads, int n_kv_heads, int hd, int max_seq) {
+  if (n_heads <= 0 || n_kv_heads <= 0 || hd <= 0 || max_seq <= 0)
+    return set_err(MIA_ERR_INVALID, "sizes must be positive (n_heads=%d n_kv_heads=%d hd=%d max_seq=%d)",
+                   n_heads, n_kv_heads, hd, max_seq);
+  if (n_heads % n_kv_heads)
+    return set_err(MIA_ERR_INVALID, "n_heads %d not a multiple of n_kv_heads %d", n_heads, n_kv_heads);
+  if (hd != kHD) return set_err(MIA_ERR_UNSUPPORTED, "head_dim %d unsupported (kernels need 128)", hd);
+  if (n_heads / n_kv_heads != kG)
+    return set_err(MIA_ERR_UNSUPPORTED, "GQA ratio %d unsupported (kernels need 4)", n_heads / n_kv_heads);
+  if (max_seq > kMaxSeq) return set_err(MIA_ERR_UNSUPPORTED, "max_seq %d above %d", max_seq, kMaxSeq);
+  if (n_kv_heads > 64) return set_err(MIA_ERR_UNSUPPORTED, "n_kv_heads %d above 64", n_kv_heads);
+  return MIA_OK;
+}
+
+int check_pos(int pos, int S) {
+  if (pos < 0 || S < 1) return set_err(MIA_ERR_INVALID, "bad position %d / token count %d", pos, S);
+  if ((long)pos + S >= (long)INT_MAX) return set_err(MIA_ERR_INVALID, "position %d + %d overflows", pos, S);
+  return MIA_OK;
+}
+
+float qscale_log2() { return (1.0f / sqrtf((float)kHD)) * 1.4426950408889634f; }
+
+int decode_impl(const float *q, const float *k, const float *v, const float *theta_inv,
+                uint16_t *k_layer, uint16_t *v_layer, float *out, int n_heads, int n_kv, int max_seq,
+                int pos, bool fused, void *stream) {
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  const int L = pos + 1 < max_seq ? pos + 1 : max_seq;
+  const long start = ((long)pos + 1 - L) % max_seq;
+  mia::DecodeParams p{};
+  p.q = q;
+  p.knew = k;
+  p.vnew = v;
+  p.theta_inv = theta_inv;
+  p.kc = reinterpret_cast<_Float16 *>(k_layer);
+  p.vc = reinterpret_cast<_Float16 *>(v_layer);
+  p.out = out;
+  p.max_seq = max_seq;
+  p.pos = pos;
+  p.L = L;
+  p.start = (int)start;
+  p.new_slot = pos % max_seq;
+  p.n_kv = n_kv;
+  p.chunk_rows = mia::decode_pick_chunk_rows(L, n_kv, 2 * c->num_cus);
+  p.nchunk = (L + p.chunk_rows - 1) / p.chunk_rows;
+  p.qscale = qscale_log2();
+  if (p.nchunk > 1) {
+    if (int rc = ensure_scratch(c, mia::decode_scratch_bytes(n_kv, kG, p.nchunk), (size_t)n_kv))
+      return rc;
+    p.part_o = reinterpret_cast<float *>(c->scratch);
+    p.part_ml = p.part_o + (size_t)n_kv * p.nchunk * kG * kHD;
+    p.counter = c->counters;
+  }
+  HIP_TRY(mia::launch_decode(p, kG, fused, pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int flash_impl(DevCtx *c, const float *Q, const uint16_t *kst, const uint16_t *vst,
+               const uint16_t *k_layer, const uint16_t *v_layer, float *out, int n_kv, int max_seq,
+               int start_pos, int S, hipStream_t s) {
+  mia::FlashParams p{};
+  int rt = 0;
+  mia::flash_plan(S, n_kv, kG, start_pos, max_seq, 4 * c->num_cus, &p.n_rtiles, &p.nsplit,
+                  &p.split_keys, &rt);
+  p.Q = Q;
+  p.kc = reinterpret_cast<const _Float16 *>(k_layer);
+  p.vc = reinterpret_cast<const _Float16 *>(v_layer);
+  p.kstage = reinterpret_cast<const _Float16 *>(kst);
+  p.vstage = reinterpret_cast<const _Float16 *>(vst);
+  p.out = out;
+  p.S = S;
+  p.n_kv = n_kv;
+  p.max_seq = max_seq;
+  p.start_pos = start_pos;
+  p.qscale = qscale_log2();
+  if (p.nsplit > 1) {
+    size_t ntile = (size_t)n_kv * p.n_rtiles;
+    if (int rc = ensure_scratch(c, mia::flash_scratch_bytes(n_kv, p.n_rtiles, p.nsplit, rt), ntile))
+      return rc;
+    p.part_o = reinterpret_cast<float *>(c->scratch);
+    p.part_ml = p.part_o + ntile * p.nsplit * rt * kHD;
+    p.counter = c->counters;
+  }
+  HIP_TRY(mia::launch_flash(p, kG, s, nullptr));
+  return MIA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mia_version(void) { return 100; }
+
+const char *mia_last_error(void) { return g_err; }
+
+int mia_device_count(int *count) {
+  if (!count) return set_err(MIA_ERR_INVALID, "count is NULL");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) {
+    *count = 0;
+    return set_err(MIA_ERR_NO_DEVICE, "hipGetDeviceCount: %s", hipGetErrorString(e));
+  }
+  *count = n;
+  return MIA_OK;
+}
+
+int mia_init(int device) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0)
+    return set_err(MIA_ERR_NO_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+  if (device < 0 || device >= n || device >= kMaxDevices)
+    return set_err(MIA_ERR_INVALID, "device %d out of range (%d devices)", device, n);
+  HIP_TRY(hipSetDevice(device));
+  DevCtx &c = g_ctx[device];
+  if (c.ready) return MIA_OK;
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, device));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return set_err(MIA_ERR_UNSUPPORTED, "device %d is %s; libmiattn is built for gfx950", device,
+                   prop.gcnArchName);
+  c.num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+  HIP_TRY(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
+  c.ready = true;
+  return MIA_OK;
+}
+
+int mia_malloc(void **dptr, size_t bytes) {
+  if (!dptr) return set_err(MIA_ERR_INVALID, "dptr is NULL");
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  HIP_TRY(hipMalloc(dptr, bytes ? bytes : 1));
+  return MIA_OK;
+}
+
+int mia_free(void *dptr) {
+  if (dptr) HIP_TRY(hipFree(dptr));
+  return MIA_OK;
+}
+
+int mia_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+  if (bytes == 0) return MIA_OK;
+  if (!dst || !src) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  return MIA_OK;
+}
+
+int mia_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+  if (bytes == 0) return MIA_OK;
+  if (!dst || !src) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return MIA_OK;
+}
+
+int mia_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+  if (bytes == 0) return MIA_OK;
+  if (!dst || !src) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+  return MIA_OK;
+}
+
+int mia_memset(void *dst, int value, size_t bytes) {
+  if (bytes == 0) return MIA_OK;
+  if (!dst) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  HIP_TRY(hipMemset(dst, value, bytes));
+  return MIA_OK;
+}
+
+int mia_stream_create(void **stream) {
+  if (!stream) return set_err(MIA_ERR_INVALID, "stream is NULL");
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  hipStream_t s;
+  HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *stream = s;
+  return MIA_OK;
+}
+
+int mia_stream_destroy(void *stream) {
+  if (stream) HIP_TRY(hipStreamDestroy(reinterpret_cast<hipStream_t>(stream)));
+  return MIA_OK;
+}
+
+int mia_stream_sync(void *stream) {
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  HIP_TRY(hipStreamSynchronize(pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_device_sync(void) {
+  HIP_TRY(hipDeviceSynchronize());
+  return MIA_OK;
+}
+
+int mia_event_create(void **event) {
+  if (!event) return set_err(MIA_ERR_INVALID, "event is NULL");
+  hipEvent_t e;
+  HIP_TRY(hipEventCreate(&e));
+  *event = e;
+  return MIA_OK;
+}
+
+int mia_event_destroy(void *event) {
+  if (event) HIP_TRY(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)));
+  return MIA_OK;
+}
+
+int mia_event_record(void *event, void *stream) {
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  HIP_TRY(hipEventRecord(reinterpret_cast<hipEvent_t>(event), pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_event_elapsed_ms(float *ms, void *start, void *stop) {
+  if (!ms) return set_err(MIA_ERR_INVALID, "ms is NULL");
+  HIP_TRY(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
+                              reinterpret_cast<hipEvent_t>(stop)));
+  return MIA_OK;
+}
+
+int mia_fill_normal_f16(uint16_t *dst, size_t n, uint64_t seed, void *stream) {
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  if (!dst && n) return set_err(MIA_ERR_INVALID, "dst is NULL");
+  HIP_TRY(mia::launch_fill_normal(reinterpret_cast<_Float16 *>(dst), n, seed, pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_scale_rows_f16(uint16_t *base, long n_rows, int row_elems, int every, int offset,
+                       float factor, void *stream) {
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  if (!base || n_rows < 0 || row_elems <= 0 || every <= 0 || offset < 0)
+    return set_err(MIA_ERR_INVALID, "bad scale_rows arguments");
+  HIP_TRY(mia::launch_scale_rows(reinterpret_cast<_Float16 *>(base), n_rows, row_elems, every,
+                                 offset, factor, pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_rope_f32(float *q, float *k, int S, int start_pos, const float *theta_inv, int n_heads,
+                 int n_kv_heads, int head_dim, void *stream) {
+  if (head_dim != kHD) return set_err(MIA_ERR_UNSUPPORTED, "head_dim %d unsupported", head_dim);
+  if (!theta_inv) return set_err(MIA_ERR_INVALID, "theta_inv is NULL");
+  if ((q && n_heads <= 0) || (k && n_kv_heads <= 0)) return set_err(MIA_ERR_INVALID, "bad head counts");
+  if (int rc = check_pos(start_pos, S)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  HIP_TRY(mia::launch_rope(q, k, S, start_pos, theta_inv, q ? n_heads : 0, k ? n_kv_heads : 0,
+                           pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_kv_write_f32(uint16_t *k_layer, uint16_t *v_layer, const float *K, const float *V, int S,
+                     int start_pos, int max_seq, int kv_dim, void *stream) {
+  if (!k_layer || !v_layer || !K || !V) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (kv_dim <= 0 || max_seq <= 0 || max_seq > kMaxSeq) return set_err(MIA_ERR_INVALID, "bad kv_dim/max_seq");
+  if (int rc = check_pos(start_pos, S)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  HIP_TRY(mia::launch_kv_write(reinterpret_cast<_Float16 *>(k_layer),
+                               reinterpret_cast<_Float16 *>(v_layer), K, V, S, start_pos, max_seq,
+                               kv_dim, pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_gqa_attention(const float *q, float *out, const uint16_t *k_layer, const uint16_t *v_layer,
+                      int n_heads, int heads_per_kv, int hd, int max_seq, int pos, void *stream) {
+  if (!q || !out || !k_layer || !v_layer) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (heads_per_kv <= 0) return set_err(MIA_ERR_INVALID, "heads_per_kv %d", heads_per_kv);
+  const int n_kv = n_heads / heads_per_kv;
+  if (n_kv * heads_per_kv != n_heads) return set_err(MIA_ERR_INVALID, "n_heads/heads_per_kv mismatch");
+  if (int rc = check_shape(n_heads, n_kv, hd, max_seq)) return rc;
+  if (int rc = check_pos(pos, 1)) return rc;
+  return decode_impl(q, nullptr, nullptr, nullptr, const_cast<uint16_t *>(k_layer),
+                     const_cast<uint16_t *>(v_layer), out, n_heads, n_kv, max_seq, pos, false, stream);
+}
+
+int mia_decode_step(const float *q, const float *k, const float *v, const float *theta_inv,
+                    uint16_t *k_layer, uint16_t *v_layer, float *out, int n_heads, int n_kv_heads,
+                    int hd, int max_seq, int pos, void *stream) {
+  if (!q || !k || !v || !theta_inv || !out || !k_layer || !v_layer)
+    return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (int rc = check_shape(n_heads, n_kv_heads, hd, max_seq)) return rc;
+  if (int rc = check_pos(pos, 1)) return rc;
+  return decode_impl(q, k, v, theta_inv, k_layer, v_layer, out, n_heads, n_kv_heads, max_seq, pos,
+                     true, stream);
+}
+
+int mia_attention_batch(const float *Q, float *out, const uint16_t *k_layer, const uint16_t *v_layer,
+                        int n_heads, int n_kv_heads, int hd, int max_seq, int start_pos, int S,
+                        void *stream) {
+  if (!Q || !out || !k_layer || !v_layer) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (int rc = check_shape(n_heads, n_kv_heads, hd, max_seq)) return rc;
+  if (int rc = check_pos(start_pos, S)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  return flash_impl(c, Q, nullptr, nullptr, k_layer, v_layer, out, n_kv_heads, max_seq, start_pos,
+                    S, pick_stream(c, stream));
+}
+
+int mia_attention_step(const float *Q, const float *K, const float *V, const float *theta_inv,
+                       uint16_t *k_layer, uint16_t *v_layer, float *out, int n_heads,
+                       int n_kv_heads, int hd, int max_seq, int start_pos, int S, void *stream) {
+  if (!Q || !K || !V || !theta_inv || !out || !k_layer || !v_layer)
+    return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (int rc = check_shape(n_heads, n_kv_heads, hd, max_seq)) return rc;
+  if (int rc = check_pos(start_pos, S)) return rc;
+  if (S == 1)
+    return decode_impl(Q, K, V, theta_inv, k_layer, v_layer, out, n_heads, n_kv_heads, max_seq,
+                       start_pos, true, stream);
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  hipStream_t s = pick_stream(c, stream);
+  const int kv_dim = n_kv_heads * kHD;
+  const size_t q_bytes = (size_t)S * n_heads * kHD * sizeof(float);
+  const size_t st_bytes = (size_t)S * kv_dim * sizeof(uint16_t);
+  if (int rc = ensure_work(c, q_bytes + 2 * st_bytes)) return rc;
+  float *Qr = reinterpret_cast<float *>(c->work);
+  _Float16 *kst = reinterpret_cast<_Float16 *>(reinterpret_cast<char *>(c->work) + q_bytes);
+  _Float16 *vst = kst + (size_t)S * kv_dim;
+  HIP_TRY(hipMemcpyAsync(Qr, Q, q_bytes, hipMemcpyDeviceToDevice, s));
+  HIP_TRY(mia::launch_rope(Qr, nullptr, S, start_pos, theta_inv, n_heads, 0, s));
+  // Drafts may go straight into the ring when no slot they take still holds
+  // a position some query of the batch attends (start_pos + S <= max_seq).
+  const bool direct = (long)start_pos + S <= (long)max_seq;
+  if (direct) {
+    HIP_TRY(mia::launch_rope_to_ring(K, V, theta_inv, S, start_pos, n_kv_heads,
+                                     reinterpret_cast<_Float16 *>(k_layer),
+                                     reinterpret_cast<_Float16 *>(v_layer), max_seq, s));
+    return flash_impl(c, Qr, nullptr, nullptr, k_layer, v_layer, out, n_kv_heads, max_seq,
+                      start_pos, S, s);
+  }
+  HIP_TRY(mia::launch_rope_to_f16(K, V, theta_inv, S, start_pos, n_kv_heads, kst, vst, s));
+  if (int rc = flash_impl(c, Qr, reinterpret_cast<uint16_t *>(kst), reinterpret_cast<uint16_t *>(vst),
+                          k_layer, v_layer, out, n_kv_heads, max_seq, start_pos, S, s))
+    return rc;
+  HIP_TRY(mia::launch_commit(reinterpret_cast<_Float16 *>(k_layer),
+                             reinterpret_cast<_Float16 *>(v_layer), kst, vst, S, start_pos, max_seq,
+                             kv_dim, s));
+  return MIA_OK;
+}
+
+}  // extern "C"

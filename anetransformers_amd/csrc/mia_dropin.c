@@ -1,0 +1,248 @@
+/*
+ * mia_dropin.c -- host C side of the drop-in: the reference's attention-step
+ * signatures (include/mia_dropin.h) implemented over the libmiattn C ABI.
+ * Host buffers are staged through one device buffer owned by this file;
+ * every call is synchronous, like the reference's.  Not re-entrant (neither is
+ * the reference: mistral_model.h shares m->q / m->att across calls).
+ */
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../../include/mia_dropin.h"
+
+static int g_abort = 1;
+static __thread int g_status = 0;
+static char *g_dbuf = NULL;
+static size_t g_dbuf_bytes = 0;
+
+void mia_dropin_set_abort(int abort_on_error) { g_abort = abort_on_error; }
+int mia_dropin_status(void) { return g_status; }
+
+static int fail(int rc, const char *what) {
+    g_status = rc;
+    if (rc && g_abort) {
+        fprintf(stderr, "miattn: %s failed (status %d): %s\n", what, rc, mia_last_error());
+        abort();
+    }
+    return rc;
+}
+
+#define TRY(what, call)                  \
+    do {                                 \
+        int rc_ = (call);                \
+        if (rc_) {                       \
+            fail(rc_, what);             \
+            return;                      \
+        }                                \
+    } while (0)
+
+/* Device staging area of at least `bytes`, carved by the callers. */
+static int dbuf(size_t bytes) {
+    if (bytes <= g_dbuf_bytes) return MIA_OK;
+    if (g_dbuf) {
+        int rc = mia_free(g_dbuf);
+        if (rc) return rc;
+    }
+    g_dbuf = NULL;
+    g_dbuf_bytes = 0;
+    size_t sz = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    int rc = mia_malloc((void **)&g_dbuf, sz);
+    if (rc) return rc;
+    g_dbuf_bytes = sz;
+    return MIA_OK;
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+void mia_dropin_kv_alloc(KVCache *c, int n_layers, int n_kv_heads, int head_dim, int max_seq) {
+    g_status = 0;
+    c->n_layers = n_layers;
+    c->n_kv_heads = n_kv_heads;
+    c->head_dim = head_dim;
+    c->max_seq = max_seq;
+    c->kv_dim = n_kv_heads * head_dim;
+    c->k_cache = NULL;
+    c->v_cache = NULL;
+    c->pos = 0;
+    c->len = 0;
+    if (n_layers <= 0 || n_kv_heads <= 0 || head_dim <= 0 || max_seq <= 0) {
+        fail(MIA_ERR_INVALID, "kv_alloc (non-positive size)");
+        return;
+    }
+    size_t sz = (size_t)n_layers * max_seq * c->kv_dim * sizeof(_Float16);
+    TRY("kv_alloc", mia_malloc((void **)&c->k_cache, sz));
+    TRY("kv_alloc", mia_malloc((void **)&c->v_cache, sz));
+    TRY("kv_alloc", mia_memset(c->k_cache, 0, sz));
+    TRY("kv_alloc", mia_memset(c->v_cache, 0, sz));
+}
+
+void mia_dropin_kv_write(KVCache *cache, int layer, int pos, const _Float16 *k_vec,
+                         const _Float16 *v_vec) {
+    g_status = 0;
+    if (layer < 0 || layer >= cache->n_layers || pos < 0) {
+        fail(MIA_ERR_INVALID, "kv_write (layer/pos out of range)");
+        return;
+    }
+    size_t sz = (size_t)cache->kv_dim * sizeof(_Float16);
+    int t = pos % cache->max_seq;
+    size_t off = (size_t)layer * cache->max_seq * cache->kv_dim + (size_t)t * cache->kv_dim;
+    TRY("kv_write", mia_memcpy_h2d(cache->k_cache + off, k_vec, sz));
+    TRY("kv_write", mia_memcpy_h2d(cache->v_cache + off, v_vec, sz));
+}
+
+void mia_dropin_kv_free(KVCache *cache) {
+    g_status = 0;
+    TRY("kv_free", mia_free(cache->k_cache));
+    TRY("kv_free", mia_free(cache->v_cache));
+    cache->k_cache = NULL;
+    cache->v_cache = NULL;
+}
+
+void mia_dropin_apply_rope_batch(float *Q, float *K, int start_pos, const float *theta_inv,
+                                 int n_heads, int n_kv_heads, int head_dim, int S) {
+    g_status = 0;
+    if (S <= 0 || head_dim <= 0) {
+        fail(MIA_ERR_INVALID, "apply_rope (bad sizes)");
+        return;
+    }
+    size_t qb = Q ? (size_t)S * n_heads * head_dim * sizeof(float) : 0;
+    size_t kb = K ? (size_t)S * n_kv_heads * head_dim * sizeof(float) : 0;
+    size_t tb = (size_t)(head_dim / 2) * sizeof(float);
+    TRY("apply_rope", dbuf(align256(qb) + align256(kb) + align256(tb)));
+    float *dq = Q ? (float *)g_dbuf : NULL;
+    float *dk = K ? (float *)(g_dbuf + align256(qb)) : NULL;
+    float *dt = (float *)(g_dbuf + align256(qb) + align256(kb));
+    TRY("apply_rope", mia_memcpy_h2d(dt, theta_inv, tb));
+    if (Q) TRY("apply_rope", mia_memcpy_h2d(dq, Q, qb));
+    if (K) TRY("apply_rope", mia_memcpy_h2d(dk, K, kb));
+    TRY("apply_rope", mia_rope_f32(dq, dk, S, start_pos, dt, n_heads, n_kv_heads, head_dim, NULL));
+    TRY("apply_rope", mia_stream_sync(NULL));
+    if (Q) TRY("apply_rope", mia_memcpy_d2h(Q, dq, qb));
+    if (K) TRY("apply_rope", mia_memcpy_d2h(K, dk, kb));
+}
+
+void mia_dropin_apply_rope(float *q, float *k, int pos, const float *theta_inv, int n_heads,
+                           int n_kv_heads, int head_dim) {
+    mia_dropin_apply_rope_batch(q, k, pos, theta_inv, n_heads, n_kv_heads, head_dim, 1);
+}
+
+void mia_dropin_gqa_attention(float *q, float *att, float *out, _Float16 *kcache_base,
+                              _Float16 *vcache_base, int n_heads, int heads_per_kv, int hd,
+                              int max_seq, int pos) {
+    (void)att;
+    g_status = 0;
+    if (n_heads <= 0 || hd <= 0) {
+        fail(MIA_ERR_INVALID, "gqa_attention (bad sizes)");
+        return;
+    }
+    size_t nb = (size_t)n_heads * hd * sizeof(float);
+    TRY("gqa_attention", dbuf(2 * align256(nb)));
+    float *dq = (float *)g_dbuf;
+    float *dout = (float *)(g_dbuf + align256(nb));
+    TRY("gqa_attention", mia_memcpy_h2d(dq, q, nb));
+    TRY("gqa_attention", mia_gqa_attention(dq, dout, (const uint16_t *)kcache_base,
+                                           (const uint16_t *)vcache_base, n_heads, heads_per_kv, hd,
+                                           max_seq, pos, NULL));
+    TRY("gqa_attention", mia_stream_sync(NULL));
+    TRY("gqa_attention", mia_memcpy_d2h(out, dout, nb));
+}
+
+void mia_dropin_kv_write_batch(KVCache *kv, int layer, int start_pos, const float *K_buf,
+                               const float *V_buf, int kv_dim, int S) {
+    g_status = 0;
+    if (layer < 0 || layer >= kv->n_layers || kv_dim != kv->kv_dim || S <= 0) {
+        fail(MIA_ERR_INVALID, "kv_write_batch (bad layer/kv_dim/S)");
+        return;
+    }
+    size_t nb = (size_t)S * kv_dim * sizeof(float);
+    TRY("kv_write_batch", dbuf(2 * align256(nb)));
+    float *dk = (float *)g_dbuf;
+    float *dv = (float *)(g_dbuf + align256(nb));
+    TRY("kv_write_batch", mia_memcpy_h2d(dk, K_buf, nb));
+    TRY("kv_write_batch", mia_memcpy_h2d(dv, V_buf, nb));
+    size_t lay = (size_t)layer * kv->max_seq * kv->kv_dim;
+    TRY("kv_write_batch", mia_kv_write_f32((uint16_t *)(kv->k_cache + lay),
+                                           (uint16_t *)(kv->v_cache + lay), dk, dv, S, start_pos,
+                                           kv->max_seq, kv_dim, NULL));
+    TRY("kv_write_batch", mia_stream_sync(NULL));
+    /* mistral_ane_prefill.h:201-203 */
+    int end_pos = start_pos + S;
+    if (end_pos > kv->len && end_pos <= kv->max_seq)
+        kv->len = end_pos;
+    else if (end_pos > kv->max_seq)
+        kv->len = kv->max_seq;
+}
+
+void mia_dropin_attention_batch(const float *Q, float *attn_out, const KVCache *kv, int layer,
+                                int start_pos, const MistralConfig *c, int S, float *att_scratch) {
+    (void)att_scratch;
+    g_status = 0;
+    if (layer < 0 || layer >= kv->n_layers || S <= 0 || c->dim != c->n_heads * c->head_dim) {
+        fail(MIA_ERR_INVALID, "attention_batch (bad layer/S/dim)");
+        return;
+    }
+    size_t nb = (size_t)S * c->dim * sizeof(float);
+    TRY("attention_batch", dbuf(2 * align256(nb)));
+    float *dq = (float *)g_dbuf;
+    float *dout = (float *)(g_dbuf + align256(nb));
+    TRY("attention_batch", mia_memcpy_h2d(dq, Q, nb));
+    size_t lay = (size_t)layer * kv->max_seq * kv->kv_dim;
+    TRY("attention_batch",
+        mia_attention_batch(dq, dout, (const uint16_t *)(kv->k_cache + lay),
+                            (const uint16_t *)(kv->v_cache + lay), c->n_heads, c->n_kv_heads,
+                            c->head_dim, kv->max_seq, start_pos, S, NULL));
+    TRY("attention_batch", mia_stream_sync(NULL));
+    TRY("attention_batch", mia_memcpy_d2h(attn_out, dout, nb));
+}
+
+static void step_common(const char *what, KVCache *kv, int layer, const float *Q, const float *K,
+                        const float *V, int start_pos, int S, const float *theta_inv, int n_heads,
+                        int n_kv_heads, float *out) {
+    g_status = 0;
+    if (layer < 0 || layer >= kv->n_layers || S <= 0 || n_heads <= 0 || n_kv_heads <= 0 ||
+        n_kv_heads * kv->head_dim != kv->kv_dim) {
+        fail(MIA_ERR_INVALID, what);
+        return;
+    }
+    int hd = kv->head_dim;
+    size_t qb = (size_t)S * n_heads * hd * sizeof(float);
+    size_t kb = (size_t)S * kv->kv_dim * sizeof(float);
+    size_t tb = (size_t)(hd / 2) * sizeof(float);
+    size_t a = align256(qb), b = align256(kb), t = align256(tb);
+    TRY(what, dbuf(2 * a + 2 * b + t));
+    float *dq = (float *)g_dbuf;
+    float *dk = (float *)(g_dbuf + a);
+    float *dv = (float *)(g_dbuf + a + b);
+    float *dt = (float *)(g_dbuf + a + 2 * b);
+    float *dout = (float *)(g_dbuf + a + 2 * b + t);
+    TRY(what, mia_memcpy_h2d(dq, Q, qb));
+    TRY(what, mia_memcpy_h2d(dk, K, kb));
+    TRY(what, mia_memcpy_h2d(dv, V, kb));
+    TRY(what, mia_memcpy_h2d(dt, theta_inv, tb));
+    size_t lay = (size_t)layer * kv->max_seq * kv->kv_dim;
+    TRY(what, mia_attention_step(dq, dk, dv, dt, (uint16_t *)(kv->k_cache + lay),
+                                 (uint16_t *)(kv->v_cache + lay), dout, n_heads, n_kv_heads, hd,
+                                 kv->max_seq, start_pos, S, NULL));
+    TRY(what, mia_stream_sync(NULL));
+    TRY(what, mia_memcpy_d2h(out, dout, qb));
+    /* mistral_model.h:858, once per token as the sequential steps do */
+    for (int i = 0; i < S; i++) {
+        int pos = start_pos + i;
+        if (kv->len < kv->max_seq && pos + 1 > kv->len) kv->len = pos + 1;
+    }
+}
+
+void mia_dropin_decode_step(KVCache *kv, int layer, const float *q, const float *k, const float *v,
+                            int pos, const float *theta_inv, int n_heads, int n_kv_heads,
+                            float *out) {
+    step_common("decode_step", kv, layer, q, k, v, pos, 1, theta_inv, n_heads, n_kv_heads, out);
+}
+
+void mia_dropin_verify_step(KVCache *kv, int layer, const float *Q, const float *K, const float *V,
+                            int start_pos, int S, const float *theta_inv, int n_heads,
+                            int n_kv_heads, float *out) {
+    step_common("verify_step", kv, layer, Q, K, V, start_pos, S, theta_inv, n_heads, n_kv_heads,
+                out);
+}

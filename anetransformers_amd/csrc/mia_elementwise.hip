@@ -1,0 +1,182 @@
+// mia_elementwise.hip -- RoPE, fp32->fp16 ring writes, staging commit and the
+// synthetic-input fills used by the benchmark.
+#include "mia_device.h"
+#include "mia_kernels.h"
+
+namespace mia {
+
+namespace {
+
+// One thread per (token, pair index); rotates that pair in every q and k head.
+// mistral/mistral_model.h:79-122 and mistral/mistral_ane_prefill.h:177-186.
+__global__ void rope_kernel(float *q, float *k, int S, int start_pos, const float *theta_inv,
+                            int n_heads, int n_kv) {
+  const int t = blockIdx.x;
+  const int i = threadIdx.x;  // pair index < 64
+  if (t >= S || i >= HD / 2) return;
+  float ang = theta_inv[i] * (float)(start_pos + t);
+  float sn, cs;
+  sincosf(ang, &sn, &cs);
+  if (q) {
+    float *qt = q + (size_t)t * n_heads * HD;
+    for (int h = 0; h < n_heads; ++h) {
+      float2 v = *reinterpret_cast<float2 *>(qt + h * HD + 2 * i);
+      rope_pair(v.x, v.y, cs, sn);
+      *reinterpret_cast<float2 *>(qt + h * HD + 2 * i) = v;
+    }
+  }
+  if (k) {
+    float *kt = k + (size_t)t * n_kv * HD;
+    for (int h = 0; h < n_kv; ++h) {
+      float2 v = *reinterpret_cast<float2 *>(kt + h * HD + 2 * i);
+      rope_pair(v.x, v.y, cs, sn);
+      *reinterpret_cast<float2 *>(kt + h * HD + 2 * i) = v;
+    }
+  }
+}
+
+// Rotated K and plain V, rounded to fp16, into [S][kv_dim] destinations
+// (ring slots when kdst_ring, else a dense staging buffer).
+__global__ void rope_kv_f16_kernel(const float *K, const float *V, const float *theta_inv, int S,
+                                   int start_pos, int n_kv, _Float16 *kdst, _Float16 *vdst,
+                                   int max_seq, bool ring) {
+  const int t = blockIdx.x;
+  const int i = threadIdx.x;
+  if (t >= S || i >= HD / 2) return;
+  float ang = theta_inv[i] * (float)(start_pos + t);
+  float sn, cs;
+  sincosf(ang, &sn, &cs);
+  const int kv_dim = n_kv * HD;
+  const size_t drow = ring ? (size_t)((start_pos + t) % max_seq) : (size_t)t;
+  for (int h = 0; h < n_kv; ++h) {
+    const size_t so = (size_t)t * kv_dim + h * HD + 2 * i;
+    const size_t dof = drow * kv_dim + h * HD + 2 * i;
+    float2 kv = *reinterpret_cast<const float2 *>(K + so);
+    rope_pair(kv.x, kv.y, cs, sn);
+    float2 vv = *reinterpret_cast<const float2 *>(V + so);
+    kdst[dof] = (_Float16)kv.x;
+    kdst[dof + 1] = (_Float16)kv.y;
+    vdst[dof] = (_Float16)vv.x;
+    vdst[dof + 1] = (_Float16)vv.y;
+  }
+}
+
+// mistral/mistral_ane_prefill.h:189-204: cvt + kv_write at (start+t) % M.
+__global__ void kv_write_kernel(_Float16 *kc, _Float16 *vc, const float *K, const float *V, int S,
+                                int start_pos, int max_seq, int kv_dim) {
+  const int t = blockIdx.y;
+  const size_t slot = (size_t)((start_pos + t) % max_seq);
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < kv_dim; e += gridDim.x * blockDim.x) {
+    kc[slot * kv_dim + e] = (_Float16)K[(size_t)t * kv_dim + e];
+    vc[slot * kv_dim + e] = (_Float16)V[(size_t)t * kv_dim + e];
+  }
+}
+
+__global__ void commit_kernel(_Float16 *kc, _Float16 *vc, const _Float16 *kst,
+                              const _Float16 *vst, int S, int start_pos, int max_seq, int kv_dim) {
+  const int t = blockIdx.y;
+  const size_t slot = (size_t)((start_pos + t) % max_seq);
+  for (int e = (blockIdx.x * blockDim.x + threadIdx.x) * 8; e < kv_dim;
+       e += gridDim.x * blockDim.x * 8) {
+    *reinterpret_cast<u4 *>(kc + slot * kv_dim + e) =
+        *reinterpret_cast<const u4 *>(kst + (size_t)t * kv_dim + e);
+    *reinterpret_cast<u4 *>(vc + slot * kv_dim + e) =
+        *reinterpret_cast<const u4 *>(vst + (size_t)t * kv_dim + e);
+  }
+}
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+// N(0,1) via Box-Muller on a counter-based splitmix64 stream, rounded to fp16.
+__global__ void fill_normal_kernel(_Float16 *dst, size_t n, uint64_t seed) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    uint64_t r = splitmix64(seed ^ (i * 0xD1B54A32D192ED03ull));
+    float u1 = ((float)(r >> 40) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+    float u2 = (float)((r >> 16) & 0xFFFFFFu) * (1.0f / 16777216.0f);
+    float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+    dst[i] = (_Float16)z;
+  }
+}
+
+__global__ void scale_rows_kernel(_Float16 *base, long n_rows, int row_elems, int every, int offset,
+                                  float factor) {
+  const long n_sel = (n_rows - offset + every - 1) / every;
+  const long total = n_sel * row_elems;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (long)gridDim.x * blockDim.x) {
+    long rr = offset + (i / row_elems) * every;
+    long e = i % row_elems;
+    _Float16 *pp = base + rr * row_elems + e;
+    *pp = (_Float16)((float)*pp * factor);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_rope(float *q, float *k, int S, int start_pos, const float *theta_inv,
+                       int n_heads, int n_kv, hipStream_t s) {
+  if (S <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_kernel, dim3(S), dim3(64), 0, s, q, k, S, start_pos, theta_inv, n_heads,
+                     n_kv);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_to_f16(const float *K, const float *V, const float *theta_inv, int S,
+                              int start_pos, int n_kv, _Float16 *kdst, _Float16 *vdst,
+                              hipStream_t s) {
+  if (S <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_kv_f16_kernel, dim3(S), dim3(64), 0, s, K, V, theta_inv, S, start_pos,
+                     n_kv, kdst, vdst, 1, false);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_to_ring(const float *K, const float *V, const float *theta_inv, int S,
+                               int start_pos, int n_kv, _Float16 *kc, _Float16 *vc, int max_seq,
+                               hipStream_t s) {
+  if (S <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_kv_f16_kernel, dim3(S), dim3(64), 0, s, K, V, theta_inv, S, start_pos,
+                     n_kv, kc, vc, max_seq, true);
+  return hipGetLastError();
+}
+
+hipError_t launch_kv_write(_Float16 *kc, _Float16 *vc, const float *K, const float *V, int S,
+                           int start_pos, int max_seq, int kv_dim, hipStream_t s) {
+  if (S <= 0) return hipSuccess;
+  int bx = (kv_dim + 255) / 256;
+  hipLaunchKernelGGL(kv_write_kernel, dim3(bx, S), dim3(256), 0, s, kc, vc, K, V, S, start_pos,
+                     max_seq, kv_dim);
+  return hipGetLastError();
+}
+
+hipError_t launch_commit(_Float16 *kc, _Float16 *vc, const _Float16 *kst, const _Float16 *vst,
+                         int S, int start_pos, int max_seq, int kv_dim, hipStream_t s) {
+  if (S <= 0) return hipSuccess;
+  int bx = (kv_dim / 8 + 127) / 128;
+  hipLaunchKernelGGL(commit_kernel, dim3(bx, S), dim3(128), 0, s, kc, vc, kst, vst, S, start_pos,
+                     max_seq, kv_dim);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(_Float16 *dst, size_t n, uint64_t seed, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(fill_normal_kernel, dim3((unsigned)blocks), dim3(256), 0, s, dst, n, seed);
+  return hipGetLastError();
+}
+
+hipError_t launch_scale_rows(_Float16 *base, long n_rows, int row_elems, int every, int offset,
+                             float factor, hipStream_t s) {
+  if (n_rows <= offset || every <= 0) return hipSuccess;
+  hipLaunchKernelGGL(scale_rows_kernel, dim3(4096), dim3(256), 0, s, base, n_rows, row_elems,
+                     every, offset, factor);
+  return hipGetLastError();
+}
+
+}  // namespace mia

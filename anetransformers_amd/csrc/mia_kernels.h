@@ -1,0 +1,77 @@
+// mia_kernels.h -- host-side launch interface of the attention kernels.
+// Only the C-ABI shim (mia_capi.cpp) calls these; no torch types anywhere.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mia {
+
+// S=1 split-K flash-decode over the fp16 sequence-major ring of one layer.
+struct DecodeParams {
+  const float *q;          // [n_kv*G][128] fp32: raw (fused) or already rotated
+  const float *knew;       // [n_kv][128] fp32 raw new key (fused only)
+  const float *vnew;       // [n_kv][128] fp32 new value (fused only)
+  const float *theta_inv;  // [64] (fused only)
+  _Float16 *kc;            // layer base [max_seq][kv_dim]
+  _Float16 *vc;
+  float *out;              // [n_kv*G][128]
+  float *part_o;           // [n_kv][nchunk][G][128] unnormalised partial outputs
+  float *part_ml;          // [n_kv][nchunk][G][2] partial (max, sum), log2 domain
+  unsigned *counter;       // [n_kv] arrival counters, zero between launches
+  int max_seq;             // ring capacity M
+  int pos;                 // absolute position of the query token
+  int L;                   // window length min(pos+1, M)
+  int start;               // slot of the oldest window entry, (pos+1-L) mod M
+  int new_slot;            // pos mod M
+  int n_kv;
+  int nchunk;              // workgroups per kv head
+  int chunk_rows;          // rows per workgroup (multiple of 256)
+  float qscale;            // (1/sqrt(128)) * log2(e)
+};
+
+// Scratch needed by launch_decode for a given shape (bytes of part_o+part_ml).
+size_t decode_scratch_bytes(int n_kv, int G, int nchunk);
+int decode_pick_chunk_rows(int L, int n_kv, int target_wgs);
+hipError_t launch_decode(const DecodeParams &p, int G, bool fused, hipStream_t s);
+
+// S>=1 causal attention on fp16 MFMA for the queries start_pos..start_pos+S-1.
+struct FlashParams {
+  const float *Q;          // [S][n_heads*128] fp32, rotated (scale applied in-kernel)
+  const _Float16 *kc;      // layer base [max_seq][kv_dim]
+  const _Float16 *vc;
+  const _Float16 *kstage;  // [S][kv_dim] staged new keys (nullptr: all keys in ring)
+  const _Float16 *vstage;
+  float *out;              // [S][n_heads*128]
+  float *part_o;           // split-K partials (nsplit > 1)
+  float *part_ml;
+  unsigned *counter;       // [n_kv * n_rtiles]
+  int S, n_kv, max_seq, start_pos;
+  int n_rtiles;            // row tiles per kv head
+  int nsplit;              // key splits per row tile
+  int split_keys;          // keys per split (multiple of 64)
+  float qscale;
+};
+size_t flash_scratch_bytes(int n_kv, int n_rtiles, int nsplit, int rows_per_tile);
+hipError_t launch_flash(const FlashParams &p, int G, hipStream_t s, int *rows_per_tile_out);
+void flash_plan(int S, int n_kv, int G, int start_pos, int max_seq, int target_wgs,
+                int *n_rtiles, int *nsplit, int *split_keys, int *rows_per_tile);
+
+// Elementwise helpers.
+hipError_t launch_rope(float *q, float *k, int S, int start_pos, const float *theta_inv,
+                       int n_heads, int n_kv, hipStream_t s);
+hipError_t launch_rope_to_f16(const float *K, const float *V, const float *theta_inv, int S,
+                              int start_pos, int n_kv, _Float16 *kdst, _Float16 *vdst,
+                              hipStream_t s);
+hipError_t launch_rope_to_ring(const float *K, const float *V, const float *theta_inv, int S,
+                               int start_pos, int n_kv, _Float16 *kc, _Float16 *vc, int max_seq,
+                               hipStream_t s);
+hipError_t launch_kv_write(_Float16 *kc, _Float16 *vc, const float *K, const float *V, int S,
+                           int start_pos, int max_seq, int kv_dim, hipStream_t s);
+hipError_t launch_commit(_Float16 *kc, _Float16 *vc, const _Float16 *kst, const _Float16 *vst,
+                         int S, int start_pos, int max_seq, int kv_dim, hipStream_t s);
+hipError_t launch_fill_normal(_Float16 *dst, size_t n, uint64_t seed, hipStream_t s);
+hipError_t launch_scale_rows(_Float16 *base, long n_rows, int row_elems, int every, int offset,
+                             float factor, hipStream_t s);
+
+}  // namespace mia

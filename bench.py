@@ -1,0 +1,313 @@
+#!/usr/bin/env python3
+"""Benchmark of the Mistral-7B GQA attention hot path on one MI355X.
+
+Headline metric: decode attention HBM GB/s (% of peak) at 32K context, and
+prefill attention TFLOP/s (% of fp16 MFMA peak).
+
+  decode  (value): 32 layers, each a 32768-slot fp16 ring already full, new
+          token at position 32768 (wraps into slot 0), every 1024th key x4.
+          One step = 32 fused launches of mia_decode_step (RoPE q/k, fp16
+          ring write, split-K flash-decode with LSE merge).
+  prefill:         32 layers, 1536 cached positions + 512 new tokens
+          (positions 1536..2047, causal), fp16-valued Q/K/V.  One step = 32
+          calls of mia_attention_step; the flash kernel alone is timed on the
+          same stream for its TFLOP/s.
+
+Inputs are synthetic (seeded) and resident in HBM before timing starts.
+Prints one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+import anetransformers_amd as mia  # noqa: E402
+from anetransformers_amd import DeviceBuffer, Event, check  # noqa: E402
+
+N_LAYERS, N_HEADS, N_KV, HD = 32, 32, 8, 128
+KV_DIM = N_KV * HD
+THETA = 1e6
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+MFMA_F16_PEAK_TFS = 2500.0   # MI355X dense fp16 MFMA
+
+DECODE_M, DECODE_POS = 32768, 32768
+DECODE_L = min(DECODE_POS + 1, DECODE_M)
+DECODE_BYTES_PER_LAYER = 2 * N_KV * HD * 2 * DECODE_L          # K and V, fp16, once
+
+PF_M, PF_START, PF_S = 4096, 1536, 512
+PF_PAIRS_PER_HEAD = sum(PF_START + 1 + i for i in range(PF_S))   # unmasked (query, key)
+PF_FLOP_PER_LAYER = 4 * HD * N_HEADS * PF_PAIRS_PER_HEAD
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def theta_inv() -> np.ndarray:
+    i = np.arange(HD // 2, dtype=np.float32)
+    return (np.float32(1.0) / np.power(np.float32(THETA), (np.float32(2.0) * i) / np.float32(HD))
+            ).astype(np.float32)
+
+
+def f16_valued(g, shape) -> np.ndarray:
+    return g.standard_normal(shape, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+class Decode:
+    """32 layers x 32768-slot rings, fused decode step per layer."""
+
+    def __init__(self, lib, seed: int = 0):
+        self.lib = lib
+        ring = (N_LAYERS * DECODE_M, KV_DIM)
+        nbytes = ring[0] * ring[1] * 2
+        self.kc = DeviceBuffer(nbytes)
+        self.vc = DeviceBuffer(nbytes)
+        check(lib.mia_fill_normal_f16(self.kc.ptr, ring[0] * ring[1], seed * 2 + 1, None))
+        check(lib.mia_fill_normal_f16(self.vc.ptr, ring[0] * ring[1], seed * 2 + 2, None))
+        # every 1024th key x4: ring full, so slot == position and rows of all
+        # layers with global row % 1024 == 0 are exactly those positions
+        check(lib.mia_scale_rows_f16(self.kc.ptr, ring[0], KV_DIM, 1024, 0, 4.0, None))
+        g = np.random.default_rng(seed)
+        self.q = DeviceBuffer.from_array(g.standard_normal((N_LAYERS, N_HEADS * HD), np.float32))
+        self.k = DeviceBuffer.from_array(g.standard_normal((N_LAYERS, KV_DIM), np.float32))
+        self.v = DeviceBuffer.from_array(g.standard_normal((N_LAYERS, KV_DIM), np.float32))
+        self.th = DeviceBuffer.from_array(theta_inv())
+        self.out = DeviceBuffer(N_LAYERS * N_HEADS * HD * 4)
+        check(lib.mia_device_sync())
+
+    def step(self) -> None:
+        lay = DECODE_M * KV_DIM * 2
+        for l in range(N_LAYERS):
+            check(self.lib.mia_decode_step(
+                self.q.ptr + l * N_HEADS * HD * 4, self.k.ptr + l * KV_DIM * 4,
+                self.v.ptr + l * KV_DIM * 4, self.th.ptr, self.kc.ptr + l * lay,
+                self.vc.ptr + l * lay, self.out.ptr + l * N_HEADS * HD * 4, N_HEADS, N_KV, HD,
+                DECODE_M, DECODE_POS, None), "decode_step")
+
+
+class Prefill:
+    """32 layers, 1536 cached + 512 new tokens per layer."""
+
+    def __init__(self, lib, seed: int = 7):
+        self.lib = lib
+        g = np.random.default_rng(seed)
+        lay_elems = PF_M * KV_DIM
+        self.kc = DeviceBuffer(N_LAYERS * lay_elems * 2)
+        self.vc = DeviceBuffer(N_LAYERS * lay_elems * 2)
+        self.kc.zero()
+        self.vc.zero()
+        for l in range(N_LAYERS):   # cached positions 0..1535 (calloc'd rest)
+            check(lib.mia_fill_normal_f16(self.kc.ptr + l * lay_elems * 2, PF_START * KV_DIM,
+                                          1000 + 2 * l, None))
+            check(lib.mia_fill_normal_f16(self.vc.ptr + l * lay_elems * 2, PF_START * KV_DIM,
+                                          1001 + 2 * l, None))
+        self.Q = DeviceBuffer.from_array(f16_valued(g, (N_LAYERS, PF_S, N_HEADS * HD)))
+        self.K = DeviceBuffer.from_array(f16_valued(g, (N_LAYERS, PF_S, KV_DIM)))
+        self.V = DeviceBuffer.from_array(f16_valued(g, (N_LAYERS, PF_S, KV_DIM)))
+        self.th = DeviceBuffer.from_array(theta_inv())
+        self.out = DeviceBuffer(N_LAYERS * PF_S * N_HEADS * HD * 4)
+        check(lib.mia_device_sync())
+
+    def _ptrs(self, l):
+        lay = PF_M * KV_DIM * 2
+        return (self.Q.ptr + l * PF_S * N_HEADS * HD * 4, self.K.ptr + l * PF_S * KV_DIM * 4,
+                self.V.ptr + l * PF_S * KV_DIM * 4, self.kc.ptr + l * lay, self.vc.ptr + l * lay,
+                self.out.ptr + l * PF_S * N_HEADS * HD * 4)
+
+    def step(self) -> None:
+        for l in range(N_LAYERS):
+            q, k, v, kc, vc, out = self._ptrs(l)
+            check(self.lib.mia_attention_step(q, k, v, self.th.ptr, kc, vc, out, N_HEADS, N_KV, HD,
+                                              PF_M, PF_START, PF_S, None), "attention_step")
+
+    def attention_only(self) -> None:
+        """The flash kernel alone over the written rings (Q used as rotated)."""
+        for l in range(N_LAYERS):
+            q, _, _, kc, vc, out = self._ptrs(l)
+            check(self.lib.mia_attention_batch(q, out, kc, vc, N_HEADS, N_KV, HD, PF_M, PF_START,
+                                               PF_S, None), "attention_batch")
+
+
+def timed(lib, fn, steps: int, warmup: int) -> float:
+    """Mean ms per call of fn over `steps`, HIP events on the library stream."""
+    for _ in range(warmup):
+        fn()
+    check(lib.mia_device_sync())
+    e0, e1 = Event(), Event()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    check(lib.mia_device_sync())
+    return e0.elapsed_ms(e1) / steps
+
+
+def cpu_baseline_decode(n_layers: int = 8, reps: int = 3):
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import _oracle as O  # the oracle is the timed CPU baseline here
+
+    g = np.random.default_rng(11)
+    kc = g.standard_normal((n_layers, DECODE_M, KV_DIM), np.float32)
+    kc[:, ::1024] *= 4.0
+    kc = kc.astype(np.float16).view(np.uint16)
+    vc = g.standard_normal((n_layers, DECODE_M, KV_DIM), np.float32).astype(np.float16).view(np.uint16)
+    Q = g.standard_normal((n_layers, N_HEADS * HD), np.float32)
+    threads = O.num_threads(fast=True)
+    O.decode_layers(Q[:1], kc[:1], vc[:1], 1, N_HEADS, N_HEADS // N_KV, HD, DECODE_M, DECODE_POS,
+                    threads=threads)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        O.decode_layers(Q, kc, vc, n_layers, N_HEADS, N_HEADS // N_KV, HD, DECODE_M, DECODE_POS,
+                        threads=threads)
+        ts.append(time.perf_counter() - t0)
+    dt = float(np.median(ts))
+    t0 = time.perf_counter()
+    O.decode_layers(Q[:1], kc[:1], vc[:1], 1, N_HEADS, N_HEADS // N_KV, HD, DECODE_M, DECODE_POS,
+                    threads=1)
+    dt1 = time.perf_counter() - t0
+    return {
+        "value": round(n_layers * DECODE_BYTES_PER_LAYER / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n_layers} of 32 layers of the same decode workload (32768-slot full ring, "
+                  f"new token at 32768), median of {reps}; oracle AVX2+F16C timing build, "
+                  f"OpenMP over (layer, head)",
+        "single_thread_value": round(DECODE_BYTES_PER_LAYER / dt1 / 1e9, 3),
+    }
+
+
+def cpu_baseline_prefill(n_layers: int = 2):
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import _oracle as O
+
+    g = np.random.default_rng(12)
+    kc = np.zeros((n_layers, PF_M, KV_DIM), np.uint16)
+    vc = np.zeros((n_layers, PF_M, KV_DIM), np.uint16)
+    kc[:, :PF_START + PF_S] = g.standard_normal((n_layers, PF_START + PF_S, KV_DIM),
+                                                np.float32).astype(np.float16).view(np.uint16)
+    vc[:, :PF_START + PF_S] = g.standard_normal((n_layers, PF_START + PF_S, KV_DIM),
+                                                np.float32).astype(np.float16).view(np.uint16)
+    Q = f16_valued(g, (n_layers, PF_S, N_HEADS * HD))
+    threads = O.num_threads(fast=True)
+    t0 = time.perf_counter()
+    O.attention_batch_layers(Q, kc, vc, n_layers, N_HEADS, N_KV, HD, PF_M, PF_START, PF_S,
+                             threads=threads)
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(n_layers * PF_FLOP_PER_LAYER / dt / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n_layers} of 32 layers of the same prefill chunk (attention_batch over "
+                  f"1536 cached + 512 new); oracle AVX2+F16C timing build, OpenMP over "
+                  f"(layer, token, head)",
+    }
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/), or None."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-prefill", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the attention path has no "
+                          "multi-GPU mode (see DESIGN.md for how it would shard)",
+                          "n_gpus": args.gpus}))
+        return 2
+
+    lib = mia.init(0)
+    log("decode: allocating 32 x 32768-slot rings (4 GiB)")
+    dec = Decode(lib)
+    dec_ms = timed(lib, dec.step, args.steps, args.warmup)
+    launch_ms = dec_ms / N_LAYERS
+    achieved = DECODE_BYTES_PER_LAYER / (launch_ms * 1e-3) / 1e9
+    value = N_LAYERS * DECODE_BYTES_PER_LAYER / (dec_ms * 1e-3) / 1e9
+    log(f"decode: {dec_ms:.3f} ms/step, {value:.1f} GB/s")
+    del dec
+
+    prefill = None
+    if not args.skip_prefill:
+        log("prefill: 32 layers x (1536 cached + 512 new)")
+        pf = Prefill(lib)
+        pf_ms = timed(lib, pf.step, max(args.steps // 2, 3), 2)
+        fl_ms = timed(lib, pf.attention_only, max(args.steps // 2, 3), 2) / N_LAYERS
+        fl_tfs = PF_FLOP_PER_LAYER / (fl_ms * 1e-3) / 1e12
+        log(f"prefill: {pf_ms:.3f} ms/step, flash kernel {fl_ms * 1e3:.1f} us, {fl_tfs:.1f} TFLOP/s")
+        prefill = {
+            "value": round(N_LAYERS * PF_FLOP_PER_LAYER / (pf_ms * 1e-3) / 1e12, 3),
+            "unit": "TFLOP/s",
+            "ms_per_step": round(pf_ms, 4),
+            "workload": "causal prefill chunk: 32 layers, 512 new tokens after 1536 cached "
+                        "positions, 32 q / 8 kv heads, hd 128, fp16 MFMA, fp32 accumulate",
+            "flop_per_layer": PF_FLOP_PER_LAYER,
+            "roofline": {"bound": "mfma", "achieved": round(fl_tfs, 3),
+                         "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
+                         "frac": round(fl_tfs / MFMA_F16_PEAK_TFS, 4),
+                         "traffic": load_traffic("flash_prefill")},
+        }
+        del pf
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline: decode sample")
+        cpu = cpu_baseline_decode()
+        if prefill is not None:
+            log("cpu baseline: prefill sample")
+            prefill["cpu_baseline"] = cpu_baseline_prefill()
+
+    line = {
+        "metric": "decode attn HBM GB/s (% peak) @32K ctx; prefill attn TFLOPS (% MFMA peak)",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 storage, f32 math",
+        "data": "synthetic (seeded N(0,1) fp16 rings generated on the GPU)",
+        "config": {
+            "workload": "decode attention step x 32 layers: 32768-slot fp16 ring full, new "
+                        "token at position 32768, every 1024th key x4, 32 q / 8 kv heads, hd 128, "
+                        "RoPE theta 1e6, fused RoPE + ring write + split-K flash-decode",
+            "layers": N_LAYERS, "ctx": DECODE_L, "max_seq": DECODE_M,
+            "bytes_per_layer": DECODE_BYTES_PER_LAYER,
+        },
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic("decode_32k")},
+        "cpu_baseline": cpu,
+        "prefill": prefill,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

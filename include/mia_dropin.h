@@ -1,0 +1,155 @@
+/*
+ * mia_dropin.h -- drop-in replacement, with the reference's C signatures, for
+ * the attention step of the Mistral-7B layer forward.  Needs a compiler with
+ * _Float16 (clang, as the reference uses).
+ *
+ * The reference's path is header-only `static` C (mistral/kv_cache.h,
+ * mistral/mistral_model.h, mistral/mistral_ane_prefill.h).  This header keeps
+ * the same types (KVCache with the same field order, MistralConfig) and, unless
+ * MIA_DROPIN_NO_REFERENCE_NAMES is defined, the same function names as static
+ * inline forwards to libmiattn.so.  Differences in behaviour:
+ *   - k_cache / v_cache are device memory (the Metal backend re-homes them the
+ *     same way, mistral/metal_matvec.h:297-310); kv_k/kv_v/kv_k_at/kv_v_at are
+ *     the same pointer arithmetic and return device pointers.
+ *   - q, k, out, Q, attn_out, K_buf, V_buf, k_vec, v_vec, theta_inv are host
+ *     buffers, as at the reference's call sites; every call is synchronous.
+ *   - gqa_attention_neon leaves q unscaled and does not write att (the
+ *     reference pre-scales q in place and leaves probabilities in att; no
+ *     caller reads either afterwards).
+ *   - Errors (no device, unsupported shape, HIP failure) print the reason and
+ *     abort(): the reference has no error channel.  mia_dropin_set_abort(0)
+ *     makes them return instead, with the message in mia_last_error().
+ */
+#ifndef MIA_DROPIN_H
+#define MIA_DROPIN_H
+
+#include <stddef.h>
+
+#include "miattn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* mistral/kv_cache.h:10-20, same fields in the same order. */
+typedef struct {
+    int n_layers;
+    int n_kv_heads;
+    int head_dim;
+    int max_seq;
+    int kv_dim;
+    _Float16 *k_cache; /* device: [n_layers][max_seq][n_kv_heads][head_dim] */
+    _Float16 *v_cache;
+    int pos;
+    int len;
+} KVCache;
+
+/* mistral/gguf_loader.h:51-63, same fields in the same order. */
+typedef struct {
+    int dim;
+    int hidden_dim;
+    int n_layers;
+    int n_heads;
+    int n_kv_heads;
+    int head_dim;
+    int vocab_size;
+    int max_seq_len;
+    float rope_theta;
+    float rms_eps;
+    int sliding_window;
+} MistralConfig;
+
+void mia_dropin_set_abort(int abort_on_error);
+int mia_dropin_status(void); /* status of the last drop-in call on this thread */
+
+/* kv_cache.h:22-35 (calloc -> zeroed device memory) */
+void mia_dropin_kv_alloc(KVCache *c, int n_layers, int n_kv_heads, int head_dim, int max_seq);
+/* kv_cache.h:53-57: host fp16 k_vec/v_vec [kv_dim] -> slot pos % max_seq */
+void mia_dropin_kv_write(KVCache *cache, int layer, int pos, const _Float16 *k_vec,
+                         const _Float16 *v_vec);
+/* kv_cache.h:70-75 */
+void mia_dropin_kv_free(KVCache *cache);
+/* mistral_model.h:79-122 */
+void mia_dropin_apply_rope(float *q, float *k, int pos, const float *theta_inv, int n_heads,
+                           int n_kv_heads, int head_dim);
+/* mistral_model.h:362-487 */
+void mia_dropin_gqa_attention(float *q, float *att, float *out, _Float16 *kcache_base,
+                              _Float16 *vcache_base, int n_heads, int heads_per_kv, int hd,
+                              int max_seq, int pos);
+/* mistral_ane_prefill.h:177-186 */
+void mia_dropin_apply_rope_batch(float *Q, float *K, int start_pos, const float *theta_inv,
+                                 int n_heads, int n_kv_heads, int head_dim, int S);
+/* mistral_ane_prefill.h:189-204 (including the len update) */
+void mia_dropin_kv_write_batch(KVCache *kv, int layer, int start_pos, const float *K_buf,
+                               const float *V_buf, int kv_dim, int S);
+/* mistral_ane_prefill.h:207-275 */
+void mia_dropin_attention_batch(const float *Q, float *attn_out, const KVCache *kv, int layer,
+                                int start_pos, const MistralConfig *c, int S, float *att_scratch);
+/* Steps 4-6 of mistral_model.h:849-863 in one call (RoPE, fp16 cvt, kv_write,
+ * len update, attention); q/k/v are the raw projections, not modified. */
+void mia_dropin_decode_step(KVCache *kv, int layer, const float *q, const float *k, const float *v,
+                            int pos, const float *theta_inv, int n_heads, int n_kv_heads,
+                            float *out);
+/* The per-layer part of mistral/speculative.h:92-101 for S tokens at once,
+ * with the same result as S decode steps (drafts staged, then committed). */
+void mia_dropin_verify_step(KVCache *kv, int layer, const float *Q, const float *K, const float *V,
+                            int start_pos, int S, const float *theta_inv, int n_heads,
+                            int n_kv_heads, float *out);
+
+#ifndef MIA_DROPIN_NO_REFERENCE_NAMES
+/* Reference names (mistral/kv_cache.h, mistral_model.h, mistral_ane_prefill.h). */
+static inline KVCache kv_alloc(int n_layers, int n_kv_heads, int head_dim, int max_seq) {
+    KVCache c;
+    mia_dropin_kv_alloc(&c, n_layers, n_kv_heads, head_dim, max_seq);
+    return c;
+}
+static inline _Float16 *kv_k_at(const KVCache *cache, int layer, int seq_pos) {
+    int t = seq_pos % cache->max_seq;
+    return cache->k_cache + (size_t)layer * cache->max_seq * cache->kv_dim +
+           (size_t)t * cache->kv_dim;
+}
+static inline _Float16 *kv_v_at(const KVCache *cache, int layer, int seq_pos) {
+    int t = seq_pos % cache->max_seq;
+    return cache->v_cache + (size_t)layer * cache->max_seq * cache->kv_dim +
+           (size_t)t * cache->kv_dim;
+}
+static inline void kv_write(KVCache *cache, int layer, int pos, const _Float16 *k_vec,
+                            const _Float16 *v_vec) {
+    mia_dropin_kv_write(cache, layer, pos, k_vec, v_vec);
+}
+static inline _Float16 *kv_k(const KVCache *cache, int layer) {
+    return cache->k_cache + (size_t)layer * cache->max_seq * cache->kv_dim;
+}
+static inline _Float16 *kv_v(const KVCache *cache, int layer) {
+    return cache->v_cache + (size_t)layer * cache->max_seq * cache->kv_dim;
+}
+static inline void kv_free(KVCache *cache) { mia_dropin_kv_free(cache); }
+static inline void apply_rope(float *q, float *k, int pos, const float *theta_inv, int n_heads,
+                              int n_kv_heads, int head_dim) {
+    mia_dropin_apply_rope(q, k, pos, theta_inv, n_heads, n_kv_heads, head_dim);
+}
+static inline void gqa_attention_neon(float *q, float *att, float *out, _Float16 *kcache_base,
+                                      _Float16 *vcache_base, int n_heads, int heads_per_kv,
+                                      int hd, int max_seq, int pos) {
+    mia_dropin_gqa_attention(q, att, out, kcache_base, vcache_base, n_heads, heads_per_kv, hd,
+                             max_seq, pos);
+}
+static inline void apply_rope_batch(float *Q, float *K, int start_pos, const float *theta_inv,
+                                    int n_heads, int n_kv_heads, int head_dim, int S) {
+    mia_dropin_apply_rope_batch(Q, K, start_pos, theta_inv, n_heads, n_kv_heads, head_dim, S);
+}
+static inline void kv_write_batch(KVCache *kv, int layer, int start_pos, const float *K_buf,
+                                  const float *V_buf, int kv_dim, int S) {
+    mia_dropin_kv_write_batch(kv, layer, start_pos, K_buf, V_buf, kv_dim, S);
+}
+static inline void attention_batch(const float *Q, float *attn_out, const KVCache *kv, int layer,
+                                   int start_pos, const MistralConfig *c, int S,
+                                   float *att_scratch) {
+    mia_dropin_attention_batch(Q, attn_out, kv, layer, start_pos, c, S, att_scratch);
+}
+#endif /* MIA_DROPIN_NO_REFERENCE_NAMES */
+
+#ifdef __cplusplus
+}
+#endif
+#endif

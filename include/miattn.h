@@ -1,0 +1,122 @@
+/*
+ * miattn.h -- C ABI of libmiattn.so: the MI355X (gfx950) Mistral-7B GQA
+ * attention hot path.  Plain pointers and sizes only.
+ *
+ * Conventions
+ *   - Every function returns 0 (MIA_OK) or a nonzero mia_status; the message
+ *     of the last failure on the calling thread is in mia_last_error().
+ *   - "dev" pointers are device memory (mia_malloc or any hipMalloc'd
+ *     memory); fp16 tensors are IEEE binary16 bit patterns (uint16_t).
+ *   - stream is a hipStream_t, or NULL for the library's stream on the
+ *     current device.  Kernels are enqueued asynchronously; outputs are valid
+ *     after mia_stream_sync(stream).
+ *   - Shapes: head_dim must be 128 and n_heads / n_kv_heads must be 4 (the
+ *     Mistral-7B GQA ratio); other shapes return MIA_ERR_UNSUPPORTED.
+ *   - KV ring layout (mistral/kv_cache.h:2-4): per layer
+ *     [max_seq][n_kv_heads][head_dim] fp16; position p lives in slot
+ *     p % max_seq (mistral/kv_cache.h:39).  k_layer / v_layer point at a
+ *     layer base (kv_k / kv_v, mistral/kv_cache.h:61-68).
+ *   - Calls that use split-K scratch share one per-device scratch area: calls
+ *     that overlap on one device (several host threads, or several streams)
+ *     race.  The first call at a new size may allocate (not inside a HIP
+ *     graph capture: warm up first).
+ */
+#ifndef MIATTN_H
+#define MIATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    MIA_OK = 0,
+    MIA_ERR_INVALID = 1,     /* bad argument */
+    MIA_ERR_UNSUPPORTED = 2, /* shape the gfx950 kernels are not built for */
+    MIA_ERR_HIP = 3,         /* HIP runtime error (message in mia_last_error) */
+    MIA_ERR_NO_DEVICE = 4    /* no HIP device / library not initialised */
+} mia_status;
+
+/* ---- runtime plumbing -------------------------------------------------- */
+int mia_init(int device);            /* select device, create stream; idempotent */
+int mia_device_count(int *count);
+const char *mia_last_error(void);
+int mia_version(void);               /* 100 * major + minor */
+int mia_malloc(void **dptr, size_t bytes);
+int mia_free(void *dptr);
+int mia_memcpy_h2d(void *dst_dev, const void *src_host, size_t bytes);
+int mia_memcpy_d2h(void *dst_host, const void *src_dev, size_t bytes);
+int mia_memcpy_d2d(void *dst_dev, const void *src_dev, size_t bytes);
+int mia_memset(void *dst_dev, int value, size_t bytes);
+int mia_stream_create(void **stream);
+int mia_stream_destroy(void *stream);
+int mia_stream_sync(void *stream);
+int mia_device_sync(void);
+int mia_event_create(void **event);
+int mia_event_destroy(void *event);
+int mia_event_record(void *event, void *stream);
+int mia_event_elapsed_ms(float *ms, void *start, void *stop);
+
+/* ---- synthetic inputs (benchmark) --------------------------------------- */
+/* dst[i] = fp16(N(0,1)) from a counter-based splitmix64 + Box-Muller stream. */
+int mia_fill_normal_f16(uint16_t *dst_dev, size_t n, uint64_t seed, void *stream);
+/* Multiply rows offset, offset+every, ... (row_elems fp16 each) by factor. */
+int mia_scale_rows_f16(uint16_t *base_dev, long n_rows, int row_elems, int every, int offset,
+                       float factor, void *stream);
+
+/* ---- hot path ------------------------------------------------------------ */
+
+/* In-place adjacent-pair RoPE of S tokens at positions start_pos + t.
+ * Replaces apply_rope (mistral/mistral_model.h:79-122) for S = 1 and
+ * apply_rope_batch (mistral/mistral_ane_prefill.h:177-186).
+ * q [S][n_heads*128] fp32 dev (may be NULL), k [S][n_kv_heads*128] (may be
+ * NULL), theta_inv [64] dev (precompute_rope_theta, mistral_model.h:69-74). */
+int mia_rope_f32(float *q, float *k, int S, int start_pos, const float *theta_inv, int n_heads,
+                 int n_kv_heads, int head_dim, void *stream);
+
+/* fp32 -> fp16 (RNE) and ring write of S tokens at slots (start_pos+t) %
+ * max_seq.  Replaces kv_write_batch (mistral/mistral_ane_prefill.h:189-204;
+ * the caller keeps the len bookkeeping).  K, V [S][kv_dim] fp32 dev. */
+int mia_kv_write_f32(uint16_t *k_layer, uint16_t *v_layer, const float *K, const float *V, int S,
+                     int start_pos, int max_seq, int kv_dim, void *stream);
+
+/* S=1 GQA attention over the ring as it stands.  Replaces gqa_attention_neon
+ * (mistral/mistral_model.h:362-487): window = last min(pos+1, max_seq)
+ * positions, oldest first; scale 1/sqrt(128).  q [n_heads*128] fp32 dev,
+ * already rotated (not modified); out [n_heads*128] fp32 dev.  The
+ * reference's att scratch is not used. */
+int mia_gqa_attention(const float *q, float *out, const uint16_t *k_layer,
+                      const uint16_t *v_layer, int n_heads, int heads_per_kv, int hd,
+                      int max_seq, int pos, void *stream);
+
+/* Steps 4-6 of the decode layer (mistral/mistral_model.h:849-863) fused in
+ * one launch: RoPE(q, k) at pos, fp16 round of k and v, ring write at
+ * pos % max_seq, S=1 attention (the new token attended from its fp16 copy).
+ * q [n_heads*128], k, v [n_kv_heads*128] raw fp32 dev (not modified);
+ * theta_inv [64] dev; out [n_heads*128] fp32 dev. */
+int mia_decode_step(const float *q, const float *k, const float *v, const float *theta_inv,
+                    uint16_t *k_layer, uint16_t *v_layer, float *out, int n_heads,
+                    int n_kv_heads, int hd, int max_seq, int pos, void *stream);
+
+/* S>=1 causal GQA attention over the ring as it stands, query t at position
+ * start_pos + t.  Replaces attention_batch (mistral/mistral_ane_prefill.h:
+ * 207-275).  Q [S][n_heads*128] fp32 dev, rotated; out [S][n_heads*128]. */
+int mia_attention_batch(const float *Q, float *out, const uint16_t *k_layer,
+                        const uint16_t *v_layer, int n_heads, int n_kv_heads, int hd,
+                        int max_seq, int start_pos, int S, void *stream);
+
+/* S tokens through steps 4-6 with sequential semantics: the result equals S
+ * calls of mia_decode_step at start_pos, start_pos+1, ... (the verify loop of
+ * mistral/speculative.h:92-101), also when the ring has wrapped: drafts are
+ * staged during attention and committed to their slots afterwards.
+ * Q [S][n_heads*128], K, V [S][n_kv_heads*128] raw fp32 dev (not modified). */
+int mia_attention_step(const float *Q, const float *K, const float *V, const float *theta_inv,
+                       uint16_t *k_layer, uint16_t *v_layer, float *out, int n_heads,
+                       int n_kv_heads, int hd, int max_seq, int start_pos, int S, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,223 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle*.so) -- test infrastructure.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this,
+and only as the checker or the timed CPU baseline.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_float, c_int, c_size_t, c_void_p
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(REPO, "oracle")
+
+_P = c_void_p
+
+
+class OraKV(ctypes.Structure):
+    _fields_ = [
+        ("n_layers", c_int),
+        ("n_kv_heads", c_int),
+        ("head_dim", c_int),
+        ("max_seq", c_int),
+        ("kv_dim", c_int),
+        ("k_cache", c_void_p),
+        ("v_cache", c_void_p),
+        ("pos", c_int),
+        ("len", c_int),
+    ]
+
+
+_SIGS = {
+    "ora_f32_to_f16": (ctypes.c_uint16, [c_float]),
+    "ora_f16_to_f32": (c_float, [ctypes.c_uint16]),
+    "ora_cvt_f32_to_f16": (None, [_P, _P, c_int]),
+    "ora_cvt_f16_to_f32": (None, [_P, _P, c_size_t]),
+    "ora_precompute_rope_theta": (None, [c_float, c_int, _P]),
+    "ora_apply_rope": (None, [_P, _P, c_int, _P, c_int, c_int, c_int]),
+    "ora_apply_rope_batch": (None, [_P, _P, c_int, _P, c_int, c_int, c_int, c_int]),
+    "ora_softmax_vec": (None, [_P, c_int]),
+    "ora_gqa_attention": (None, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int]),
+    "ora_kv_write_batch": (None, [POINTER(OraKV), c_int, c_int, _P, _P, c_int, c_int]),
+    "ora_attention_batch": (
+        None,
+        [_P, _P, POINTER(OraKV), c_int, c_int, c_int, c_int, c_int, c_int, _P],
+    ),
+    "ora_decode_step": (
+        None,
+        [POINTER(OraKV), c_int, _P, _P, _P, c_int, _P, c_int, c_int, _P, _P],
+    ),
+    "ora_verify_steps": (
+        None,
+        [POINTER(OraKV), c_int, _P, _P, _P, c_int, c_int, _P, c_int, c_int, _P, _P],
+    ),
+    "ora_ref_gqa_attention": (None, [_P, _P, _P, _P, c_int, c_int, c_int, c_int]),
+    "ora_decode_layers": (
+        None,
+        [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
+    ),
+    "ora_attention_batch_layers": (
+        None,
+        [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
+    ),
+    "ora_num_threads": (c_int, []),
+}
+
+_libs: dict = {}
+
+
+def load(fast: bool = False) -> ctypes.CDLL:
+    name = "liboracle_fast.so" if fast else "liboracle.so"
+    if name in _libs:
+        return _libs[name]
+    path = os.path.join(ORACLE_DIR, name)
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+    lib = ctypes.CDLL(path)
+    for fn, (res, args) in _SIGS.items():
+        f = getattr(lib, fn)
+        f.restype = res
+        f.argtypes = args
+    _libs[name] = lib
+    return lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"], "array must be contiguous"
+    return a.ctypes.data
+
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    load().ora_cvt_f32_to_f16(_p(x), _p(out), x.size)
+    return out
+
+
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    load().ora_cvt_f16_to_f32(_p(h), _p(out), h.size)
+    return out
+
+
+def theta_inv(theta: float = 1e6, hd: int = 128) -> np.ndarray:
+    out = np.empty(hd // 2, dtype=np.float32)
+    load().ora_precompute_rope_theta(theta, hd, _p(out))
+    return out
+
+
+def apply_rope(q, k, pos, th, n_heads, n_kv, hd):
+    """In place on float32 arrays (either may be None)."""
+    load().ora_apply_rope(_p(q) if q is not None else None, _p(k) if k is not None else None,
+                          pos, _p(th), n_heads, n_kv, hd)
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    y = np.array(x, dtype=np.float32, copy=True)
+    load().ora_softmax_vec(_p(y), y.size)
+    return y
+
+
+def gqa_attention(q, kc, vc, n_heads, heads_per_kv, hd, max_seq, pos):
+    """mistral_model.h:362-487 on a copy of q; kc/vc uint16 [max_seq, kv_dim]."""
+    qq = np.array(q, dtype=np.float32, copy=True)
+    att = np.zeros(n_heads * max_seq, dtype=np.float32)
+    out = np.empty(n_heads * hd, dtype=np.float32)
+    load().ora_gqa_attention(_p(qq), _p(att), _p(out), _p(kc), _p(vc), n_heads, heads_per_kv,
+                             hd, max_seq, pos)
+    return out
+
+
+def make_kv(kc: np.ndarray, vc: np.ndarray, n_kv: int, hd: int, max_seq: int) -> OraKV:
+    """OraKV (one layer) over caller-owned uint16 arrays [max_seq, kv_dim]."""
+    assert kc.dtype == np.uint16 and kc.shape == (max_seq, n_kv * hd)
+    return OraKV(1, n_kv, hd, max_seq, n_kv * hd, _p(kc), _p(vc), 0, 0)
+
+
+def attention_batch(Q, kc, vc, n_heads, n_kv, hd, max_seq, start_pos, S):
+    Q = np.ascontiguousarray(Q, dtype=np.float32)
+    kv = make_kv(kc, vc, n_kv, hd, max_seq)
+    out = np.empty((S, n_heads * hd), dtype=np.float32)
+    att = np.zeros(n_heads * max_seq, dtype=np.float32)
+    load().ora_attention_batch(_p(Q), _p(out), ctypes.byref(kv), 0, start_pos, n_heads, n_kv, hd,
+                               S, _p(att))
+    return out
+
+
+def attention_batch_parallel(Q, kc, vc, n_heads, n_kv, hd, max_seq, start_pos, S, threads=0):
+    """Same arithmetic as attention_batch, units spread over OpenMP threads."""
+    Q = np.ascontiguousarray(Q, dtype=np.float32)
+    out = np.empty((S, n_heads * hd), dtype=np.float32)
+    load().ora_attention_batch_layers(_p(Q), _p(out), _p(kc), _p(vc), 1, n_heads, n_kv, hd,
+                                      max_seq, start_pos, S, threads)
+    return out
+
+
+def kv_write_batch(kc, vc, K, V, n_kv, hd, max_seq, start_pos, S):
+    kv = make_kv(kc, vc, n_kv, hd, max_seq)
+    K = np.ascontiguousarray(K, dtype=np.float32)
+    V = np.ascontiguousarray(V, dtype=np.float32)
+    load().ora_kv_write_batch(ctypes.byref(kv), 0, start_pos, _p(K), _p(V), n_kv * hd, S)
+    return kv.len
+
+
+def decode_step(kc, vc, q, k, v, pos, th, n_heads, n_kv, hd, max_seq):
+    """Steps 4-6 of mistral_model.h:849-863 on copies of q/k; kc/vc updated."""
+    kv = make_kv(kc, vc, n_kv, hd, max_seq)
+    qq = np.array(q, dtype=np.float32, copy=True)
+    kk = np.array(k, dtype=np.float32, copy=True)
+    vv = np.ascontiguousarray(v, dtype=np.float32)
+    att = np.zeros(n_heads * max_seq, dtype=np.float32)
+    out = np.empty(n_heads * hd, dtype=np.float32)
+    load().ora_decode_step(ctypes.byref(kv), 0, _p(qq), _p(kk), _p(vv), pos, _p(th), n_heads, n_kv,
+                           _p(att), _p(out))
+    return out
+
+
+def verify_steps(kc, vc, Q, K, V, start_pos, S, th, n_heads, n_kv, hd, max_seq):
+    kv = make_kv(kc, vc, n_kv, hd, max_seq)
+    QQ = np.array(Q, dtype=np.float32, copy=True)
+    KK = np.array(K, dtype=np.float32, copy=True)
+    VV = np.ascontiguousarray(V, dtype=np.float32)
+    att = np.zeros(n_heads * max_seq, dtype=np.float32)
+    out = np.empty((S, n_heads * hd), dtype=np.float32)
+    load().ora_verify_steps(ctypes.byref(kv), 0, _p(QQ), _p(KK), _p(VV), start_pos, S, _p(th),
+                            n_heads, n_kv, _p(att), _p(out))
+    return out
+
+
+def ref_gqa_attention(q, k, v, S, n_heads, n_kv, hd):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.empty((S, n_heads * hd), dtype=np.float32)
+    load().ora_ref_gqa_attention(_p(out), _p(q), _p(k), _p(v), S, n_heads, n_kv, hd)
+    return out
+
+
+def decode_layers(Q, kcache, vcache, n_layers, n_heads, heads_per_kv, hd, max_seq, pos,
+                  threads=0, fast=True):
+    """CPU baseline: n_layers independent S=1 attentions (OpenMP over layer x head)."""
+    Q = np.ascontiguousarray(Q, dtype=np.float32)
+    out = np.empty((n_layers, n_heads * hd), dtype=np.float32)
+    load(fast).ora_decode_layers(_p(Q), _p(out), _p(kcache), _p(vcache), n_layers, n_heads,
+                                 heads_per_kv, hd, max_seq, pos, threads)
+    return out
+
+
+def attention_batch_layers(Q, kcache, vcache, n_layers, n_heads, n_kv, hd, max_seq, start_pos, S,
+                           threads=0, fast=True):
+    Q = np.ascontiguousarray(Q, dtype=np.float32)
+    out = np.empty((n_layers, S, n_heads * hd), dtype=np.float32)
+    load(fast).ora_attention_batch_layers(_p(Q), _p(out), _p(kcache), _p(vcache), n_layers,
+                                          n_heads, n_kv, hd, max_seq, start_pos, S, threads)
+    return out
+
+
+def num_threads(fast: bool = True) -> int:
+    return int(load(fast).ora_num_threads())

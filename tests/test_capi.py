@@ -1,0 +1,136 @@
+"""CPU tier: the C-ABI library loads, exports every symbol the headers declare,
+the drop-in header compiles and links as C, and argument errors are reported
+before any device work (no kernel is launched here)."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import anetransformers_amd as mia
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(REPO, "include")
+CLANG = "/opt/rocm/llvm/bin/clang"
+
+
+def declared_functions():
+    names = set()
+    for h in ("miattn.h", "mia_dropin.h"):
+        text = open(os.path.join(INCLUDE, h)).read()
+        # top-level prototypes "type name(" ending in ");" (not static inline wrappers)
+        for m in re.finditer(r"^(?:const\s+)?[A-Za-z_][\w \*]*?\b(mia_\w+)\s*\(", text, re.M):
+            names.add(m.group(1))
+    return sorted(names)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = mia.load()
+    names = declared_functions()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # the Python binding covers the same set
+    assert set(names) <= set(mia.exported_symbols())
+
+
+def test_library_exports_nothing_unprefixed():
+    out = subprocess.run(["nm", "-D", "--defined-only", mia.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = [l.split()[-1] for l in out.splitlines() if " T " in l]
+    ours = [n for n in exported if n.startswith("mia_")]
+    assert len(ours) >= 30
+    assert not [n for n in exported if n in ("apply_rope", "kv_write", "gqa_attention_neon",
+                                               "attention_batch", "kv_alloc")]
+
+
+@pytest.mark.skipif(not os.path.exists(CLANG), reason="ROCm clang not present")
+def test_dropin_header_compiles_and_links(tmp_path):
+    src = tmp_path / "use_dropin.c"
+    src.write_text(r'''
+#include "mia_dropin.h"
+/* the reference's call sequence, mistral/mistral_model.h:849-863 */
+void layer_attention(KVCache *kv, float *q, float *k, float *att, float *out, _Float16 *k16,
+                     _Float16 *v16, const float *theta_inv, int layer, int pos) {
+    apply_rope(q, k, pos, theta_inv, 32, 8, 128);
+    int cache_pos = pos % kv->max_seq;
+    kv_write(kv, layer, cache_pos, k16, v16);
+    if (kv->len < kv->max_seq && pos + 1 > kv->len) kv->len = pos + 1;
+    gqa_attention_neon(q, att, out, kv_k(kv, layer), kv_v(kv, layer), 32, 4, 128, kv->max_seq, pos);
+}
+void prefill(KVCache *kv, float *Q, float *K, float *V, float *out, const float *th,
+             const MistralConfig *c, int start, int S) {
+    apply_rope_batch(Q, K, start, th, c->n_heads, c->n_kv_heads, c->head_dim, S);
+    kv_write_batch(kv, 0, start, K, V, kv->kv_dim, S);
+    attention_batch(Q, out, kv, 0, start, c, S, 0);
+}
+int main(void) { KVCache kv = kv_alloc(1, 8, 128, 16); kv_free(&kv); return kv_k_at(&kv, 0, 0) != 0; }
+''')
+    exe = tmp_path / "use_dropin"
+    r = subprocess.run([CLANG, "-std=c11", "-Wall", "-Werror", "-I", INCLUDE, str(src), "-o",
+                        str(exe), "-L", mia.PKG_DIR, "-lmiattn",
+                        f"-Wl,-rpath,{mia.PKG_DIR}"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_kvcache_struct_layout_matches_reference():
+    # mistral/metal_matvec.h:302 casts KVCache as {int a,b,c,d,e; ptr k, v; int f,g}
+    assert mia.KVCache.k_cache.offset == 24 and mia.KVCache.v_cache.offset == 32
+    assert mia.KVCache.pos.offset == 40 and ctypes.sizeof(mia.KVCache) == 48
+
+
+def test_argument_errors_without_device_work():
+    lib = mia.load()
+    buf = np.zeros(16, np.float32)
+    p = buf.ctypes.data
+    rc = lib.mia_gqa_attention(p, p, p, p, 32, 4, 64, 128, 5, None)     # head_dim 64
+    assert rc == mia.MIA_ERR_UNSUPPORTED and b"head_dim" in lib.mia_last_error()
+    rc = lib.mia_gqa_attention(p, p, p, p, 32, 8, 128, 128, 5, None)    # GQA ratio 8
+    assert rc == mia.MIA_ERR_UNSUPPORTED
+    rc = lib.mia_gqa_attention(None, p, p, p, 32, 4, 128, 128, 5, None)
+    assert rc == mia.MIA_ERR_INVALID
+    rc = lib.mia_gqa_attention(p, p, p, p, 32, 4, 128, 128, -1, None)   # negative pos
+    assert rc == mia.MIA_ERR_INVALID
+    rc = lib.mia_attention_batch(p, p, p, p, 32, 8, 128, 1 << 23, 0, 4, None)  # max_seq too big
+    assert rc == mia.MIA_ERR_UNSUPPORTED
+    rc = lib.mia_attention_step(p, p, p, p, p, p, p, 32, 8, 128, 4096, 2**31 - 4, 8, None)
+    assert rc == mia.MIA_ERR_INVALID and b"overflow" in lib.mia_last_error()
+    rc = lib.mia_rope_f32(p, p, 1, 0, p, 32, 8, 96, None)
+    assert rc == mia.MIA_ERR_UNSUPPORTED
+
+
+def test_no_device_is_reported(monkeypatch):
+    lib = mia.load()
+    n = ctypes.c_int(-1)
+    rc = lib.mia_device_count(ctypes.byref(n))
+    if rc == mia.MIA_OK and n.value > 0:
+        pytest.skip("a device is present")
+    rc = lib.mia_init(0)
+    assert rc in (mia.MIA_ERR_NO_DEVICE, mia.MIA_ERR_INVALID)
+    with pytest.raises(mia.MiattnError):
+        mia.check(rc, "mia_init")
+
+
+def test_dropin_error_path_returns_when_abort_disabled():
+    lib = mia.load()
+    lib.mia_dropin_set_abort(0)
+    try:
+        kv = mia.KVCache()
+        lib.mia_dropin_kv_alloc(ctypes.byref(kv), 0, 8, 128, 16)   # invalid: no layers
+        assert lib.mia_dropin_status() == mia.MIA_ERR_INVALID
+        assert kv.k_cache is None and kv.kv_dim == 1024
+    finally:
+        lib.mia_dropin_set_abort(1)
+
+
+def test_binding_fails_loudly_without_library(tmp_path):
+    saved = mia._lib
+    try:
+        mia._lib = None
+        with pytest.raises(mia.MiattnError):
+            mia.load(str(tmp_path / "nope.so"))
+    finally:
+        mia._lib = saved

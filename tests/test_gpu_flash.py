@@ -1,0 +1,114 @@
+"""GPU parity: S>1 causal attention (fp16 MFMA flash kernel) against the CPU
+oracle on the same seeded inputs, through the C ABI.
+
+mia_attention_batch follows attention_batch (mistral/mistral_ane_prefill.h:
+207-275) over the ring as it stands; mia_attention_step equals S sequential
+decode steps (mistral/speculative.h:92-101), also on a wrapped ring."""
+
+import numpy as np
+import pytest
+
+import _data as D
+import _gpu as G
+import _oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TH = O.theta_inv(D.THETA, D.HD)
+
+
+def _oracle_prefill(kc, vc, Q, K, V, M, start, S):
+    """Reference batched prefill on an unwrapped ring: apply_rope_batch,
+    kv_write_batch, attention_batch (mistral_ane_prefill.h:746-755)."""
+    Qr, Kr = Q.copy(), K.copy()
+    O.load().ora_apply_rope_batch(Qr.ctypes.data, Kr.ctypes.data, start, TH.ctypes.data, 32, 8,
+                                  128, S)
+    O.kv_write_batch(kc, vc, Kr, V, 8, 128, M, start, S)
+    return Qr, O.attention_batch_parallel(Qr, kc, vc, 32, 8, 128, M, start, S)
+
+
+def test_prefill_chunk_after_cache():
+    # 512 new tokens appended after 1536 cached positions (2048 total).
+    G.say("attention_step prefill S=512 start=1536 M=4096")
+    g = D.rng(40)
+    M, start, S = 4096, 1536, 512
+    kc, vc = D.ring(g, M, filled=start)
+    Q, K, V = D.normal(g, (S, 4096)), D.normal(g, (S, 1024)), D.normal(g, (S, 1024))
+    out, kc_g, vc_g = G.attention_step(kc, vc, Q, K, V, TH, M, start, S)
+    kc_o, vc_o = kc.copy(), vc.copy()
+    Qr, ref = _oracle_prefill(kc_o, vc_o, Q, K, V, M, start, S)
+    D.check_close(out, ref, what="prefill S=512")
+    assert np.array_equal(kc_g, kc_o) and np.array_equal(vc_g, vc_o)
+    # the literal attention_batch over the written ring gives the same answer
+    G.say("attention_batch prefill S=512 start=1536 M=4096")
+    out_b = G.attention_batch(Qr, kc_o, vc_o, M, start, S)
+    D.check_close(out_b, ref, what="attention_batch S=512")
+
+
+@pytest.mark.parametrize("start,S", [(0, 2), (0, 3), (5, 7), (0, 8), (100, 9), (0, 33), (3, 64),
+                                     (250, 100)])
+def test_attention_batch_shapes(start, S):
+    G.say(f"attention_batch start={start} S={S}")
+    g = D.rng(50 + start + S)
+    M = 512
+    kc, vc = D.ring(g, M, filled=start + S)
+    Q = D.normal(g, (S, 4096))
+    out = G.attention_batch(Q, kc, vc, M, start, S)
+    ref = O.attention_batch(Q, kc, vc, 32, 8, 128, M, start, S)
+    D.check_close(out, ref, what=f"start={start} S={S}")
+
+
+@pytest.mark.parametrize("M,start,S", [(300, 1000, 8), (64, 200, 5), (128, 100, 40),
+                                       (2048, 2000, 64)])
+def test_verify_step_wrapped_small(M, start, S):
+    G.say(f"attention_step wrapped M={M} start={start} S={S}")
+    g = D.rng(M + start + S)
+    kc, vc = D.ring(g, M)
+    Q, K, V = D.normal(g, (S, 4096)), D.normal(g, (S, 1024)), D.normal(g, (S, 1024))
+    out, kc_g, vc_g = G.attention_step(kc, vc, Q, K, V, TH, M, start, S)
+    kc_o, vc_o = kc.copy(), vc.copy()
+    ref = O.verify_steps(kc_o, vc_o, Q, K, V, start, S, TH, 32, 8, 128, M)
+    D.check_close(out, ref, what=f"verify M={M} start={start} S={S}")
+    assert np.array_equal(kc_g, kc_o) and np.array_equal(vc_g, vc_o)
+
+
+@pytest.mark.parametrize("start", [70000, 66536])
+def test_verify_step_wrapped_65536_ring(start):
+    # 65536-slot ring already wrapped; S=8 drafts at start..start+7 (slots
+    # 4464.. for 70000, slots 1000.. for 66536).
+    G.say(f"attention_step verify M=65536 start={start} S=8")
+    g = D.rng(start)
+    M, S = 65536, 8
+    kc, vc = D.ring(g, M)
+    Q, K, V = D.normal(g, (S, 4096)), D.normal(g, (S, 1024)), D.normal(g, (S, 1024))
+    out, kc_g, vc_g = G.attention_step(kc, vc, Q, K, V, TH, M, start, S)
+    kc_o, vc_o = kc.copy(), vc.copy()
+    ref = O.verify_steps(kc_o, vc_o, Q, K, V, start, S, TH, 32, 8, 128, M)
+    D.check_close(out, ref, what=f"verify 65536 start={start}")
+    assert np.array_equal(kc_g, kc_o) and np.array_equal(vc_g, vc_o)
+
+
+def test_verify_causal_among_drafts_index_revealing():
+    # Drafts carry keys aligned with every query (in the lowest-frequency RoPE
+    # pair, so the alignment survives rotation) and V = their position id; old
+    # ring entries have zero keys.  Query t must average exactly drafts 0..t:
+    # any future draft leaking in, or an evicted entry resurfacing, moves it.
+    G.say("attention_step index-revealing drafts M=40 start=100 S=8")
+    M, start, S = 40, 100, 8
+    kc = np.zeros((M, 1024), np.uint16)
+    vc = np.zeros((M, 1024), np.uint16)
+    vc[:] = D.to_f16_bits(np.full(1024, -500.0, np.float32))
+    Q = np.zeros((S, 4096), np.float32)
+    K = np.zeros((S, 1024), np.float32)
+    Q.reshape(S, 32, 128)[:, :, 126] = 40.0
+    K.reshape(S, 8, 128)[:, :, 126] = 40.0
+    ids = np.arange(start, start + S)
+    V = np.zeros((S, 1024), np.float32)
+    V[:, 0::2] = (ids // 64)[:, None]
+    V[:, 1::2] = (ids % 64)[:, None]
+    out, _, _ = G.attention_step(kc, vc, Q, K, V, TH, M, start, S)
+    out = out.reshape(S, 32, 128)
+    for t in range(S):
+        sel = ids[: t + 1]
+        assert np.allclose(out[t, :, 0::2], (sel // 64).mean(), atol=2e-2), t
+        assert np.allclose(out[t, :, 1::2], (sel % 64).mean(), atol=2e-2), t
