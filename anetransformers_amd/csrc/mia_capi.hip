@@ -1,6 +1,6 @@
 // mia_capi.hip -- extern "C" shim of libmiattn.so (see include/miattn.h).
 // Host code only: validation, per-device context (stream, split-K scratch,
-// arrival counters, work buffers) and launch planning.
+// work buffers) and launch planning.
 #include <hip/hip_runtime.h>
 
 #include <climits>
@@ -25,8 +25,6 @@ struct DevCtx {
   int num_cus = 256;
   void *scratch = nullptr;  // split-K partials
   size_t scratch_bytes = 0;
-  unsigned *counters = nullptr;  // arrival counters, zero between launches
-  size_t n_counters = 0;
   void *work = nullptr;  // rotated Q + fp16 staging for mia_attention_step
   size_t work_bytes = 0;
 };
@@ -67,9 +65,9 @@ hipStream_t pick_stream(DevCtx *c, void *stream) {
   return stream ? reinterpret_cast<hipStream_t>(stream) : c->stream;
 }
 
-// Grows the split-K scratch and the counters.  Growth synchronises the device
-// so that no queued kernel still uses the old buffers.
-int ensure_scratch(DevCtx *c, size_t bytes, size_t n_counters) {
+// Grows the split-K scratch.  Growth synchronises the device so that no
+// queued kernel still uses the old buffer.
+int ensure_scratch(DevCtx *c, size_t bytes) {
   if (bytes > c->scratch_bytes) {
     HIP_TRY(hipDeviceSynchronize());
     if (c->scratch) HIP_TRY(hipFree(c->scratch));
@@ -78,16 +76,6 @@ int ensure_scratch(DevCtx *c, size_t bytes, size_t n_counters) {
     size_t sz = bytes + (bytes >> 2);
     HIP_TRY(hipMalloc(&c->scratch, sz));
     c->scratch_bytes = sz;
-  }
-  if (n_counters > c->n_counters) {
-    HIP_TRY(hipDeviceSynchronize());
-    if (c->counters) HIP_TRY(hipFree(c->counters));
-    c->counters = nullptr;
-    c->n_counters = 0;
-    size_t n = n_counters < 1024 ? 1024 : n_counters * 2;
-    HIP_TRY(hipMalloc(&c->counters, n * sizeof(unsigned)));
-    HIP_TRY(hipMemset(c->counters, 0, n * sizeof(unsigned)));
-    c->n_counters = n;
   }
   return MIA_OK;
 }
@@ -147,15 +135,13 @@ int decode_impl(const float *q, const float *k, const float *v, const float *the
   p.start = (int)start;
   p.new_slot = pos % max_seq;
   p.n_kv = n_kv;
-  p.chunk_rows = mia::decode_pick_chunk_rows(L, n_kv, 2 * c->num_cus);
+  p.chunk_rows = mia::decode_pick_chunk_rows(L, n_kv, 3 * c->num_cus);
   p.nchunk = (L + p.chunk_rows - 1) / p.chunk_rows;
   p.qscale = qscale_log2();
   if (p.nchunk > 1) {
-    if (int rc = ensure_scratch(c, mia::decode_scratch_bytes(n_kv, kG, p.nchunk), (size_t)n_kv))
-      return rc;
+    if (int rc = ensure_scratch(c, mia::decode_scratch_bytes(n_kv, kG, p.nchunk))) return rc;
     p.part_o = reinterpret_cast<float *>(c->scratch);
     p.part_ml = p.part_o + (size_t)n_kv * p.nchunk * kG * kHD;
-    p.counter = c->counters;
   }
   HIP_TRY(mia::launch_decode(p, kG, fused, pick_stream(c, stream)));
   return MIA_OK;
@@ -181,11 +167,10 @@ int flash_impl(DevCtx *c, const float *Q, const uint16_t *kst, const uint16_t *v
   p.qscale = qscale_log2();
   if (p.nsplit > 1) {
     size_t ntile = (size_t)n_kv * p.n_rtiles;
-    if (int rc = ensure_scratch(c, mia::flash_scratch_bytes(n_kv, p.n_rtiles, p.nsplit, rt), ntile))
+    if (int rc = ensure_scratch(c, mia::flash_scratch_bytes(n_kv, p.n_rtiles, p.nsplit, rt)))
       return rc;
     p.part_o = reinterpret_cast<float *>(c->scratch);
     p.part_ml = p.part_o + ntile * p.nsplit * rt * kHD;
-    p.counter = c->counters;
   }
   HIP_TRY(mia::launch_flash(p, kG, s, nullptr));
   return MIA_OK;

@@ -5,17 +5,22 @@
 // fp16 round of k/v, ring write at pos % max_seq, attention).
 //
 // Grid: one workgroup per (kv head, chunk of the window); blockIdx % n_kv is
-// the kv head so that, with the hardware's round-robin workgroup dispatch over
-// the 8 XCDs, every chunk of one kv head (and its partials) stays on one XCD.
+// the kv head, so with the hardware's round-robin workgroup dispatch over the
+// 8 XCDs every chunk of one kv head (and its partials) stays on one XCD.
 //
-// Workgroup = 4 waves; each wave owns 64-row slices of the chunk.  Inside a
-// wave a 16-lane DPP row handles one cache row: lane j holds dims 8j..8j+7, so
-// a wave load instruction fetches 4 rows x 256 contiguous bytes, and each
-// loaded fp16 element is used by all G query heads of the group from
-// registers (v_fma_mix_f32, no conversion instructions).  Scores of a 64-row
-// slice go through LDS once (one lane per row) for the wave-level online
-// softmax; the 4 wave partials are merged in LDS, and chunk partials are merged
-// by the last-arriving workgroup of the kv head (log-sum-exp merge).
+// Each of the 4 waves of a workgroup is an independent pipeline over 16-key
+// tiles (wave w takes tiles w, w+4, ...), double-buffered in registers so that
+// the next tiles' loads are in flight while the current tile is computed:
+//   scores  v_mfma_f32_16x16x32_f16: A = 16 key rows straight from the
+//           loads (lane = key row, 64 contiguous bytes), B = the G=4 query
+//           heads of the group with q split into fp16 hi + lo parts along K
+//           (q = hi + lo to ~2^-22), so the scores carry fp32 q accuracy.
+//   softmax wave-local online max / sum in the log2 domain; probabilities go
+//           through 256 B of LDS to the V-lane layout.
+//   P.V     v_fma_mix_f32: a 16-lane row owns 8 dims of 4 keys, every loaded
+//           fp16 V element feeds the 4 heads without a conversion.
+// The 4 wave partials are merged in LDS; chunk partials are merged by a
+// second, small kernel (log-sum-exp merge).
 #include "mia_device.h"
 #include "mia_kernels.h"
 
@@ -24,48 +29,89 @@ namespace mia {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kBlockRows = 256;  // rows per workgroup pass (4 waves x 64)
-constexpr int kGroups = 16;      // 4-row load groups per wave slice
+constexpr int kWaves = 4;
+constexpr int kTile = 16;        // keys per wave tile
+constexpr int kChunkAlign = 64;  // chunk_rows granularity (one tile per wave)
 constexpr int kMaxChunks = 256;  // merge capacity per kv head
+constexpr int G = 4;             // query heads per kv head
 
-template <int G>
 struct DecodeSmem {
-  float2 cs[64];               // RoPE (cos, sin) for the 64 pair indices
-  float p[4][64][G];           // per-wave slice scores -> probabilities
-  float ml[4][2 * G];          // per-wave (max, sum)
-  int last;
-  union {
-    float acc[4][4][G][HD];    // per-(wave, row group) partial outputs
-    struct {
-      float2 mlc[kMaxChunks * G];
-      float wt[kMaxChunks * G];
-      float2 fin[G];
-    } merge;
-  } u;
+  float2 cs[64];                 // RoPE (cos, sin) for the 64 pair indices
+  _Float16 knew[HD];             // rotated fp16 new key of this kv head
+  _Float16 vnew[HD];
+  float p[kWaves][16][kTile];    // per-wave tile probabilities [column][key]
+  float ml[kWaves][2 * G];       // per-wave (max, sum)
+  float acc[kWaves][4][G][HD];   // per-(wave, row group) partial outputs
 };
 
-template <int G>
-__device__ __forceinline__ void load_row_vec(const float *src, float (&v)[G]) {
-#pragma unroll
-  for (int g = 0; g < G; ++g) v[g] = src[g];
+struct TileBuf {
+  u4 k[4];  // MFMA A operand, k-step s: key row lane%16, dims 32*s + 8*(lane/16) .. +8
+  u4 v[4];  // P.V operand: keys 4*(lane/16) + m, dims 8*(lane%16) .. +8
+};
+
+// Value of x in lane `src` (uniform result).
+__device__ __forceinline__ float lane_value(float x, int src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), src));
 }
 
-template <int G, bool FUSED>
-__global__ void __launch_bounds__(kThreads, 2) decode_kernel(DecodeParams p) {
-  static_assert(G == 4, "decode kernel is instantiated for 4 query heads per kv head");
-  __shared__ DecodeSmem<G> sm;
+__device__ __forceinline__ int ring_slot(int start, int t, int max_seq) {
+  int s = start + t;
+  return s >= max_seq ? s - max_seq : s;
+}
+
+template <bool FUSED>
+__global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
+  __shared__ DecodeSmem sm;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
-  const int r = lane >> 4;  // row within a 4-row load group
-  const int j = lane & 15;  // dims 8j..8j+7
+  const int lc = lane & 15;  // MFMA column / V dim block
+  const int lg = lane >> 4;  // MFMA k group / V key group
   const int kvh = blockIdx.x % p.n_kv;
   const int chunk = blockIdx.x / p.n_kv;
   const int kv_dim = p.n_kv * HD;
   const int c0 = chunk * p.chunk_rows;
   const int c1 = min(c0 + p.chunk_rows, p.L);
   const bool has_new = FUSED && (c1 == p.L);
+
+  // The new token (fused, last chunk) is attended after the loop from its
+  // fp16 copy in LDS, so the tiles cover [c0, ce).
+  const int ce = has_new ? p.L - 1 : c1;
+  // Tiles of this wave: global tile index tt = (c0/16) + w + 4*i.
+  const int first_tile = c0 / kTile + w;
+  const int end_tile = (ce + kTile - 1) / kTile;  // exclusive
+  const int n_my = first_tile < end_tile ? (end_tile - first_tile + kWaves - 1) / kWaves : 0;
+  const int last_tile = first_tile + kWaves * (n_my > 0 ? n_my - 1 : 0);
+
+  const _Float16 *kbase = p.kc + (size_t)kvh * HD;
+  const _Float16 *vbase = p.vc + (size_t)kvh * HD;
+
+  auto issue = [&](TileBuf &b, int i) {
+    const int tt = min(first_tile + kWaves * i, last_tile);  // clamp: re-read, L2 hit
+    const int t0 = tt * kTile;
+    {
+      int t = min(t0 + lc, ce - 1);
+      unsigned off = (unsigned)ring_slot(p.start, t, p.max_seq) * (unsigned)kv_dim + 8 * lg;
+      const _Float16 *src = kbase + off;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) b.k[s] = *reinterpret_cast<const u4 *>(src + 32 * s);
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      int t = min(t0 + 4 * lg + m, ce - 1);
+      unsigned off = (unsigned)ring_slot(p.start, t, p.max_seq) * (unsigned)kv_dim + 8 * lc;
+      b.v[m] = *reinterpret_cast<const u4 *>(vbase + off);
+    }
+  };
+
+  // First two tiles are requested before the prologue so that their latency
+  // overlaps the RoPE table, the new-token write and the q operand set-up.
+  TileBuf ba, bb;
+  if (n_my > 0) {
+    issue(ba, 0);
+    issue(bb, 1);
+  }
 
   if (FUSED) {
     if (tid < 64) {
@@ -76,165 +122,158 @@ __global__ void __launch_bounds__(kThreads, 2) decode_kernel(DecodeParams p) {
       sm.cs[tid] = make_float2(cs, sn);
     }
     __syncthreads();
+    if (has_new && tid < 64) {
+      // new k rotated (pair tid) and v, rounded to fp16 (mistral_model.h:854-857)
+      float2 kv = *reinterpret_cast<const float2 *>(p.knew + (size_t)kvh * HD + 2 * tid);
+      float2 cs = sm.cs[tid];
+      rope_pair(kv.x, kv.y, cs.x, cs.y);
+      float2 vv = *reinterpret_cast<const float2 *>(p.vnew + (size_t)kvh * HD + 2 * tid);
+      sm.knew[2 * tid] = (_Float16)kv.x;
+      sm.knew[2 * tid + 1] = (_Float16)kv.y;
+      sm.vnew[2 * tid] = (_Float16)vv.x;
+      sm.vnew[2 * tid + 1] = (_Float16)vv.y;
+    }
+    __syncthreads();
+    if (has_new && tid < 16) {  // ring write of the new row (256 B per tensor)
+      size_t off = (size_t)p.new_slot * kv_dim + (size_t)kvh * HD + 8 * tid;
+      *reinterpret_cast<u4 *>(p.kc + off) = *reinterpret_cast<const u4 *>(&sm.knew[8 * tid]);
+      *reinterpret_cast<u4 *>(p.vc + off) = *reinterpret_cast<const u4 *>(&sm.vnew[8 * tid]);
+    }
   }
 
-  // q of the G heads sharing this kv head, dims 8j..8j+7, rotated and scaled.
-  float q[G][8];
+  // B operand: column lc < G is query head kvh*G + lc; k-step s covers dims
+  // 32*s + 8*lg .. +8 (the same dims the A lanes load), hi and lo parts.
+  h8 qhi[4], qlo[4];
+  {
+    const bool col = lc < G;
+    const float *qsrc = p.q + (size_t)(kvh * G + (col ? lc : 0)) * HD + 8 * lg;
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const f4 *src = reinterpret_cast<const f4 *>(p.q + (size_t)(kvh * G + g) * HD + 8 * j);
-    f4 a = src[0], b = src[1];
-    float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    if (FUSED) {
+    for (int s = 0; s < 4; ++s) {
+      const f4 *src = reinterpret_cast<const f4 *>(qsrc + 32 * s);
+      f4 a = src[0], b = src[1];
+      float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      if (FUSED) {
 #pragma unroll
-      for (int pi = 0; pi < 4; ++pi) {
-        float2 cs = sm.cs[4 * j + pi];
-        rope_pair(v[2 * pi], v[2 * pi + 1], cs.x, cs.y);
+        for (int pi = 0; pi < 4; ++pi) {
+          float2 cs = sm.cs[16 * s + 4 * lg + pi];
+          rope_pair(v[2 * pi], v[2 * pi + 1], cs.x, cs.y);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float x = col ? v[e] * p.qscale : 0.f;
+        _Float16 hi = (_Float16)x;
+        qhi[s][e] = hi;
+        qlo[s][e] = (_Float16)(x - (float)hi);
       }
     }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) q[g][e] = v[e] * p.qscale;
   }
 
-  // The new token's fp16 k/v for this kv head (only the last chunk uses it).
-  h8 kn16 = {}, vn16 = {};
-  if (has_new) {
-    const f4 *ks = reinterpret_cast<const f4 *>(p.knew + (size_t)kvh * HD + 8 * j);
-    const f4 *vs = reinterpret_cast<const f4 *>(p.vnew + (size_t)kvh * HD + 8 * j);
-    f4 a = ks[0], b = ks[1];
-    float kv8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int pi = 0; pi < 4; ++pi) {
-      float2 cs = sm.cs[4 * j + pi];
-      rope_pair(kv8[2 * pi], kv8[2 * pi + 1], cs.x, cs.y);
-    }
-    f4 va = vs[0], vb = vs[1];
-    float vv8[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      kn16[e] = (_Float16)kv8[e];  // RNE, as vcvt_f16_f32 (mistral_model.h:854)
-      vn16[e] = (_Float16)vv8[e];
-    }
-    if (tid < 16) {  // one 256-B row per tensor: kv_write at pos % max_seq
-      size_t off = (size_t)p.new_slot * kv_dim + (size_t)kvh * HD + 8 * j;
-      *reinterpret_cast<u4 *>(p.kc + off) = __builtin_bit_cast(u4, kn16);
-      *reinterpret_cast<u4 *>(p.vc + off) = __builtin_bit_cast(u4, vn16);
-    }
-  }
 
-  float m_run[G], l_run[G], acc[G][8];
+  // m_run[g]: wave-uniform running max of head g; m_lane: the same value for
+  // the head of this lane's MFMA column (lanes with lc >= G carry junk).
+  float m_run[G], m_lane = -INFINITY, l_part = 0.f, acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m_run[g] = -INFINITY;
-    l_run[g] = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   }
 
-  const _Float16 *kbase = p.kc + (size_t)kvh * HD + 8 * j;
-  const _Float16 *vbase = p.vc + (size_t)kvh * HD + 8 * j;
-
-  for (int b0 = c0; b0 < c1; b0 += kBlockRows) {
-    const int rb = b0 + w * 64;  // first row of this wave's slice
-    if (rb >= c1) break;         // wave-uniform: nothing left for this wave
-
-    u4 kd[kGroups], vd[kGroups];
+  // One 16-key tile starting at key t0; keys >= cend are masked.
+  auto process = [&](const TileBuf &b, int t0, int cend) {
+    h8 ka[4];
 #pragma unroll
-    for (int g = 0; g < kGroups; ++g) {
-      int t = min(rb + g * 4 + r, c1 - 1);
-      int slot = p.start + t;
-      slot = slot >= p.max_seq ? slot - p.max_seq : slot;
-      unsigned off = (unsigned)slot * (unsigned)kv_dim;
-      kd[g] = *reinterpret_cast<const u4 *>(kbase + off);
+    for (int s = 0; s < 4; ++s) ka[s] = __builtin_bit_cast(h8, b.k[s]);
+    f4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s], qhi[s], d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s], qlo[s], d, 0, 0, 0);
     }
+    // d[i]: score of key t0 + 4*lg + i for head lc (lanes lc < G).
+    float sc[4];
+    float mx = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < kGroups; ++g) {
-      int t = min(rb + g * 4 + r, c1 - 1);
-      int slot = p.start + t;
-      slot = slot >= p.max_seq ? slot - p.max_seq : slot;
-      unsigned off = (unsigned)slot * (unsigned)kv_dim;
-      vd[g] = *reinterpret_cast<const u4 *>(vbase + off);
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = (t0 + 4 * lg + i < cend) ? d[i] : -INFINITY;
+      mx = fmaxf(mx, sc[i]);
     }
-
-    // Scores: 8-dim partial dots per lane, summed over the 16-lane row.
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // every lane of column lc now holds the tile max of head lc
+    const float m_lane_new = fmaxf(m_lane, mx);
+    float m_new[G];
+    bool grow = false;
 #pragma unroll
-    for (int g = 0; g < kGroups; ++g) {
-      const int t = rb + g * 4 + r;
-      h8 kh = __builtin_bit_cast(h8, kd[g]);
-      if (has_new && t == p.L - 1) kh = kn16;
-      float d[G];
+    for (int g = 0; g < G; ++g) {
+      m_new[g] = lane_value(m_lane_new, g);
+      grow |= m_new[g] > m_run[g];
+    }
+    if (grow) {  // wave-uniform
 #pragma unroll
-      for (int gg = 0; gg < G; ++gg) d[gg] = 0.f;
+      for (int g = 0; g < G; ++g) {
+        const float alpha = fast_exp2(m_run[g] - m_new[g]);
+        m_run[g] = m_new[g];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] *= alpha;
+      }
+      l_part *= fast_exp2(m_lane - m_lane_new);
+    }
+    m_lane = m_lane_new;
+    const float mine = m_lane;
+    f4 pv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pv[i] = fast_exp2(sc[i] - mine);
+    if (lc < G) l_part += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+    *reinterpret_cast<f4 *>(&sm.p[w][lc][4 * lg]) = pv;
+    wave_lds_sync();
+    f4 pp[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) pp[g] = *reinterpret_cast<const f4 *>(&sm.p[w][g][4 * lg]);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const h8 vh = __builtin_bit_cast(h8, b.v[m]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        float kf = (float)kh[e];
+        const float vf = (float)vh[e];
 #pragma unroll
-        for (int gg = 0; gg < G; ++gg) d[gg] = __builtin_fmaf(q[gg][e], kf, d[gg]);
-      }
-#pragma unroll
-      for (int gg = 0; gg < G; ++gg) d[gg] = row16_sum(d[gg]);
-      if (j == 0) {
-        const bool valid = t < c1;
-        f4 sv = {valid ? d[0] : -INFINITY, valid ? d[1] : -INFINITY,
-                 valid ? d[2] : -INFINITY, valid ? d[3] : -INFINITY};
-        *reinterpret_cast<f4 *>(&sm.p[w][g * 4 + r][0]) = sv;
+        for (int g = 0; g < G; ++g) acc[g][e] = __builtin_fmaf(pp[g][m], vf, acc[g][e]);
       }
     }
     wave_lds_sync();
+  };
 
-    // Wave-level online softmax over the slice (one row per lane).
-    {
-      f4 sc = *reinterpret_cast<const f4 *>(&sm.p[w][lane][0]);
-      float s[G] = {sc.x, sc.y, sc.z, sc.w};
-      float pr[G];
-#pragma unroll
-      for (int gg = 0; gg < G; ++gg) {
-        float mb = wave_max(s[gg]);
-        float mn = fmaxf(m_run[gg], mb);
-        float alpha = fast_exp2(m_run[gg] - mn);
-        pr[gg] = fast_exp2(s[gg] - mn);
-        float lb = wave_sum(pr[gg]);
-        l_run[gg] = l_run[gg] * alpha + lb;
-        m_run[gg] = mn;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[gg][e] *= alpha;
-      }
-      f4 pv = {pr[0], pr[1], pr[2], pr[3]};
-      *reinterpret_cast<f4 *>(&sm.p[w][lane][0]) = pv;
-    }
-    wave_lds_sync();
-
-    // Weighted V sum.
-#pragma unroll
-    for (int g = 0; g < kGroups; ++g) {
-      const int t = rb + g * 4 + r;
-      f4 pp = *reinterpret_cast<const f4 *>(&sm.p[w][g * 4 + r][0]);
-      float pw[G] = {pp.x, pp.y, pp.z, pp.w};
-      h8 vh = __builtin_bit_cast(h8, vd[g]);
-      if (has_new && t == p.L - 1) vh = vn16;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float vf = (float)vh[e];
-#pragma unroll
-        for (int gg = 0; gg < G; ++gg) acc[gg][e] = __builtin_fmaf(pw[gg], vf, acc[gg][e]);
-      }
-    }
-    wave_lds_sync();
-  }
-
-  // Merge the 4 waves x 4 row groups inside the workgroup.
-  if (lane == 0) {
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg) {
-      sm.ml[w][gg] = m_run[gg];
-      sm.ml[w][G + gg] = l_run[gg];
+  if (n_my > 0) {
+    for (int i = 0; i < n_my; i += 2) {
+      process(ba, (first_tile + kWaves * i) * kTile, ce);
+      issue(ba, i + 2);
+      if (i + 1 < n_my) process(bb, (first_tile + kWaves * (i + 1)) * kTile, ce);
+      issue(bb, i + 3);
     }
   }
+  if (has_new && w == 0) {
+    // Every row of this tile is the new key / value; only key 0 is unmasked.
+    TileBuf nb;
 #pragma unroll
-  for (int gg = 0; gg < G; ++gg) {
-    f4 *dst = reinterpret_cast<f4 *>(&sm.u.acc[w][r][gg][8 * j]);
-    dst[0] = f4{acc[gg][0], acc[gg][1], acc[gg][2], acc[gg][3]};
-    dst[1] = f4{acc[gg][4], acc[gg][5], acc[gg][6], acc[gg][7]};
+    for (int s = 0; s < 4; ++s) nb.k[s] = *reinterpret_cast<const u4 *>(&sm.knew[32 * s + 8 * lg]);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) nb.v[m] = *reinterpret_cast<const u4 *>(&sm.vnew[8 * lc]);
+    process(nb, p.L - 1, p.L);
+  }
+
+  // Wave totals: l over the 4 key groups of column lc.
+  l_part += __shfl_xor(l_part, 16);
+  l_part += __shfl_xor(l_part, 32);
+  if (lane < G) {
+    sm.ml[w][lane] = m_lane;
+    sm.ml[w][G + lane] = l_part;
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    f4 *dst = reinterpret_cast<f4 *>(&sm.acc[w][lg][g][8 * lc]);
+    dst[0] = f4{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
+    dst[1] = f4{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
   }
   __syncthreads();
 
@@ -243,17 +282,18 @@ __global__ void __launch_bounds__(kThreads, 2) decode_kernel(DecodeParams p) {
 #pragma unroll
   for (int oi = 0; oi < kOuts; ++oi) {
     const int o = tid + oi * kThreads;
-    const int gg = o / HD, d = o % HD;
+    const int g = o / HD, d = o % HD;
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, sm.ml[ww][gg]);
+    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, sm.ml[ww][g]);
+    const float Mu = M == -INFINITY ? 0.f : M;
     float Ls = 0.f, O = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
-      float e = fast_exp2(sm.ml[ww][gg] - M);
-      Ls = __builtin_fmaf(e, sm.ml[ww][G + gg], Ls);
-      float s = (sm.u.acc[ww][0][gg][d] + sm.u.acc[ww][1][gg][d]) +
-                (sm.u.acc[ww][2][gg][d] + sm.u.acc[ww][3][gg][d]);
+    for (int ww = 0; ww < kWaves; ++ww) {
+      float e = fast_exp2(sm.ml[ww][g] - Mu);
+      Ls = __builtin_fmaf(e, sm.ml[ww][G + g], Ls);
+      float s = (sm.acc[ww][0][g][d] + sm.acc[ww][1][g][d]) +
+                (sm.acc[ww][2][g][d] + sm.acc[ww][3][g][d]);
       O = __builtin_fmaf(e, s, O);
     }
     o_val[oi] = O;
@@ -263,10 +303,8 @@ __global__ void __launch_bounds__(kThreads, 2) decode_kernel(DecodeParams p) {
 
   if (p.nchunk == 1) {
 #pragma unroll
-    for (int oi = 0; oi < kOuts; ++oi) {
-      const int o = tid + oi * kThreads;
-      p.out[(size_t)kvh * G * HD + o] = o_val[oi] / l_wg[oi];
-    }
+    for (int oi = 0; oi < kOuts; ++oi)
+      p.out[(size_t)kvh * G * HD + tid + oi * kThreads] = o_val[oi] / l_wg[oi];
     return;
   }
 
@@ -275,90 +313,78 @@ __global__ void __launch_bounds__(kThreads, 2) decode_kernel(DecodeParams p) {
   for (int oi = 0; oi < kOuts; ++oi) {
     const int o = tid + oi * kThreads;
     p.part_o[pbase * HD + o] = o_val[oi];
-    if ((o % HD) == 0) {
-      const int gg = o / HD;
-      *reinterpret_cast<float2 *>(p.part_ml + (pbase + gg) * 2) = make_float2(m_wg[oi], l_wg[oi]);
-    }
+    if ((o % HD) == 0)
+      *reinterpret_cast<float2 *>(p.part_ml + (pbase + o / HD) * 2) = make_float2(m_wg[oi], l_wg[oi]);
   }
+}
 
-  // Last-arriving workgroup of this kv head merges all chunk partials.
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    unsigned prev = atomicAdd(&p.counter[kvh], 1u);
-    sm.last = (prev == (unsigned)(p.nchunk - 1));
-  }
-  __syncthreads();
-  if (!sm.last) return;
-  __threadfence();
-
-  const size_t hbase = (size_t)kvh * p.nchunk * G;
-  for (int i = tid; i < p.nchunk * G; i += kThreads)
-    sm.u.merge.mlc[i] = *reinterpret_cast<const float2 *>(p.part_ml + (hbase + i) * 2);
-  __syncthreads();
-  if (tid < G) {
+// Cross-chunk log-sum-exp merge, one workgroup per (kv head, q head).  A
+// separate launch: the kernel boundary orders the partial writes before these
+// reads, where an in-kernel last-arriver merge would need an agent-scope fence
+// (an L2 write-back) in every workgroup.
+__global__ void __launch_bounds__(HD) decode_merge_kernel(DecodeParams p) {
+  __shared__ float wt[kMaxChunks];
+  __shared__ float inv_l;
+  const int kvh = blockIdx.x / G, g = blockIdx.x % G;
+  const int tid = threadIdx.x;
+  const size_t hb = (size_t)kvh * p.nchunk * G;
+  if (tid < 64) {
     float M = -INFINITY;
-    for (int c = 0; c < p.nchunk; ++c) M = fmaxf(M, sm.u.merge.mlc[c * G + tid].x);
+    for (int c = tid; c < p.nchunk; c += 64) M = fmaxf(M, p.part_ml[(hb + (size_t)c * G + g) * 2]);
+    M = wave_max(M);
     float Ls = 0.f;
-    for (int c = 0; c < p.nchunk; ++c) {
-      float2 ml = sm.u.merge.mlc[c * G + tid];
-      Ls = __builtin_fmaf(fast_exp2(ml.x - M), ml.y, Ls);
+    for (int c = tid; c < p.nchunk; c += 64) {
+      float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + (hb + (size_t)c * G + g) * 2);
+      float e = fast_exp2(ml.x - M);
+      wt[c] = e;
+      Ls = __builtin_fmaf(e, ml.y, Ls);
     }
-    sm.u.merge.fin[tid] = make_float2(M, 1.0f / Ls);
+    Ls = wave_sum(Ls);
+    if (tid == 0) inv_l = 1.0f / Ls;
   }
   __syncthreads();
-  for (int i = tid; i < p.nchunk * G; i += kThreads) {
-    float2 fin = sm.u.merge.fin[i % G];
-    sm.u.merge.wt[i] = fast_exp2(sm.u.merge.mlc[i].x - fin.x) * fin.y;
+  float O = 0.f;
+  const float *src = p.part_o + (hb + g) * HD + tid;
+  int c = 0;
+  for (; c + 4 <= p.nchunk; c += 4) {
+    float a0 = src[(size_t)(c + 0) * G * HD], a1 = src[(size_t)(c + 1) * G * HD];
+    float a2 = src[(size_t)(c + 2) * G * HD], a3 = src[(size_t)(c + 3) * G * HD];
+    O = __builtin_fmaf(wt[c + 0], a0, O);
+    O = __builtin_fmaf(wt[c + 1], a1, O);
+    O = __builtin_fmaf(wt[c + 2], a2, O);
+    O = __builtin_fmaf(wt[c + 3], a3, O);
   }
-  __syncthreads();
-#pragma unroll
-  for (int oi = 0; oi < kOuts; ++oi) {
-    const int o = tid + oi * kThreads;
-    const int gg = o / HD;
-    float O = 0.f;
-    const float *src = p.part_o + hbase * HD + o;
-    int c = 0;
-    for (; c + 4 <= p.nchunk; c += 4) {
-      float a0 = src[(size_t)(c + 0) * G * HD], a1 = src[(size_t)(c + 1) * G * HD];
-      float a2 = src[(size_t)(c + 2) * G * HD], a3 = src[(size_t)(c + 3) * G * HD];
-      O = __builtin_fmaf(sm.u.merge.wt[(c + 0) * G + gg], a0, O);
-      O = __builtin_fmaf(sm.u.merge.wt[(c + 1) * G + gg], a1, O);
-      O = __builtin_fmaf(sm.u.merge.wt[(c + 2) * G + gg], a2, O);
-      O = __builtin_fmaf(sm.u.merge.wt[(c + 3) * G + gg], a3, O);
-    }
-    for (; c < p.nchunk; ++c) O = __builtin_fmaf(sm.u.merge.wt[c * G + gg], src[(size_t)c * G * HD], O);
-    p.out[(size_t)kvh * G * HD + o] = O;
-  }
-  if (tid == 0) atomicExch(&p.counter[kvh], 0u);
+  for (; c < p.nchunk; ++c) O = __builtin_fmaf(wt[c], src[(size_t)c * G * HD], O);
+  p.out[((size_t)kvh * G + g) * HD + tid] = O * inv_l;
 }
 
 }  // namespace
 
-size_t decode_scratch_bytes(int n_kv, int G, int nchunk) {
-  return (size_t)n_kv * nchunk * G * (HD + 2) * sizeof(float);
+size_t decode_scratch_bytes(int n_kv, int g, int nchunk) {
+  return (size_t)n_kv * nchunk * g * (HD + 2) * sizeof(float);
 }
 
 int decode_pick_chunk_rows(int L, int n_kv, int target_wgs) {
   long per = ((long)L * n_kv + target_wgs - 1) / target_wgs;
-  long rows = ((per + kBlockRows - 1) / kBlockRows) * kBlockRows;
-  if (rows < kBlockRows) rows = kBlockRows;
+  long rows = ((per + kChunkAlign - 1) / kChunkAlign) * kChunkAlign;
+  if (rows < kChunkAlign) rows = kChunkAlign;
   long nchunk = (L + rows - 1) / rows;
   while (nchunk > kMaxChunks) {
-    rows += kBlockRows;
+    rows += kChunkAlign;
     nchunk = (L + rows - 1) / rows;
   }
   return (int)rows;
 }
 
-hipError_t launch_decode(const DecodeParams &p, int G, bool fused, hipStream_t s) {
-  if (G != 4) return hipErrorInvalidValue;
-  if (p.nchunk > kMaxChunks || p.chunk_rows % kBlockRows) return hipErrorInvalidValue;
+hipError_t launch_decode(const DecodeParams &p, int g, bool fused, hipStream_t s) {
+  if (g != G) return hipErrorInvalidValue;
+  if (p.nchunk > kMaxChunks || p.chunk_rows % kChunkAlign) return hipErrorInvalidValue;
   dim3 grid(p.n_kv * p.nchunk), block(kThreads);
   if (fused)
-    hipLaunchKernelGGL((decode_kernel<4, true>), grid, block, 0, s, p);
+    hipLaunchKernelGGL(decode_kernel<true>, grid, block, 0, s, p);
   else
-    hipLaunchKernelGGL((decode_kernel<4, false>), grid, block, 0, s, p);
+    hipLaunchKernelGGL(decode_kernel<false>, grid, block, 0, s, p);
+  if (p.nchunk > 1) hipLaunchKernelGGL(decode_merge_kernel, dim3(p.n_kv * G), dim3(HD), 0, s, p);
   return hipGetLastError();
 }
 

@@ -17,8 +17,8 @@
 // min(pos+1, max_seq) (mistral_ane_prefill.h:220-241); positions >= start come
 // from the staging buffer when one is given, which keeps the ring untouched
 // until the caller commits (sequential-verify semantics on a wrapped ring).
-// Key ranges are split over workgroups; the last-arriving workgroup of a tile
-// merges the partials (log-sum-exp).
+// Key ranges are split over workgroups; a second kernel merges the partials
+// (log-sum-exp).
 #include "mia_device.h"
 #include "mia_kernels.h"
 
@@ -32,7 +32,6 @@ constexpr int kPitch = HD + 8;           // LDS row pitch in halfs (272 B)
 struct FlashSmem {
   _Float16 k[kKeys][kPitch];
   _Float16 v[kKeys][kPitch];
-  int last;
 };
 
 __device__ __forceinline__ int window_lo(int pos, int max_seq) {
@@ -215,41 +214,38 @@ __global__ void __launch_bounds__(64 * NW) flash_kernel(FlashParams p) {
     if (half == 0)
       *reinterpret_cast<float2 *>(p.part_ml + pb_idx * 2) = make_float2(m_run, l_tot);
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    unsigned prev = atomicAdd(&p.counter[tile_id], 1u);
-    sm.last = (prev == (unsigned)(p.nsplit - 1));
-  }
-  __syncthreads();
-  if (!sm.last) return;
-  __threadfence();
+}
 
-  // Merge: thread handles (row, 4 dims) items.
-  for (int it = tid; it < RT * (HD / 4); it += NT) {
-    const int rl = it / (HD / 4);
-    const int d4 = it % (HD / 4);
-    const int rrow = row0 + rl;
-    const int tt = rrow / G, gg = rrow % G;
-    if (tt >= p.S) continue;
-    float M = -INFINITY;
-    for (int sp = 0; sp < p.nsplit; ++sp)
-      M = fmaxf(M, p.part_ml[((tile_id * p.nsplit + sp) * RT + rl) * 2]);
-    float Ls = 0.f;
-    f4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < p.nsplit; ++sp) {
-      const size_t idx = (tile_id * p.nsplit + sp) * RT + rl;
-      float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + idx * 2);
-      float e = fast_exp2(ml.x - M);
-      Ls = __builtin_fmaf(e, ml.y, Ls);
-      f4 v = *reinterpret_cast<const f4 *>(p.part_o + idx * HD + 4 * d4);
-      acc += e * v;
-    }
-    const float inv = 1.0f / Ls;
-    *reinterpret_cast<f4 *>(p.out + (size_t)tt * dim_model + (size_t)(kvh * G + gg) * HD + 4 * d4) =
-        acc * inv;
+// Split-K merge: one workgroup per 8 rows of a tile, thread = (row, 4 dims).
+// A separate launch, so the kernel boundary orders the partial writes before
+// these reads (no agent-scope fence in the attention kernel).
+template <int G>
+__global__ void __launch_bounds__(256) flash_merge_kernel(FlashParams p, int rt) {
+  const int tid = threadIdx.x;
+  const int blocks_per_tile = rt / 8;
+  const int tile_id = blockIdx.x / blocks_per_tile;
+  const int rl = (blockIdx.x % blocks_per_tile) * 8 + tid / 32;
+  const int d4 = tid % 32;
+  const int kvh = tile_id / p.n_rtiles, rtile = tile_id % p.n_rtiles;
+  const int row = rtile * rt + rl;
+  const int t = row / G, g = row % G;
+  if (t >= p.S) return;
+  const int dim_model = p.n_kv * G * HD;
+  float M = -INFINITY;
+  for (int sp = 0; sp < p.nsplit; ++sp)
+    M = fmaxf(M, p.part_ml[(((size_t)tile_id * p.nsplit + sp) * rt + rl) * 2]);
+  float Ls = 0.f;
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < p.nsplit; ++sp) {
+    const size_t idx = ((size_t)tile_id * p.nsplit + sp) * rt + rl;
+    float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + idx * 2);
+    float e = fast_exp2(ml.x - M);
+    Ls = __builtin_fmaf(e, ml.y, Ls);
+    f4 v = *reinterpret_cast<const f4 *>(p.part_o + idx * HD + 4 * d4);
+    acc += e * v;
   }
-  if (tid == 0) atomicExch(&p.counter[tile_id], 0u);
+  *reinterpret_cast<f4 *>(p.out + (size_t)t * dim_model + (size_t)(kvh * G + g) * HD + 4 * d4) =
+      acc * (1.0f / Ls);
 }
 
 }  // namespace
@@ -297,6 +293,9 @@ hipError_t launch_flash(const FlashParams &p, int G, hipStream_t s, int *rows_pe
     hipLaunchKernelGGL((flash_kernel<4, 1>), grid, dim3(64), 0, s, p);
   else
     hipLaunchKernelGGL((flash_kernel<4, 4>), grid, dim3(256), 0, s, p);
+  if (p.nsplit > 1)
+    hipLaunchKernelGGL((flash_merge_kernel<4>), dim3(p.n_kv * p.n_rtiles * (rt / 8)), dim3(256), 0,
+                       s, p, rt);
   return hipGetLastError();
 }
 

@@ -18,7 +18,6 @@ struct DecodeParams {
   float *out;              // [n_kv*G][128]
   float *part_o;           // [n_kv][nchunk][G][128] unnormalised partial outputs
   float *part_ml;          // [n_kv][nchunk][G][2] partial (max, sum), log2 domain
-  unsigned *counter;       // [n_kv] arrival counters, zero between launches
   int max_seq;             // ring capacity M
   int pos;                 // absolute position of the query token
   int L;                   // window length min(pos+1, M)
@@ -26,7 +25,7 @@ struct DecodeParams {
   int new_slot;            // pos mod M
   int n_kv;
   int nchunk;              // workgroups per kv head
-  int chunk_rows;          // rows per workgroup (multiple of 256)
+  int chunk_rows;          // rows per workgroup (multiple of 64)
   float qscale;            // (1/sqrt(128)) * log2(e)
 };
 
@@ -45,7 +44,6 @@ struct FlashParams {
   float *out;              // [S][n_heads*128]
   float *part_o;           // split-K partials (nsplit > 1)
   float *part_ml;
-  unsigned *counter;       // [n_kv * n_rtiles]
   int S, n_kv, max_seq, start_pos;
   int n_rtiles;            // row tiles per kv head
   int nsplit;              // key splits per row tile

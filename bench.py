@@ -232,6 +232,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run 5 device-to-device copies of 512 MiB (a copy kernel of known "
+                         "size, to scale HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the attention path has no "
@@ -240,6 +243,14 @@ def main() -> int:
         return 2
 
     lib = mia.init(0)
+    if args.copy_calibration:
+        nb = 512 << 20
+        src, dst = DeviceBuffer(nb), DeviceBuffer(nb)
+        src.zero()
+        for _ in range(5):
+            check(lib.mia_memcpy_d2d(dst.ptr, src.ptr, nb))
+        check(lib.mia_device_sync())
+        del src, dst
     log("decode: allocating 32 x 32768-slot rings (4 GiB)")
     dec = Decode(lib)
     dec_ms = timed(lib, dec.step, args.steps, args.warmup)

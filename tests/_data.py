@@ -98,3 +98,39 @@ def rope_f64(x: np.ndarray, pos: int, th: np.ndarray, n_vec: int, hd: int) -> np
     y[..., 0] = e * c - o * s
     y[..., 1] = o * c + e * s
     return y.reshape(-1)
+
+
+def check_rotated_k(k16_bits, K_raw, positions, th, n_kv=N_KV, hd=HD, what=""):
+    """fp16 ring keys against the exact rotation: float64 RoPE on the fp32
+    angle fl32(theta_inv*pos).  Bound: half an fp16 ulp (the final rounding)
+    plus 4e-7 x the pair norm (fp32 sin/cos and products; covers results
+    that nearly cancel, where the two sides' libm/ocml ulps show up)."""
+    K_raw = np.asarray(K_raw, np.float32).reshape(len(positions), n_kv * hd)
+    exact = np.stack([rope_f64(K_raw[i], int(p), th, n_kv, hd) for i, p in enumerate(positions)])
+    got = f16_bits_to_f32(k16_bits).astype(np.float64).reshape(exact.shape)
+    pr = K_raw.astype(np.float64).reshape(len(positions), -1, 2)
+    pair_norm = np.repeat(np.sqrt((pr ** 2).sum(-1)), 2, axis=-1)
+    mag = np.maximum(np.abs(exact), np.abs(got)).astype(np.float16)
+    bound = 0.5 * np.spacing(mag).astype(np.float64) + 4e-7 * pair_norm
+    bad = np.abs(got - exact) > bound
+    assert not bad.any(), f"{what}: {int(bad.sum())} rotated keys off the exact rounding"
+
+
+def check_ring(kc_g, kc_o, vc_g, vc_o, written_slots, K_raw=None, positions=None, th=None,
+               what=""):
+    """Ring after a write step: V and every slot outside `written_slots` are
+    bit-exact with the oracle's ring, and the written slots' keys are faithful
+    fp16 roundings of the exact rotation on both sides.  Rotated keys are not
+    compared bit for bit: RoPE's sin/cos come from different libraries (device
+    ocml, host libm, the reference's Accelerate) and an ulp of fp32 can flip
+    the fp16 rounding."""
+    written_slots = np.asarray(written_slots)
+    assert np.array_equal(vc_g, vc_o), f"{what}: V ring differs"
+    diff = kc_g != kc_o
+    rows = np.unique(np.nonzero(diff)[0])
+    assert set(rows.tolist()) <= set(written_slots.tolist()), \
+        f"{what}: unwritten slots changed: {rows[:10]}"
+    if K_raw is not None:
+        check_rotated_k(kc_g[written_slots], K_raw, positions, th, what=what + " (gpu)")
+        check_rotated_k(kc_o[written_slots], K_raw, positions, th, what=what + " (oracle)")
+    return int(diff.sum())

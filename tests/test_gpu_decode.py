@@ -1,8 +1,10 @@
 """GPU parity: S=1 decode attention (split-K flash-decode kernel) against the
 CPU oracle on the same seeded inputs, through the C ABI.
 
-Bar: outputs within max-abs 2e-3 / max-rel 1e-2 of the oracle; the fp16 ring
-after the fused step bit-exact with the oracle's ring."""
+Bar: outputs within max-abs 2e-3 / max-rel 1e-2 of the oracle; after the
+fused step the slot written is pos % max_seq, V and every other slot are
+bit-exact, and the rotated key is a faithful fp16 rounding of the exact
+rotation (the sin/cos library boundary rules out bit equality)."""
 
 import numpy as np
 import pytest
@@ -32,7 +34,7 @@ def test_decode_step_single_layer_repo_cpu_case():
     kc_o, vc_o = kc.copy(), vc.copy()
     ref = O.decode_step(kc_o, vc_o, q, k, v, pos, TH, 32, 8, 128, M)
     D.check_close(out, ref, what="decode_step L=513")
-    assert np.array_equal(kc_g, kc_o) and np.array_equal(vc_g, vc_o)
+    D.check_ring(kc_g, kc_o, vc_g, vc_o, [pos % M], k, [pos], TH, "decode ring")
 
 
 @pytest.mark.parametrize("pos", [0, 1, 62, 63, 64, 255, 256, 257, 300, 512, 1000, 2047, 4096])
@@ -71,7 +73,7 @@ def test_decode_step_long_context_sharp_peaks():
     kc_o, vc_o = kc.copy(), vc.copy()
     ref = O.decode_step(kc_o, vc_o, q, k, v, pos, TH, 32, 8, 128, M)
     D.check_close(out, ref, what="32K spikes")
-    assert np.array_equal(kc_g, kc_o) and np.array_equal(vc_g, vc_o)
+    D.check_ring(kc_g, kc_o, vc_g, vc_o, [pos % M], k, [pos], TH, "decode ring")
 
 
 def test_decode_step_first_token_returns_v():
