@@ -135,8 +135,7 @@ int decode_impl(const float *q, const float *k, const float *v, const float *the
   p.start = (int)start;
   p.new_slot = pos % max_seq;
   p.n_kv = n_kv;
-  p.chunk_rows = mia::decode_pick_chunk_rows(L, n_kv, 3 * c->num_cus);
-  p.nchunk = (L + p.chunk_rows - 1) / p.chunk_rows;
+  p.nchunk = mia::decode_pick_nchunk(L, n_kv, 2 * c->num_cus);
   p.qscale = qscale_log2();
   if (p.nchunk > 1) {
     if (int rc = ensure_scratch(c, mia::decode_scratch_bytes(n_kv, kG, p.nchunk))) return rc;

@@ -9,16 +9,18 @@
 // 8 XCDs every chunk of one kv head (and its partials) stays on one XCD.
 //
 // Each of the 4 waves of a workgroup is an independent pipeline over 16-key
-// tiles (wave w takes tiles w, w+4, ...), double-buffered in registers so that
-// the next tiles' loads are in flight while the current tile is computed:
+// tiles (wave w takes tiles w, w+4, ...), held in a ring of register buffers
+// so that the next tiles' loads are in flight while one tile is computed:
 //   scores  v_mfma_f32_16x16x32_f16: A = 16 key rows straight from the
 //           loads (lane = key row, 64 contiguous bytes), B = the G=4 query
 //           heads of the group with q split into fp16 hi + lo parts along K
 //           (q = hi + lo to ~2^-22), so the scores carry fp32 q accuracy.
-//   softmax wave-local online max / sum in the log2 domain; probabilities go
-//           through 256 B of LDS to the V-lane layout.
-//   P.V     v_fma_mix_f32: a 16-lane row owns 8 dims of 4 keys, every loaded
-//           fp16 V element feeds the 4 heads without a conversion.
+//   softmax wave-local online max / sum in the log2 domain.
+//   P.V     v_mfma_f32_16x16x16_f16 computing O^T = V^T P^T: the score
+//           accumulator layout (lane = 4 keys of one head) is already the B
+//           operand layout with keys along K, so P (fp16 hi + lo) never
+//           leaves its lane; V^T comes from the 4 loaded V rows of the lane
+//           (4 keys x 8 dims) by byte permutes.
 // The 4 wave partials are merged in LDS; chunk partials are merged by a
 // second, small kernel (log-sum-exp merge).
 #include "mia_device.h"
@@ -31,7 +33,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kTile = 16;        // keys per wave tile
-constexpr int kChunkAlign = 64;  // chunk_rows granularity (one tile per wave)
+constexpr int kDepth = 2;        // register tile buffers per wave (3, 4 measured no faster)
 constexpr int kMaxChunks = 256;  // merge capacity per kv head
 constexpr int G = 4;             // query heads per kv head
 
@@ -39,14 +41,13 @@ struct DecodeSmem {
   float2 cs[64];                 // RoPE (cos, sin) for the 64 pair indices
   _Float16 knew[HD];             // rotated fp16 new key of this kv head
   _Float16 vnew[HD];
-  float p[kWaves][16][kTile];    // per-wave tile probabilities [column][key]
   float ml[kWaves][2 * G];       // per-wave (max, sum)
-  float acc[kWaves][4][G][HD];   // per-(wave, row group) partial outputs
+  float acc[kWaves][G][HD];      // per-wave partial outputs
 };
 
 struct TileBuf {
   u4 k[4];  // MFMA A operand, k-step s: key row lane%16, dims 32*s + 8*(lane/16) .. +8
-  u4 v[4];  // P.V operand: keys 4*(lane/16) + m, dims 8*(lane%16) .. +8
+  u4 v[4];  // V rows: keys 4*(lane/16) + m, dims 8*(lane%16) .. +8
 };
 
 // Value of x in lane `src` (uniform result).
@@ -71,8 +72,11 @@ __global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
   const int kvh = blockIdx.x % p.n_kv;
   const int chunk = blockIdx.x / p.n_kv;
   const int kv_dim = p.n_kv * HD;
-  const int c0 = chunk * p.chunk_rows;
-  const int c1 = min(c0 + p.chunk_rows, p.L);
+  // Chunk = tiles [chunk*T/nchunk, (chunk+1)*T/nchunk) of the T 16-key tiles
+  // of the window, so workgroups differ by at most one tile.
+  const long n_tiles = (p.L + kTile - 1) / kTile;
+  const int c0 = (int)((long)chunk * n_tiles / p.nchunk) * kTile;
+  const int c1 = min((int)((long)(chunk + 1) * n_tiles / p.nchunk) * kTile, p.L);
   const bool has_new = FUSED && (c1 == p.L);
 
   // The new token (fused, last chunk) is attended after the loop from its
@@ -105,12 +109,12 @@ __global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
     }
   };
 
-  // First two tiles are requested before the prologue so that their latency
-  // overlaps the RoPE table, the new-token write and the q operand set-up.
-  TileBuf ba, bb;
+  // The first kDepth tiles are requested before the prologue so that their
+  // latency overlaps the RoPE table, the new-token write and the q set-up.
+  TileBuf buf[kDepth];
   if (n_my > 0) {
-    issue(ba, 0);
-    issue(bb, 1);
+#pragma unroll
+    for (int b = 0; b < kDepth; ++b) issue(buf[b], b);
   }
 
   if (FUSED) {
@@ -172,13 +176,13 @@ __global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
 
   // m_run[g]: wave-uniform running max of head g; m_lane: the same value for
   // the head of this lane's MFMA column (lanes with lc >= G carry junk).
-  float m_run[G], m_lane = -INFINITY, l_part = 0.f, acc[G][8];
+  // o[e]: O^T accumulator of MFMA e (dims 8*(4*lg+i) + e, head lc).
+  float m_run[G], m_lane = -INFINITY, l_part = 0.f;
+  f4 o[8];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m_run[g] = -INFINITY;
+  for (int g = 0; g < G; ++g) m_run[g] = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-  }
+  for (int e = 0; e < 8; ++e) o[e] = f4{0.f, 0.f, 0.f, 0.f};
 
   // One 16-key tile starting at key t0; keys >= cend are masked.
   auto process = [&](const TileBuf &b, int t0, int cend) {
@@ -203,53 +207,53 @@ __global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     // every lane of column lc now holds the tile max of head lc
     const float m_lane_new = fmaxf(m_lane, mx);
-    float m_new[G];
     bool grow = false;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      m_new[g] = lane_value(m_lane_new, g);
-      grow |= m_new[g] > m_run[g];
-    }
+    for (int g = 0; g < G; ++g) grow |= lane_value(m_lane_new, g) > m_run[g];
     if (grow) {  // wave-uniform
+      const float alpha = fast_exp2(m_lane - m_lane_new);  // per column (head)
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float alpha = fast_exp2(m_run[g] - m_new[g]);
-        m_run[g] = m_new[g];
+      for (int e = 0; e < 8; ++e) o[e] *= alpha;
+      l_part *= alpha;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] *= alpha;
-      }
-      l_part *= fast_exp2(m_lane - m_lane_new);
+      for (int g = 0; g < G; ++g) m_run[g] = lane_value(m_lane_new, g);
     }
     m_lane = m_lane_new;
-    const float mine = m_lane;
-    f4 pv;
+    // P^T as the B operand of O^T += V^T P^T (k = this lane group's 4 keys,
+    // column = head lc), split into fp16 hi + lo parts.
+    h4 phi, plo;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pv[i] = fast_exp2(sc[i] - mine);
-    if (lc < G) l_part += (pv[0] + pv[1]) + (pv[2] + pv[3]);
-    *reinterpret_cast<f4 *>(&sm.p[w][lc][4 * lg]) = pv;
-    wave_lds_sync();
-    f4 pp[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) pp[g] = *reinterpret_cast<const f4 *>(&sm.p[w][g][4 * lg]);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const h8 vh = __builtin_bit_cast(h8, b.v[m]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float vf = (float)vh[e];
-#pragma unroll
-        for (int g = 0; g < G; ++g) acc[g][e] = __builtin_fmaf(pp[g][m], vf, acc[g][e]);
-      }
+    for (int i = 0; i < 4; ++i) {
+      float pv = lc < G ? fast_exp2(sc[i] - m_lane) : 0.f;
+      l_part += pv;
+      _Float16 h = (_Float16)pv;
+      phi[i] = h;
+      plo[i] = (_Float16)(pv - (float)h);
     }
-    wave_lds_sync();
+    // A operand of MFMA e: V^T rows = dims 8*lc + e, k = keys 4*lg + m, i.e.
+    // element e of the 4 loaded V rows, gathered with byte permutes.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const unsigned a0 = b.v[0][j], a1 = b.v[1][j], a2 = b.v[2][j], a3 = b.v[3][j];
+      u2 lo = {__builtin_amdgcn_perm(a1, a0, 0x05040100u), __builtin_amdgcn_perm(a3, a2, 0x05040100u)};
+      u2 hi = {__builtin_amdgcn_perm(a1, a0, 0x07060302u), __builtin_amdgcn_perm(a3, a2, 0x07060302u)};
+      const h4 ae = __builtin_bit_cast(h4, lo), ao = __builtin_bit_cast(h4, hi);
+      o[2 * j] = __builtin_amdgcn_mfma_f32_16x16x16f16(ae, phi, o[2 * j], 0, 0, 0);
+      o[2 * j] = __builtin_amdgcn_mfma_f32_16x16x16f16(ae, plo, o[2 * j], 0, 0, 0);
+      o[2 * j + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(ao, phi, o[2 * j + 1], 0, 0, 0);
+      o[2 * j + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(ao, plo, o[2 * j + 1], 0, 0, 0);
+    }
   };
 
   if (n_my > 0) {
-    for (int i = 0; i < n_my; i += 2) {
-      process(ba, (first_tile + kWaves * i) * kTile, ce);
-      issue(ba, i + 2);
-      if (i + 1 < n_my) process(bb, (first_tile + kWaves * (i + 1)) * kTile, ce);
-      issue(bb, i + 3);
+    // Ring of kDepth register buffers: tile i+kDepth is requested as soon as
+    // tile i has been consumed, so kDepth-1 tiles stay in flight.
+    for (int i = 0; i < n_my; i += kDepth) {
+#pragma unroll
+      for (int b = 0; b < kDepth; ++b) {
+        if (i + b < n_my) process(buf[b], (first_tile + kWaves * (i + b)) * kTile, ce);
+        issue(buf[b], i + b + kDepth);
+      }
     }
   }
   if (has_new && w == 0) {
@@ -269,11 +273,11 @@ __global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
     sm.ml[w][lane] = m_lane;
     sm.ml[w][G + lane] = l_part;
   }
+  if (lc < G) {
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    f4 *dst = reinterpret_cast<f4 *>(&sm.acc[w][lg][g][8 * lc]);
-    dst[0] = f4{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
-    dst[1] = f4{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sm.acc[w][lc][8 * (4 * lg + i) + e] = o[e][i];
   }
   __syncthreads();
 
@@ -292,9 +296,7 @@ __global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
     for (int ww = 0; ww < kWaves; ++ww) {
       float e = fast_exp2(sm.ml[ww][g] - Mu);
       Ls = __builtin_fmaf(e, sm.ml[ww][G + g], Ls);
-      float s = (sm.acc[ww][0][g][d] + sm.acc[ww][1][g][d]) +
-                (sm.acc[ww][2][g][d] + sm.acc[ww][3][g][d]);
-      O = __builtin_fmaf(e, s, O);
+      O = __builtin_fmaf(e, sm.acc[ww][g][d], O);
     }
     o_val[oi] = O;
     m_wg[oi] = M;
@@ -318,14 +320,19 @@ __global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
   }
 }
 
-// Cross-chunk log-sum-exp merge, one workgroup per (kv head, q head).  A
-// separate launch: the kernel boundary orders the partial writes before these
-// reads, where an in-kernel last-arriver merge would need an agent-scope fence
-// (an L2 write-back) in every workgroup.
-__global__ void __launch_bounds__(HD) decode_merge_kernel(DecodeParams p) {
+// Cross-chunk log-sum-exp merge.  Workgroup = (kv head, q head, 32-dim block);
+// its 256 threads = 8 chunk groups x 32 dims, so each thread sums about
+// nchunk/8 independent partials.  A separate launch: the kernel boundary
+// orders the partial writes before these reads, where an in-kernel
+// last-arriver merge would need an agent-scope fence (an L2 write-back) in
+// every workgroup.
+__global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
   __shared__ float wt[kMaxChunks];
-  __shared__ float inv_l;
-  const int kvh = blockIdx.x / G, g = blockIdx.x % G;
+  __shared__ float red[8][32];
+  __shared__ float stat[2];
+  const int db = blockIdx.x % 4;
+  const int hg = blockIdx.x / 4;  // kvh * G + g
+  const int kvh = hg / G, g = hg % G;
   const int tid = threadIdx.x;
   const size_t hb = (size_t)kvh * p.nchunk * G;
   if (tid < 64) {
@@ -340,22 +347,22 @@ __global__ void __launch_bounds__(HD) decode_merge_kernel(DecodeParams p) {
       Ls = __builtin_fmaf(e, ml.y, Ls);
     }
     Ls = wave_sum(Ls);
-    if (tid == 0) inv_l = 1.0f / Ls;
+    if (tid == 0) stat[0] = 1.0f / Ls;
   }
   __syncthreads();
+  const int cg = tid >> 5, d = 32 * db + (tid & 31);
+  const float *src = p.part_o + (hb + g) * HD + d;
   float O = 0.f;
-  const float *src = p.part_o + (hb + g) * HD + tid;
-  int c = 0;
-  for (; c + 4 <= p.nchunk; c += 4) {
-    float a0 = src[(size_t)(c + 0) * G * HD], a1 = src[(size_t)(c + 1) * G * HD];
-    float a2 = src[(size_t)(c + 2) * G * HD], a3 = src[(size_t)(c + 3) * G * HD];
-    O = __builtin_fmaf(wt[c + 0], a0, O);
-    O = __builtin_fmaf(wt[c + 1], a1, O);
-    O = __builtin_fmaf(wt[c + 2], a2, O);
-    O = __builtin_fmaf(wt[c + 3], a3, O);
+#pragma unroll 4
+  for (int c = cg; c < p.nchunk; c += 8) O = __builtin_fmaf(wt[c], src[(size_t)c * G * HD], O);
+  red[cg][tid & 31] = O;
+  __syncthreads();
+  if (tid < 32) {
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) t += red[k][tid];
+    p.out[(size_t)hg * HD + d] = t * stat[0];
   }
-  for (; c < p.nchunk; ++c) O = __builtin_fmaf(wt[c], src[(size_t)c * G * HD], O);
-  p.out[((size_t)kvh * G + g) * HD + tid] = O * inv_l;
 }
 
 }  // namespace
@@ -364,27 +371,25 @@ size_t decode_scratch_bytes(int n_kv, int g, int nchunk) {
   return (size_t)n_kv * nchunk * g * (HD + 2) * sizeof(float);
 }
 
-int decode_pick_chunk_rows(int L, int n_kv, int target_wgs) {
-  long per = ((long)L * n_kv + target_wgs - 1) / target_wgs;
-  long rows = ((per + kChunkAlign - 1) / kChunkAlign) * kChunkAlign;
-  if (rows < kChunkAlign) rows = kChunkAlign;
-  long nchunk = (L + rows - 1) / rows;
-  while (nchunk > kMaxChunks) {
-    rows += kChunkAlign;
-    nchunk = (L + rows - 1) / rows;
-  }
-  return (int)rows;
+int decode_pick_nchunk(int L, int n_kv, int target_wgs) {
+  const int n_tiles = (L + kTile - 1) / kTile;
+  // at least one tile per wave, at most kMaxChunks chunks
+  int nchunk = (target_wgs + n_kv - 1) / n_kv;
+  if (nchunk > n_tiles / kWaves) nchunk = n_tiles / kWaves;
+  if (nchunk > kMaxChunks) nchunk = kMaxChunks;
+  if (nchunk < 1) nchunk = 1;
+  return nchunk;
 }
 
 hipError_t launch_decode(const DecodeParams &p, int g, bool fused, hipStream_t s) {
   if (g != G) return hipErrorInvalidValue;
-  if (p.nchunk > kMaxChunks || p.chunk_rows % kChunkAlign) return hipErrorInvalidValue;
+  if (p.nchunk < 1 || p.nchunk > kMaxChunks) return hipErrorInvalidValue;
   dim3 grid(p.n_kv * p.nchunk), block(kThreads);
   if (fused)
     hipLaunchKernelGGL(decode_kernel<true>, grid, block, 0, s, p);
   else
     hipLaunchKernelGGL(decode_kernel<false>, grid, block, 0, s, p);
-  if (p.nchunk > 1) hipLaunchKernelGGL(decode_merge_kernel, dim3(p.n_kv * G), dim3(HD), 0, s, p);
+  if (p.nchunk > 1) hipLaunchKernelGGL(decode_merge_kernel, dim3(p.n_kv * G * 4), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

@@ -24,14 +24,13 @@ struct DecodeParams {
   int start;               // slot of the oldest window entry, (pos+1-L) mod M
   int new_slot;            // pos mod M
   int n_kv;
-  int nchunk;              // workgroups per kv head
-  int chunk_rows;          // rows per workgroup (multiple of 64)
+  int nchunk;              // workgroups per kv head (chunks of whole 16-key tiles)
   float qscale;            // (1/sqrt(128)) * log2(e)
 };
 
 // Scratch needed by launch_decode for a given shape (bytes of part_o+part_ml).
 size_t decode_scratch_bytes(int n_kv, int G, int nchunk);
-int decode_pick_chunk_rows(int L, int n_kv, int target_wgs);
+int decode_pick_nchunk(int L, int n_kv, int target_wgs);
 hipError_t launch_decode(const DecodeParams &p, int G, bool fused, hipStream_t s);
 
 // S>=1 causal attention on fp16 MFMA for the queries start_pos..start_pos+S-1.
