@@ -25,7 +25,7 @@ struct DevCtx {
   int num_cus = 256;
   void *scratch = nullptr;  // split-K partials
   size_t scratch_bytes = 0;
-  void *work = nullptr;  // rotated Q + fp16 staging for mia_attention_step
+  void *work = nullptr;  // fp16 draft staging for mia_attention_step
   size_t work_bytes = 0;
 };
 
@@ -146,14 +146,15 @@ int decode_impl(const float *q, const float *k, const float *v, const float *the
   return MIA_OK;
 }
 
-int flash_impl(DevCtx *c, const float *Q, const uint16_t *kst, const uint16_t *vst,
-               const uint16_t *k_layer, const uint16_t *v_layer, float *out, int n_kv, int max_seq,
-               int start_pos, int S, hipStream_t s) {
+int flash_impl(DevCtx *c, const float *Q, const float *theta_inv, const uint16_t *kst,
+               const uint16_t *vst, const uint16_t *k_layer, const uint16_t *v_layer, float *out,
+               int n_kv, int max_seq, int start_pos, int S, hipStream_t s) {
   mia::FlashParams p{};
   int rt = 0;
-  mia::flash_plan(S, n_kv, kG, start_pos, max_seq, 4 * c->num_cus, &p.n_rtiles, &p.nsplit,
+  mia::flash_plan(S, n_kv, kG, start_pos, max_seq, c->num_cus, &p.n_rtiles, &p.nsplit,
                   &p.split_keys, &rt);
   p.Q = Q;
+  p.theta_inv = theta_inv;
   p.kc = reinterpret_cast<const _Float16 *>(k_layer);
   p.vc = reinterpret_cast<const _Float16 *>(v_layer);
   p.kstage = reinterpret_cast<const _Float16 *>(kst);
@@ -388,8 +389,8 @@ int mia_attention_batch(const float *Q, float *out, const uint16_t *k_layer, con
   if (int rc = check_pos(start_pos, S)) return rc;
   DevCtx *c;
   if (int rc = current_ctx(&c)) return rc;
-  return flash_impl(c, Q, nullptr, nullptr, k_layer, v_layer, out, n_kv_heads, max_seq, start_pos,
-                    S, pick_stream(c, stream));
+  return flash_impl(c, Q, nullptr, nullptr, nullptr, k_layer, v_layer, out, n_kv_heads, max_seq,
+                    start_pos, S, pick_stream(c, stream));
 }
 
 int mia_attention_step(const float *Q, const float *K, const float *V, const float *theta_inv,
@@ -406,27 +407,25 @@ int mia_attention_step(const float *Q, const float *K, const float *V, const flo
   if (int rc = current_ctx(&c)) return rc;
   hipStream_t s = pick_stream(c, stream);
   const int kv_dim = n_kv_heads * kHD;
-  const size_t q_bytes = (size_t)S * n_heads * kHD * sizeof(float);
-  const size_t st_bytes = (size_t)S * kv_dim * sizeof(uint16_t);
-  if (int rc = ensure_work(c, q_bytes + 2 * st_bytes)) return rc;
-  float *Qr = reinterpret_cast<float *>(c->work);
-  _Float16 *kst = reinterpret_cast<_Float16 *>(reinterpret_cast<char *>(c->work) + q_bytes);
-  _Float16 *vst = kst + (size_t)S * kv_dim;
-  HIP_TRY(hipMemcpyAsync(Qr, Q, q_bytes, hipMemcpyDeviceToDevice, s));
-  HIP_TRY(mia::launch_rope(Qr, nullptr, S, start_pos, theta_inv, n_heads, 0, s));
   // Drafts may go straight into the ring when no slot they take still holds
   // a position some query of the batch attends (start_pos + S <= max_seq).
+  // Q is rotated inside the attention kernel.
   const bool direct = (long)start_pos + S <= (long)max_seq;
   if (direct) {
     HIP_TRY(mia::launch_rope_to_ring(K, V, theta_inv, S, start_pos, n_kv_heads,
                                      reinterpret_cast<_Float16 *>(k_layer),
                                      reinterpret_cast<_Float16 *>(v_layer), max_seq, s));
-    return flash_impl(c, Qr, nullptr, nullptr, k_layer, v_layer, out, n_kv_heads, max_seq,
-                      start_pos, S, s);
+    return flash_impl(c, Q, theta_inv, nullptr, nullptr, k_layer, v_layer, out, n_kv_heads,
+                      max_seq, start_pos, S, s);
   }
+  const size_t st_bytes = (size_t)S * kv_dim * sizeof(uint16_t);
+  if (int rc = ensure_work(c, 2 * st_bytes)) return rc;
+  _Float16 *kst = reinterpret_cast<_Float16 *>(c->work);
+  _Float16 *vst = kst + (size_t)S * kv_dim;
   HIP_TRY(mia::launch_rope_to_f16(K, V, theta_inv, S, start_pos, n_kv_heads, kst, vst, s));
-  if (int rc = flash_impl(c, Qr, reinterpret_cast<uint16_t *>(kst), reinterpret_cast<uint16_t *>(vst),
-                          k_layer, v_layer, out, n_kv_heads, max_seq, start_pos, S, s))
+  if (int rc = flash_impl(c, Q, theta_inv, reinterpret_cast<uint16_t *>(kst),
+                          reinterpret_cast<uint16_t *>(vst), k_layer, v_layer, out, n_kv_heads,
+                          max_seq, start_pos, S, s))
     return rc;
   HIP_TRY(mia::launch_commit(reinterpret_cast<_Float16 *>(k_layer),
                              reinterpret_cast<_Float16 *>(v_layer), kst, vst, S, start_pos, max_seq,

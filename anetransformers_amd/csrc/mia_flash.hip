@@ -3,22 +3,27 @@
 // Replaces mistral/mistral_ane_prefill.h:207-275 (attention_batch) and, with
 // staged drafts, the sequential verify of mistral/speculative.h:92-101.
 //
-// Rows of a tile are (query t, head g) pairs of one kv head, row = t*G + g, so
-// the G query heads of a group share every K/V tile.  One wave owns 32 rows.
-// Per 64-key tile (staged in LDS):
-//   S^T[key][row] = K . Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS,
-//                             B = Q^T held in registers for the whole loop
+// Rows are (query t, head g) pairs of one kv head, row = t*G + g, so the G
+// query heads of a group share every K/V tile.  A workgroup holds SL row slabs
+// of 32 rows and KH key groups; wave w works on slab w % SL over the key range
+// of group w / SL, and the KH partial results are merged in LDS at the end.
+// Per 32-key tile (double-buffered in LDS per key group):
+//   S^T[key][row] = K . Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS
+//                             (ds_read_b128), B = Q^T held in registers
 //   online softmax per row    each lane owns one row (the D column), so the
-//                             running max/sum/rescale stay lane-local
-//   O^T[dim][row] += V^T . P^T  P^T feeds the B operand straight from the
-//                             S^T accumulator layout (same key permutation on
-//                             both operands); V^T is gathered from LDS.
+//                             running max / sum / rescale stay lane-local
+//   O^T[dim][row] += V^T . P^T  P^T is the B operand straight from the S^T
+//                             accumulator (same key permutation on both
+//                             operands); V^T comes from the row-major V tile
+//                             by the transposing LDS read ds_read_b64_tr_b16.
 // Query t at position start+t attends the window [pos-L+1, pos], L =
 // min(pos+1, max_seq) (mistral_ane_prefill.h:220-241); positions >= start come
 // from the staging buffer when one is given, which keeps the ring untouched
 // until the caller commits (sequential-verify semantics on a wrapped ring).
-// Key ranges are split over workgroups; a second kernel merges the partials
-// (log-sum-exp).
+// With p.theta_inv set, the adjacent-pair RoPE of Q (mistral_model.h:79-122)
+// is applied while the Q operand is built.  Masks are applied only to tiles
+// that cross a window edge of the slab.  Very long key ranges over few rows
+// are additionally split over workgroups and merged by a second kernel.
 #include "mia_device.h"
 #include "mia_kernels.h"
 
@@ -26,12 +31,19 @@ namespace mia {
 
 namespace {
 
-constexpr int kKeys = 64;                // keys per LDS tile
-constexpr int kPitch = HD + 8;           // LDS row pitch in halfs (272 B)
+constexpr int kKT = 32;         // keys per tile
+constexpr int kPitch = HD + 8;  // LDS row pitch in halfs (272 B)
 
-struct FlashSmem {
-  _Float16 k[kKeys][kPitch];
-  _Float16 v[kKeys][kPitch];
+template <int SL, int KH>
+struct FlashLayout {
+  static constexpr int kTileHalfs = kKT * kPitch;
+  // [KH][2 buffers][K, V] tiles
+  static constexpr size_t kTiles = (size_t)KH * 2 * 2 * kTileHalfs * sizeof(_Float16);
+  static constexpr size_t kRope = (size_t)8 * SL * 64 * sizeof(float2);
+  // after the loop the tile area holds [KH][SL][32 rows][HD] partial outputs
+  // and [KH][SL][32][2] (max, sum)
+  static constexpr size_t kMerge = (size_t)KH * SL * 32 * (HD + 2) * sizeof(float);
+  static constexpr size_t kBytes = (kTiles > kMerge ? kTiles : kMerge) + kRope;
 };
 
 __device__ __forceinline__ int window_lo(int pos, int max_seq) {
@@ -39,15 +51,40 @@ __device__ __forceinline__ int window_lo(int pos, int max_seq) {
   return pos + 1 > max_seq ? pos + 1 - max_seq : 0;
 }
 
-template <int G, int NW>
-__global__ void __launch_bounds__(64 * NW) flash_kernel(FlashParams p) {
-  constexpr int RT = 32 * NW;  // rows per tile
-  constexpr int NT = 64 * NW;
-  __shared__ FlashSmem sm;
+typedef short s4 __attribute__((ext_vector_type(4)));
+// LDS (address space 3) pointers: 32-bit addressing, no generic-pointer checks.
+typedef __attribute__((address_space(3))) _Float16 lds_half;
+typedef __attribute__((address_space(3))) s4 lds_s4;
+typedef __attribute__((address_space(3))) h8 lds_h8;
+typedef __attribute__((address_space(3))) u4 lds_u4;
+
+// Four consecutive keys k0..k0+3 of dim d0 + (lane % 16) from a row-major
+// [key][kPitch] fp16 tile: input lane i of each 16-lane group points at
+// (k0 + i/4, d0 + 4*(i%4)); the transposing read returns, in output lane j,
+// elements (k0 + e, d0 + j) for e = 0..3.
+__device__ __forceinline__ h4 read_vt4(lds_half *tile, int k0, int d0, int lane) {
+  const int i = lane & 15;
+  lds_half *src = tile + (k0 + (i >> 2)) * kPitch + d0 + 4 * (i & 3);
+  s4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)src);
+  return __builtin_bit_cast(h4, r);
+}
+
+template <int G, int SL, int KH>
+__global__ void __launch_bounds__(64 * SL * KH) flash_kernel(FlashParams p) {
+  using Lay = FlashLayout<SL, KH>;
+  constexpr int NW = SL * KH;
+  constexpr int RT = 32 * SL;     // rows per workgroup
+  constexpr int QT = RT / G;      // queries per workgroup
+  constexpr int LT = 64 * SL;     // threads per key group
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  lds_half *tiles = (lds_half *)smem;
+  float2 *rope = reinterpret_cast<float2 *>(smem + (Lay::kBytes - Lay::kRope));
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
+  const int slab = w % SL;
+  const int kg = w / SL;
   const int half = lane >> 5;
   const int col = lane & 31;
   const int kvh = blockIdx.x % p.n_kv;
@@ -57,37 +94,134 @@ __global__ void __launch_bounds__(64 * NW) flash_kernel(FlashParams p) {
   const int kv_dim = p.n_kv * HD;
   const int dim_model = p.n_kv * G * HD;
 
-  // This lane's row.
+  // This lane's row and its window.
   const int row0 = rtile * RT;
-  const int row = row0 + w * 32 + col;
+  const int row = row0 + slab * 32 + col;
   const int t = row / G;
   const int g = row % G;
   const bool row_valid = t < p.S;
   const int pos_t = p.start_pos + (row_valid ? t : p.S - 1);
   const int lo_t = window_lo(pos_t, p.max_seq);
   const int hi_t = pos_t;
+  // Slab-uniform bounds: keys in [lo_max, hi_min] are inside every row's window.
+  const int ts0 = (row0 + slab * 32) / G;
+  const int ts1 = (row0 + slab * 32 + 31) / G;
+  const bool slab_full = ts1 < p.S;
+  const int lo_max = window_lo(p.start_pos + min(ts1, p.S - 1), p.max_seq);
+  const int hi_min = p.start_pos + ts0;
 
-  // Key range of the tile and of this split.
-  const int t0 = row0 / G;
-  const int t1 = min((row0 + RT - 1) / G, p.S - 1);
-  const int klo = window_lo(p.start_pos + t0, p.max_seq);
-  const int khi = p.start_pos + t1;
+  // Key range of the workgroup (one split), then of this key group.
+  const int tq0 = row0 / G;
+  const int tq1 = min((row0 + RT - 1) / G, p.S - 1);
+  const int klo = window_lo(p.start_pos + tq0, p.max_seq);
+  const int khi = p.start_pos + tq1;
   const int ks = klo + split * p.split_keys;
   const int ke = min(ks + p.split_keys, khi + 1);
+  const int nt = ke > ks ? (ke - ks + kKT - 1) / kKT : 0;
+  const int g_first = (int)((long)kg * nt / KH);
+  const int g_count = (int)((long)(kg + 1) * nt / KH) - g_first;
+  const int n_iter = (nt + KH - 1) / KH;
 
-  // Q^T operand: col = row, k = dims 16*st + 8*half .. +8, scaled, fp16.
+  // RoPE (cos, sin) for the workgroup's queries, fl32(theta_inv[i] * pos) as
+  // vDSP_vsmul (mistral_model.h:87-88).
+  if (p.theta_inv != nullptr) {
+    for (int i = tid; i < QT * 64; i += 64 * NW) {
+      const int qi = i >> 6, pr = i & 63;
+      const int tq = min(tq0 + qi, p.S - 1);
+      float ang = p.theta_inv[pr] * (float)(p.start_pos + tq);
+      float sn, cs;
+      sincosf(ang, &sn, &cs);
+      rope[i] = make_float2(cs, sn);
+    }
+    __syncthreads();
+  }
+
+  // Q^T operand: col = row, k-step st covers dims 16*st + 8*half .. +8.
   h8 qb[8];
   {
     const float *qsrc = p.Q + (size_t)(row_valid ? t : 0) * dim_model + (size_t)(kvh * G + g) * HD;
+    const float2 *rt = rope + (row_valid ? t - tq0 : 0) * 64;
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
       const f4 *src = reinterpret_cast<const f4 *>(qsrc + 16 * st + 8 * half);
       f4 a = src[0], b = src[1];
       float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      if (p.theta_inv != nullptr) {
+#pragma unroll
+        for (int pi = 0; pi < 4; ++pi) {
+          float2 cs = rt[8 * st + 4 * half + pi];
+          rope_pair(v[2 * pi], v[2 * pi + 1], cs.x, cs.y);
+        }
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) qb[st][e] = (_Float16)(row_valid ? v[e] * p.qscale : 0.f);
     }
   }
+
+  // Tile loading by the LT threads of this key group: 32 keys x 16 chunks of
+  // 16 B per tensor.
+  constexpr int CPT = kKT * 16 / LT;  // chunks per thread per tensor
+  const int lt = slab * 64 + lane;
+  lds_half *ktile[2], *vtile[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    ktile[b] = tiles + ((size_t)(kg * 2 + b) * 2 + 0) * Lay::kTileHalfs;
+    vtile[b] = tiles + ((size_t)(kg * 2 + b) * 2 + 1) * Lay::kTileHalfs;
+  }
+  u4 rk[CPT], rv[CPT];
+  // Lane offsets inside a tile are loop invariant; the tile base is uniform.
+  int lane_off[CPT], lane_row[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int ch = lt + c * LT;
+    lane_row[c] = ch >> 4;
+    lane_off[c] = (ch >> 4) * kv_dim + kvh * HD + 8 * (ch & 15);
+  }
+  auto gload = [&](int tile_idx) {
+    const int kb = ks + kKT * tile_idx;
+    const bool full = kb + kKT <= ke;
+    const int slot0 = kb % p.max_seq;  // uniform, once per tile
+    const bool contiguous = full && slot0 + kKT <= p.max_seq &&
+                            (p.kstage == nullptr || kb + kKT <= p.start_pos);
+    if (contiguous) {  // wave-uniform fast path: all 32 keys in consecutive ring slots
+      const _Float16 *kt = p.kc + (size_t)slot0 * kv_dim;
+      const _Float16 *vt = p.vc + (size_t)slot0 * kv_dim;
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        rk[c] = *reinterpret_cast<const u4 *>(kt + lane_off[c]);
+        rv[c] = *reinterpret_cast<const u4 *>(vt + lane_off[c]);
+      }
+      return;
+    }
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int kp = min(kb + lane_row[c], ke - 1);
+      const int in_tile = lane_off[c] - lane_row[c] * kv_dim;
+      const _Float16 *ksrc, *vsrc;
+      if (p.kstage != nullptr && kp >= p.start_pos) {
+        size_t off = (size_t)(kp - p.start_pos) * kv_dim + in_tile;
+        ksrc = p.kstage + off;
+        vsrc = p.vstage + off;
+      } else {
+        int slot = slot0 + (kp - kb);
+        slot = slot >= p.max_seq ? slot - p.max_seq : slot;
+        size_t off = (size_t)slot * kv_dim + in_tile;
+        ksrc = p.kc + off;
+        vsrc = p.vc + off;
+      }
+      rk[c] = *reinterpret_cast<const u4 *>(ksrc);
+      rv[c] = *reinterpret_cast<const u4 *>(vsrc);
+    }
+  };
+  auto lstore = [&](int b) {
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int ch = lt + c * LT;
+      const int kr = ch >> 4, cc = ch & 15;
+      *(lds_u4 *)(ktile[b] + kr * kPitch + 8 * cc) = rk[c];
+      *(lds_u4 *)(vtile[b] + kr * kPitch + 8 * cc) = rv[c];
+    }
+  };
 
   f16v o[4];
 #pragma unroll
@@ -96,128 +230,141 @@ __global__ void __launch_bounds__(64 * NW) flash_kernel(FlashParams p) {
     for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  for (int kb = ks; kb < ke; kb += kKeys) {
-    // Cooperative K/V tile load: 64 keys x 16 chunks of 16 B per tensor.
-    for (int c = tid; c < kKeys * 16; c += NT) {
-      const int kr = c >> 4, cc = c & 15;
-      const int kp = min(kb + kr, ke - 1);  // absolute key position (clamped)
-      const _Float16 *ksrc;
-      const _Float16 *vsrc;
-      if (p.kstage != nullptr && kp >= p.start_pos) {
-        size_t off = (size_t)(kp - p.start_pos) * kv_dim + (size_t)kvh * HD + 8 * cc;
-        ksrc = p.kstage + off;
-        vsrc = p.vstage + off;
-      } else {
-        int slot = kp % p.max_seq;
-        size_t off = (size_t)slot * kv_dim + (size_t)kvh * HD + 8 * cc;
-        ksrc = p.kc + off;
-        vsrc = p.vc + off;
-      }
-      *reinterpret_cast<u4 *>(&sm.k[kr][8 * cc]) = *reinterpret_cast<const u4 *>(ksrc);
-      *reinterpret_cast<u4 *>(&sm.v[kr][8 * cc]) = *reinterpret_cast<const u4 *>(vsrc);
-    }
-    __syncthreads();
+  if (g_count > 0) {
+    gload(g_first);
+    lstore(0);
+  }
+  __syncthreads();
 
-    // S^T for two 32-key blocks.
-    f16v s[2];
+  for (int it = 0; it < n_iter; ++it) {
+    const bool more = it + 1 < g_count;
+    if (more) gload(g_first + it + 1);
+    if (it < g_count) {
+      const int b = it & 1;
+      const int kb = ks + kKT * (g_first + it);
+      // S^T block: keys kb..kb+31 x this slab's 32 rows.
+      f16v s;
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[kb2][i] = 0.f;
+      for (int i = 0; i < 16; ++i) s[i] = 0.f;
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
-        h8 a = *reinterpret_cast<const h8 *>(&sm.k[32 * kb2 + col][16 * st + 8 * half]);
-        s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[st], s[kb2], 0, 0, 0);
+        h8 a = *(lds_h8 *)(ktile[b] + col * kPitch + 16 * st + 8 * half);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[st], s, 0, 0, 0);
       }
-    }
-
-    // Mask + online softmax (lane-local row state).
-    float mloc = -INFINITY;
+      // s[i]: key kb + (i/4)*8 + 4*half + (i%4) for row `row`.
+      const bool inside = slab_full && kb >= lo_max && kb + kKT - 1 <= hi_min && kb + kKT <= ke;
+      if (!inside) {
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2)
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb + (i >> 2) * 8 + 4 * half + (i & 3);
+          const bool ok = row_valid && key >= lo_t && key <= hi_t && key < ke;
+          s[i] = ok ? s[i] : -INFINITY;
+        }
+      }
+      float mloc = s[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, s[i]);
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+      // Lazy rescale: m_run is the reference max of the row's exponentials and
+      // moves only when a score exceeds it by more than 8 (log2 domain), so
+      // every p = 2^(s - m_run) stays <= 256 (exact range for fp16) and the
+      // accumulators are rescaled rarely.  Normalisation by l at the end is
+      // unaffected by the choice of reference.
+      const bool move = mloc > m_run + 8.0f;
+      if (__ballot(move) != 0) {  // wave-uniform
+        // rows that do not move keep alpha = 1 (also while still fully masked,
+        // m_run = -inf); the first move of a row gives alpha = 0
+        const float alpha = move ? fast_exp2(m_run - mloc) : 1.0f;
+        const float m_ref = move ? mloc : m_run;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+        m_run = m_ref;
+      }
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+      h8 pb[2];  // P^T B operands for keys 0..15 and 16..31 of the tile
+      float lsum = 0.f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int key = kb + 32 * kb2 + (i >> 2) * 8 + 4 * half + (i & 3);
-        const bool ok = row_valid && key >= lo_t && key <= hi_t && key < ke;
-        s[kb2][i] = ok ? s[kb2][i] : -INFINITY;
-        mloc = fmaxf(mloc, s[kb2][i]);
-      }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-    const float m_new = fmaxf(m_run, mloc);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = fast_exp2(m_run - m_use);
-    float lsum = 0.f;
-    h8 pb[4];  // P^T B operands: 2 blocks x 2 k-steps
-#pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float pv = fast_exp2(s[kb2][i] - m_use);
+        const float pv = fast_exp2(s[i] - m_use);
         lsum += pv;
-        pb[kb2 * 2 + (i >> 3)][i & 7] = (_Float16)pv;
+        pb[i >> 3][i & 7] = (_Float16)pv;
       }
-    l_run = l_run * alpha + lsum;
-    m_run = m_new;
+      l_run += lsum;
+      // O^T += V^T P^T; k-step ks covers keys 16*ks .. +16, this half's 8 keys
+      // being {0-3, 8-11} + 4*half (the S^T row permutation).
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+      for (int kst = 0; kst < 2; ++kst) {
+        const int k0 = 16 * kst + 4 * half;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-
-    // O^T += V^T P^T.  k-step ks4 covers keys 16*ks4 .. +16; this half's 8
-    // keys are {0-3, 8-11} + 4*half within it (the S^T row permutation).
-#pragma unroll
-    for (int ks4 = 0; ks4 < 4; ++ks4) {
-      const int kbase = 16 * ks4 + 4 * half;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const int dim = 32 * db + col;
-        h8 a;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) a[e] = sm.v[kbase + (e >> 2) * 8 + (e & 3)][dim];
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[ks4], o[db], 0, 0, 0);
+        for (int db = 0; db < 4; ++db) {
+          const int d0 = 32 * db + 16 * ((lane >> 4) & 1);
+          h4 lo = read_vt4(vtile[b], k0, d0, lane);
+          h4 hi = read_vt4(vtile[b], k0 + 8, d0, lane);
+          h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[kst], o[db], 0, 0, 0);
+        }
       }
     }
+    if (more) lstore((it + 1) & 1);
     __syncthreads();
   }
 
+  // Merge the KH key groups (LDS; the tile area is free after the loop).
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  // O^T layout: lane holds row `row` (column of D) and dims
-  // 32*db + (i/4)*8 + 4*half + (i%4).
-  if (p.nsplit == 1) {
-    if (row_valid) {
-      float *dst = p.out + (size_t)t * dim_model + (size_t)(kvh * G + g) * HD;
-      const float inv = 1.0f / l_tot;
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          f4 v = {o[db][4 * i4 + 0] * inv, o[db][4 * i4 + 1] * inv, o[db][4 * i4 + 2] * inv,
-                  o[db][4 * i4 + 3] * inv};
-          *reinterpret_cast<f4 *>(dst + 32 * db + 8 * i4 + 4 * half) = v;
-        }
-    }
-    return;
-  }
-
-  // Split partials: [tile][split][RT][128] and [tile][split][RT] (m, l).
-  const size_t tile_id = (size_t)kvh * p.n_rtiles + rtile;
-  const size_t pb_idx = (tile_id * p.nsplit + split) * RT + (w * 32 + col);
+  float *mo = reinterpret_cast<float *>(smem);             // [KH][SL][32][HD]
+  float *mml = mo + (size_t)KH * SL * 32 * HD;              // [KH][SL][32][2]
   {
-    float *dst = p.part_o + pb_idx * HD;
+    float *dst = mo + ((size_t)(kg * SL + slab) * 32 + col) * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        f4 v = {o[db][4 * i4 + 0], o[db][4 * i4 + 1], o[db][4 * i4 + 2], o[db][4 * i4 + 3]};
-        *reinterpret_cast<f4 *>(dst + 32 * db + 8 * i4 + 4 * half) = v;
-      }
+      for (int i4 = 0; i4 < 4; ++i4)
+        *reinterpret_cast<f4 *>(dst + 32 * db + 8 * i4 + 4 * half) =
+            f4{o[db][4 * i4 + 0], o[db][4 * i4 + 1], o[db][4 * i4 + 2], o[db][4 * i4 + 3]};
     if (half == 0)
-      *reinterpret_cast<float2 *>(p.part_ml + pb_idx * 2) = make_float2(m_run, l_tot);
+      *reinterpret_cast<float2 *>(mml + ((size_t)(kg * SL + slab) * 32 + col) * 2) =
+          make_float2(m_run, l_tot);
+  }
+  __syncthreads();
+
+  // Thread -> (row, 4 dims) items of the workgroup's RT rows.
+  const size_t tile_id = (size_t)kvh * p.n_rtiles + rtile;
+  for (int itm = tid; itm < RT * (HD / 4); itm += 64 * NW) {
+    const int rl = itm / (HD / 4), d4 = itm % (HD / 4);
+    const int sl = rl / 32, rr = rl % 32;
+    const int rrow = row0 + rl;
+    const int tt = rrow / G, gg = rrow % G;
+    if (tt >= p.S) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < KH; ++k) M = fmaxf(M, mml[((size_t)(k * SL + sl) * 32 + rr) * 2]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float Ls = 0.f;
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < KH; ++k) {
+      const size_t r = (size_t)(k * SL + sl) * 32 + rr;
+      const float2 ml = *reinterpret_cast<const float2 *>(mml + r * 2);
+      const float e = fast_exp2(ml.x - Mu);
+      Ls = __builtin_fmaf(e, ml.y, Ls);
+      acc += e * *reinterpret_cast<const f4 *>(mo + r * HD + 4 * d4);
+    }
+    if (p.nsplit == 1) {
+      *reinterpret_cast<f4 *>(p.out + (size_t)tt * dim_model + (size_t)(kvh * G + gg) * HD +
+                              4 * d4) = acc * (1.0f / Ls);
+    } else {
+      const size_t pidx = (tile_id * p.nsplit + split) * RT + rl;
+      *reinterpret_cast<f4 *>(p.part_o + pidx * HD + 4 * d4) = acc;
+      if (d4 == 0) *reinterpret_cast<float2 *>(p.part_ml + pidx * 2) = make_float2(M, Ls);
+    }
   }
 }
 
-// Split-K merge: one workgroup per 8 rows of a tile, thread = (row, 4 dims).
-// A separate launch, so the kernel boundary orders the partial writes before
+// Split merge: one workgroup per 8 rows of a tile, thread = (row, 4 dims).  A
+// separate launch, so the kernel boundary orders the partial writes before
 // these reads (no agent-scope fence in the attention kernel).
 template <int G>
 __global__ void __launch_bounds__(256) flash_merge_kernel(FlashParams p, int rt) {
@@ -234,18 +381,33 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(FlashParams p, int rt)
   float M = -INFINITY;
   for (int sp = 0; sp < p.nsplit; ++sp)
     M = fmaxf(M, p.part_ml[(((size_t)tile_id * p.nsplit + sp) * rt + rl) * 2]);
+  const float Mu = M == -INFINITY ? 0.f : M;
   float Ls = 0.f;
   f4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int sp = 0; sp < p.nsplit; ++sp) {
     const size_t idx = ((size_t)tile_id * p.nsplit + sp) * rt + rl;
     float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + idx * 2);
-    float e = fast_exp2(ml.x - M);
+    float e = fast_exp2(ml.x - Mu);
     Ls = __builtin_fmaf(e, ml.y, Ls);
-    f4 v = *reinterpret_cast<const f4 *>(p.part_o + idx * HD + 4 * d4);
-    acc += e * v;
+    acc += e * *reinterpret_cast<const f4 *>(p.part_o + idx * HD + 4 * d4);
   }
   *reinterpret_cast<f4 *>(p.out + (size_t)t * dim_model + (size_t)(kvh * G + g) * HD + 4 * d4) =
       acc * (1.0f / Ls);
+}
+
+template <int SL, int KH>
+hipError_t launch_variant(const FlashParams &p, hipStream_t s) {
+  using Lay = FlashLayout<SL, KH>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void *)flash_kernel<4, SL, KH>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)Lay::kBytes);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  dim3 grid(p.n_kv * p.n_rtiles * p.nsplit);
+  hipLaunchKernelGGL((flash_kernel<4, SL, KH>), grid, dim3(64 * SL * KH), Lay::kBytes, s, p);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -254,12 +416,15 @@ size_t flash_scratch_bytes(int n_kv, int n_rtiles, int nsplit, int rows_per_tile
   return (size_t)n_kv * n_rtiles * nsplit * rows_per_tile * (HD + 2) * sizeof(float);
 }
 
+// Few rows (S*G <= 32, e.g. speculative verify): one slab, 4 key groups, and
+// key splits over workgroups until about target_wgs workgroups.  Otherwise
+// (prefill): two slabs (64 rows) and 4 key groups per workgroup, no split
+// unless the row tiles alone leave the device mostly idle.
 void flash_plan(int S, int n_kv, int G, int start_pos, int max_seq, int target_wgs, int *n_rtiles,
                 int *nsplit, int *split_keys, int *rows_per_tile) {
   const int rows = S * G;
-  const int rt = rows <= 32 ? 32 : 128;
+  const int rt = rows <= 32 ? 32 : 64;
   const int ntiles = (rows + rt - 1) / rt;
-  // Widest key range over the tiles (the last tile reaches the furthest).
   long maxkeys = 0;
   for (int ti = 0; ti < ntiles; ++ti) {
     int t0 = (ti * rt) / G;
@@ -270,11 +435,13 @@ void flash_plan(int S, int n_kv, int G, int start_pos, int max_seq, int target_w
     long hi = (long)start_pos + t1;
     if (hi - lo + 1 > maxkeys) maxkeys = hi - lo + 1;
   }
-  long want_splits = (target_wgs + (long)n_kv * ntiles - 1) / ((long)n_kv * ntiles);
-  if (want_splits < 1) want_splits = 1;
-  long sk = (maxkeys + want_splits - 1) / want_splits;
-  sk = ((sk + kKeys - 1) / kKeys) * kKeys;
-  if (sk < 256) sk = 256;
+  long want = (long)target_wgs / ((long)n_kv * ntiles);
+  if (want < 1) want = 1;
+  // at least 4 tiles of 32 keys per key group and split
+  long max_split = maxkeys / (4L * 4 * kKT);
+  if (want > max_split) want = max_split > 0 ? max_split : 1;
+  long sk = (maxkeys + want - 1) / want;
+  sk = ((sk + kKT - 1) / kKT) * kKT;
   long ns = (maxkeys + sk - 1) / sk;
   if (ns < 1) ns = 1;
   *n_rtiles = ntiles;
@@ -286,13 +453,10 @@ void flash_plan(int S, int n_kv, int G, int start_pos, int max_seq, int target_w
 hipError_t launch_flash(const FlashParams &p, int G, hipStream_t s, int *rows_per_tile_out) {
   if (G != 4) return hipErrorInvalidValue;
   const int rows = p.S * G;
-  const int rt = rows <= 32 ? 32 : 128;
+  const int rt = rows <= 32 ? 32 : 64;
   if (rows_per_tile_out) *rows_per_tile_out = rt;
-  dim3 grid(p.n_kv * p.n_rtiles * p.nsplit);
-  if (rt == 32)
-    hipLaunchKernelGGL((flash_kernel<4, 1>), grid, dim3(64), 0, s, p);
-  else
-    hipLaunchKernelGGL((flash_kernel<4, 4>), grid, dim3(256), 0, s, p);
+  hipError_t e = rt == 32 ? launch_variant<1, 4>(p, s) : launch_variant<2, 4>(p, s);
+  if (e != hipSuccess) return e;
   if (p.nsplit > 1)
     hipLaunchKernelGGL((flash_merge_kernel<4>), dim3(p.n_kv * p.n_rtiles * (rt / 8)), dim3(256), 0,
                        s, p, rt);

@@ -35,7 +35,8 @@ hipError_t launch_decode(const DecodeParams &p, int G, bool fused, hipStream_t s
 
 // S>=1 causal attention on fp16 MFMA for the queries start_pos..start_pos+S-1.
 struct FlashParams {
-  const float *Q;          // [S][n_heads*128] fp32, rotated (scale applied in-kernel)
+  const float *Q;          // [S][n_heads*128] fp32 (scale applied in-kernel)
+  const float *theta_inv;  // [64]: apply RoPE to Q in-kernel; nullptr: Q already rotated
   const _Float16 *kc;      // layer base [max_seq][kv_dim]
   const _Float16 *vc;
   const _Float16 *kstage;  // [S][kv_dim] staged new keys (nullptr: all keys in ring)

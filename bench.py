@@ -232,6 +232,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--skip-decode", action="store_true", help="prefill only (profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 5 device-to-device copies of 512 MiB (a copy kernel of known "
                          "size, to scale HBM byte counters)")
@@ -251,14 +252,16 @@ def main() -> int:
             check(lib.mia_memcpy_d2d(dst.ptr, src.ptr, nb))
         check(lib.mia_device_sync())
         del src, dst
-    log("decode: allocating 32 x 32768-slot rings (4 GiB)")
-    dec = Decode(lib)
-    dec_ms = timed(lib, dec.step, args.steps, args.warmup)
+    dec_ms = float("nan")
+    if not args.skip_decode:
+        log("decode: allocating 32 x 32768-slot rings (4 GiB)")
+        dec = Decode(lib)
+        dec_ms = timed(lib, dec.step, args.steps, args.warmup)
+        del dec
     launch_ms = dec_ms / N_LAYERS
     achieved = DECODE_BYTES_PER_LAYER / (launch_ms * 1e-3) / 1e9
     value = N_LAYERS * DECODE_BYTES_PER_LAYER / (dec_ms * 1e-3) / 1e9
     log(f"decode: {dec_ms:.3f} ms/step, {value:.1f} GB/s")
-    del dec
 
     prefill = None
     if not args.skip_prefill:
