@@ -87,6 +87,8 @@ _SIGS = {
     "mia_event_destroy": (c_int, [_P]),
     "mia_event_record": (c_int, [_P, _P]),
     "mia_event_elapsed_ms": (c_int, [POINTER(c_float), _P, _P]),
+    "mia_profile_begin": (c_int, []),
+    "mia_profile_end": (c_int, [c_int, POINTER(c_int), POINTER(ctypes.c_double)]),
     "mia_fill_normal_f16": (c_int, [_P, c_size_t, c_uint64, _P]),
     "mia_scale_rows_f16": (c_int, [_P, c_long, c_int, c_int, c_int, c_float, _P]),
     # hot path

@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <vector>
 
 #include "../../include/miattn.h"
 #include "mia_kernels.h"
@@ -27,6 +28,11 @@ struct DevCtx {
   size_t scratch_bytes = 0;
   void *work = nullptr;  // fp16 draft staging for mia_attention_step
   size_t work_bytes = 0;
+  // Opt-in kernel timing: an event pair around the main attention kernel of
+  // each call (kind 0 = decode kernel, 1 = flash kernel).
+  bool prof_on = false;
+  std::vector<hipEvent_t> prof_ev[2];
+  size_t prof_n[2] = {0, 0};
 };
 
 DevCtx g_ctx[kMaxDevices];
@@ -114,6 +120,24 @@ int check_pos(int pos, int S) {
 
 float qscale_log2() { return (1.0f / sqrtf((float)kHD)) * 1.4426950408889634f; }
 
+// When timing is on, hands out the next event pair of this kind (created on
+// demand); the launch stamps them at the main kernel's start and end.
+int prof_pair(DevCtx *c, int kind, hipEvent_t *ev0, hipEvent_t *ev1) {
+  *ev0 = *ev1 = nullptr;
+  if (!c->prof_on) return MIA_OK;
+  std::vector<hipEvent_t> &ev = c->prof_ev[kind];
+  size_t idx = 2 * c->prof_n[kind];
+  while (ev.size() < idx + 2) {
+    hipEvent_t e;
+    HIP_TRY(hipEventCreate(&e));
+    ev.push_back(e);
+  }
+  *ev0 = ev[idx];
+  *ev1 = ev[idx + 1];
+  c->prof_n[kind]++;
+  return MIA_OK;
+}
+
 int decode_impl(const float *q, const float *k, const float *v, const float *theta_inv,
                 uint16_t *k_layer, uint16_t *v_layer, float *out, int n_heads, int n_kv, int max_seq,
                 int pos, bool fused, void *stream) {
@@ -142,7 +166,11 @@ int decode_impl(const float *q, const float *k, const float *v, const float *the
     p.part_o = reinterpret_cast<float *>(c->scratch);
     p.part_ml = p.part_o + (size_t)n_kv * p.nchunk * kG * kHD;
   }
-  HIP_TRY(mia::launch_decode(p, kG, fused, pick_stream(c, stream)));
+  hipStream_t s = pick_stream(c, stream);
+  hipEvent_t ev0, ev1;
+  if (int rc = prof_pair(c, 0, &ev0, &ev1)) return rc;
+  HIP_TRY(mia::launch_decode(p, kG, fused, s, ev0, ev1));
+  HIP_TRY(mia::launch_decode_merge(p, s));
   return MIA_OK;
 }
 
@@ -172,7 +200,10 @@ int flash_impl(DevCtx *c, const float *Q, const float *theta_inv, const uint16_t
     p.part_o = reinterpret_cast<float *>(c->scratch);
     p.part_ml = p.part_o + ntile * p.nsplit * rt * kHD;
   }
-  HIP_TRY(mia::launch_flash(p, kG, s, nullptr));
+  hipEvent_t ev0, ev1;
+  if (int rc = prof_pair(c, 1, &ev0, &ev1)) return rc;
+  HIP_TRY(mia::launch_flash(p, kG, s, ev0, ev1));
+  HIP_TRY(mia::launch_flash_merge(p, s));
   return MIA_OK;
 }
 
@@ -215,6 +246,31 @@ int mia_init(int device) {
   c.num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   HIP_TRY(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
   c.ready = true;
+  return MIA_OK;
+}
+
+int mia_profile_begin(void) {
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  c->prof_n[0] = c->prof_n[1] = 0;
+  c->prof_on = true;
+  return MIA_OK;
+}
+
+int mia_profile_end(int kind, int *count, double *total_ms) {
+  if (kind < 0 || kind > 1 || !count || !total_ms) return set_err(MIA_ERR_INVALID, "bad profile query");
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  c->prof_on = false;
+  HIP_TRY(hipDeviceSynchronize());
+  double total = 0.0;
+  for (size_t i = 0; i < c->prof_n[kind]; ++i) {
+    float ms = 0.f;
+    HIP_TRY(hipEventElapsedTime(&ms, c->prof_ev[kind][2 * i], c->prof_ev[kind][2 * i + 1]));
+    total += ms;
+  }
+  *count = (int)c->prof_n[kind];
+  *total_ms = total;
   return MIA_OK;
 }
 

@@ -381,14 +381,19 @@ int decode_pick_nchunk(int L, int n_kv, int target_wgs) {
   return nchunk;
 }
 
-hipError_t launch_decode(const DecodeParams &p, int g, bool fused, hipStream_t s) {
+hipError_t launch_decode(const DecodeParams &p, int g, bool fused, hipStream_t s, hipEvent_t ev0,
+                         hipEvent_t ev1) {
   if (g != G) return hipErrorInvalidValue;
   if (p.nchunk < 1 || p.nchunk > kMaxChunks) return hipErrorInvalidValue;
   dim3 grid(p.n_kv * p.nchunk), block(kThreads);
   if (fused)
-    hipLaunchKernelGGL(decode_kernel<true>, grid, block, 0, s, p);
+    hipExtLaunchKernelGGL(decode_kernel<true>, grid, block, 0, s, ev0, ev1, 0, p);
   else
-    hipLaunchKernelGGL(decode_kernel<false>, grid, block, 0, s, p);
+    hipExtLaunchKernelGGL(decode_kernel<false>, grid, block, 0, s, ev0, ev1, 0, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_merge(const DecodeParams &p, hipStream_t s) {
   if (p.nchunk > 1) hipLaunchKernelGGL(decode_merge_kernel, dim3(p.n_kv * G * 4), dim3(256), 0, s, p);
   return hipGetLastError();
 }

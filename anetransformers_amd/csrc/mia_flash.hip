@@ -396,7 +396,7 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(FlashParams p, int rt)
 }
 
 template <int SL, int KH>
-hipError_t launch_variant(const FlashParams &p, hipStream_t s) {
+hipError_t launch_variant(const FlashParams &p, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   using Lay = FlashLayout<SL, KH>;
   static bool attr_set = false;
   if (!attr_set) {
@@ -406,7 +406,8 @@ hipError_t launch_variant(const FlashParams &p, hipStream_t s) {
     attr_set = true;
   }
   dim3 grid(p.n_kv * p.n_rtiles * p.nsplit);
-  hipLaunchKernelGGL((flash_kernel<4, SL, KH>), grid, dim3(64 * SL * KH), Lay::kBytes, s, p);
+  hipExtLaunchKernelGGL((flash_kernel<4, SL, KH>), grid, dim3(64 * SL * KH), Lay::kBytes, s, ev0, ev1,
+                        0, p);
   return hipGetLastError();
 }
 
@@ -450,13 +451,14 @@ void flash_plan(int S, int n_kv, int G, int start_pos, int max_seq, int target_w
   *rows_per_tile = rt;
 }
 
-hipError_t launch_flash(const FlashParams &p, int G, hipStream_t s, int *rows_per_tile_out) {
+hipError_t launch_flash(const FlashParams &p, int G, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   if (G != 4) return hipErrorInvalidValue;
-  const int rows = p.S * G;
-  const int rt = rows <= 32 ? 32 : 64;
-  if (rows_per_tile_out) *rows_per_tile_out = rt;
-  hipError_t e = rt == 32 ? launch_variant<1, 4>(p, s) : launch_variant<2, 4>(p, s);
-  if (e != hipSuccess) return e;
+  const int rt = p.S * G <= 32 ? 32 : 64;
+  return rt == 32 ? launch_variant<1, 4>(p, s, ev0, ev1) : launch_variant<2, 4>(p, s, ev0, ev1);
+}
+
+hipError_t launch_flash_merge(const FlashParams &p, hipStream_t s) {
+  const int rt = p.S * 4 <= 32 ? 32 : 64;
   if (p.nsplit > 1)
     hipLaunchKernelGGL((flash_merge_kernel<4>), dim3(p.n_kv * p.n_rtiles * (rt / 8)), dim3(256), 0,
                        s, p, rt);

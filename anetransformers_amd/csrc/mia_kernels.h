@@ -2,6 +2,7 @@
 // Only the C-ABI shim (mia_capi.cpp) calls these; no torch types anywhere.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -31,7 +32,11 @@ struct DecodeParams {
 // Scratch needed by launch_decode for a given shape (bytes of part_o+part_ml).
 size_t decode_scratch_bytes(int n_kv, int G, int nchunk);
 int decode_pick_nchunk(int L, int n_kv, int target_wgs);
-hipError_t launch_decode(const DecodeParams &p, int G, bool fused, hipStream_t s);
+// Main kernel only; launch_decode_merge adds the cross-chunk merge (nchunk > 1).
+// ev0/ev1 (may be null) are stamped at the kernel's start and end.
+hipError_t launch_decode(const DecodeParams &p, int G, bool fused, hipStream_t s, hipEvent_t ev0,
+                         hipEvent_t ev1);
+hipError_t launch_decode_merge(const DecodeParams &p, hipStream_t s);
 
 // S>=1 causal attention on fp16 MFMA for the queries start_pos..start_pos+S-1.
 struct FlashParams {
@@ -51,7 +56,10 @@ struct FlashParams {
   float qscale;
 };
 size_t flash_scratch_bytes(int n_kv, int n_rtiles, int nsplit, int rows_per_tile);
-hipError_t launch_flash(const FlashParams &p, int G, hipStream_t s, int *rows_per_tile_out);
+// Main kernel only; launch_flash_merge adds the split merge (nsplit > 1).
+// ev0/ev1 (may be null) are stamped at the kernel's start and end.
+hipError_t launch_flash(const FlashParams &p, int G, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
+hipError_t launch_flash_merge(const FlashParams &p, hipStream_t s);
 void flash_plan(int S, int n_kv, int G, int start_pos, int max_seq, int target_wgs,
                 int *n_rtiles, int *nsplit, int *split_keys, int *rows_per_tile);
 

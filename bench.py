@@ -10,8 +10,12 @@ prefill attention TFLOP/s (% of fp16 MFMA peak).
           ring write, split-K flash-decode with LSE merge).
   prefill:         32 layers, 1536 cached positions + 512 new tokens
           (positions 1536..2047, causal), fp16-valued Q/K/V.  One step = 32
-          calls of mia_attention_step; the flash kernel alone is timed on the
-          same stream for its TFLOP/s.
+          calls of mia_attention_step (K RoPE + ring write, flash kernel).
+
+roofline.achieved divides the algorithmic bytes (decode) or FLOPs (prefill)
+of one launch by the dominant kernel's average duration, taken from HIP event
+pairs the library records around that kernel on its stream during a second
+pass over the same timed loop.
 
 Inputs are synthetic (seeded) and resident in HBM before timing starts.
 Prints one JSON line.
@@ -20,6 +24,7 @@ Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -129,13 +134,6 @@ class Prefill:
             check(self.lib.mia_attention_step(q, k, v, self.th.ptr, kc, vc, out, N_HEADS, N_KV, HD,
                                               PF_M, PF_START, PF_S, None), "attention_step")
 
-    def attention_only(self) -> None:
-        """The flash kernel alone over the written rings (Q used as rotated)."""
-        for l in range(N_LAYERS):
-            q, _, _, kc, vc, out = self._ptrs(l)
-            check(self.lib.mia_attention_batch(q, out, kc, vc, N_HEADS, N_KV, HD, PF_M, PF_START,
-                                               PF_S, None), "attention_batch")
-
 
 def timed(lib, fn, steps: int, warmup: int) -> float:
     """Mean ms per call of fn over `steps`, HIP events on the library stream."""
@@ -149,6 +147,20 @@ def timed(lib, fn, steps: int, warmup: int) -> float:
     e1.record()
     check(lib.mia_device_sync())
     return e0.elapsed_ms(e1) / steps
+
+
+def kernel_avg_ms(lib, fn, steps: int, kind: int) -> float:
+    """Average duration of the main attention kernel (kind 0 decode, 1 flash)
+    over `steps` calls of fn, from the library's per-kernel HIP event pairs on
+    the kernel's own stream (merge kernels excluded)."""
+    check(lib.mia_device_sync())
+    check(lib.mia_profile_begin())
+    for _ in range(steps):
+        fn()
+    n = ctypes.c_int()
+    tot = ctypes.c_double()
+    check(lib.mia_profile_end(kind, ctypes.byref(n), ctypes.byref(tot)))
+    return tot.value / max(n.value, 1)
 
 
 def cpu_baseline_decode(n_layers: int = 8, reps: int = 3):
@@ -252,23 +264,25 @@ def main() -> int:
             check(lib.mia_memcpy_d2d(dst.ptr, src.ptr, nb))
         check(lib.mia_device_sync())
         del src, dst
-    dec_ms = float("nan")
+    dec_ms = kern_ms = float("nan")
     if not args.skip_decode:
         log("decode: allocating 32 x 32768-slot rings (4 GiB)")
         dec = Decode(lib)
         dec_ms = timed(lib, dec.step, args.steps, args.warmup)
+        kern_ms = kernel_avg_ms(lib, dec.step, args.steps, 0)
         del dec
-    launch_ms = dec_ms / N_LAYERS
-    achieved = DECODE_BYTES_PER_LAYER / (launch_ms * 1e-3) / 1e9
+    achieved = DECODE_BYTES_PER_LAYER / (kern_ms * 1e-3) / 1e9
     value = N_LAYERS * DECODE_BYTES_PER_LAYER / (dec_ms * 1e-3) / 1e9
-    log(f"decode: {dec_ms:.3f} ms/step, {value:.1f} GB/s")
+    log(f"decode: {dec_ms:.3f} ms/step, {value:.1f} GB/s; decode kernel {kern_ms * 1e3:.2f} us "
+        f"({achieved:.1f} GB/s)")
 
     prefill = None
     if not args.skip_prefill:
         log("prefill: 32 layers x (1536 cached + 512 new)")
         pf = Prefill(lib)
-        pf_ms = timed(lib, pf.step, max(args.steps // 2, 3), 2)
-        fl_ms = timed(lib, pf.attention_only, max(args.steps // 2, 3), 2) / N_LAYERS
+        pf_steps = max(args.steps // 2, 3)
+        pf_ms = timed(lib, pf.step, pf_steps, 2)
+        fl_ms = kernel_avg_ms(lib, pf.step, pf_steps, 1)
         fl_tfs = PF_FLOP_PER_LAYER / (fl_ms * 1e-3) / 1e12
         log(f"prefill: {pf_ms:.3f} ms/step, flash kernel {fl_ms * 1e3:.1f} us, {fl_tfs:.1f} TFLOP/s")
         prefill = {
@@ -278,6 +292,7 @@ def main() -> int:
             "workload": "causal prefill chunk: 32 layers, 512 new tokens after 1536 cached "
                         "positions, 32 q / 8 kv heads, hd 128, fp16 MFMA, fp32 accumulate",
             "flop_per_layer": PF_FLOP_PER_LAYER,
+            "kernel_us": round(fl_ms * 1e3, 2),
             "roofline": {"bound": "mfma", "achieved": round(fl_tfs, 3),
                          "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
                          "frac": round(fl_tfs / MFMA_F16_PEAK_TFS, 4),
@@ -312,6 +327,7 @@ def main() -> int:
                         "RoPE theta 1e6, fused RoPE + ring write + split-K flash-decode",
             "layers": N_LAYERS, "ctx": DECODE_L, "max_seq": DECODE_M,
             "bytes_per_layer": DECODE_BYTES_PER_LAYER,
+            "decode_kernel_us": round(kern_ms * 1e3, 2),
         },
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),

@@ -59,6 +59,16 @@ int mia_event_destroy(void *event);
 int mia_event_record(void *event, void *stream);
 int mia_event_elapsed_ms(float *ms, void *start, void *stop);
 
+/* Opt-in kernel timing on the current device: while on, the main kernel of
+ * every attention call is launched with a HIP event pair that the dispatch
+ * stamps at its start and end (kind 0: the S=1 decode kernel of
+ * mia_gqa_attention / mia_decode_step / mia_attention_step with S=1; kind 1:
+ * the S>1 flash kernel); merge and RoPE kernels are not timed.
+ * mia_profile_end stops recording, synchronises and returns the number of
+ * timed launches of that kind and their summed duration. */
+int mia_profile_begin(void);
+int mia_profile_end(int kind, int *count, double *total_ms);
+
 /* ---- synthetic inputs (benchmark) --------------------------------------- */
 /* dst[i] = fp16(N(0,1)) from a counter-based splitmix64 + Box-Muller stream. */
 int mia_fill_normal_f16(uint16_t *dst_dev, size_t n, uint64_t seed, void *stream);
