@@ -14,8 +14,12 @@ prefill attention TFLOP/s (% of fp16 MFMA peak).
 
 roofline.achieved divides the algorithmic bytes (decode) or FLOPs (prefill)
 of one launch by the dominant kernel's average duration, taken from HIP event
-pairs the library records around that kernel on its stream during a second
-pass over the same timed loop.
+pairs that the kernel's own dispatch stamps (mia_profile_begin/end) during a
+second pass over the same timed loop.
+
+dropin: the same decode step through the C drop-in (mia_dropin_decode_step)
+with host q/k/v/out buffers, synchronous per layer as the reference's call
+site is: the PCIe-inclusive rate, reported beside the headline, never as it.
 
 Inputs are synthetic (seeded) and resident in HBM before timing starts.
 Prints one JSON line.
@@ -97,6 +101,44 @@ class Decode:
                 self.v.ptr + l * KV_DIM * 4, self.th.ptr, self.kc.ptr + l * lay,
                 self.vc.ptr + l * lay, self.out.ptr + l * N_HEADS * HD * 4, N_HEADS, N_KV, HD,
                 DECODE_M, DECODE_POS, None), "decode_step")
+
+
+class DropinDecode:
+    """The decode workload through the C drop-in: host buffers, one
+    synchronous mia_dropin_decode_step per layer on the same device rings."""
+
+    def __init__(self, lib, dec: Decode, seed: int = 0):
+        self.lib = lib
+        g = np.random.default_rng(seed + 100)
+        self.kv = mia.KVCache(N_LAYERS, N_KV, HD, DECODE_M, KV_DIM, dec.kc.ptr, dec.vc.ptr, 0,
+                              DECODE_M)
+        self.q = g.standard_normal((N_LAYERS, N_HEADS * HD), np.float32)
+        self.k = g.standard_normal((N_LAYERS, KV_DIM), np.float32)
+        self.v = g.standard_normal((N_LAYERS, KV_DIM), np.float32)
+        self.th = theta_inv()
+        self.out = np.empty((N_LAYERS, N_HEADS * HD), np.float32)
+        lib.mia_dropin_set_abort(0)
+
+    def step(self) -> None:
+        kv = ctypes.byref(self.kv)
+        for l in range(N_LAYERS):
+            self.lib.mia_dropin_decode_step(kv, l, self.q[l].ctypes.data, self.k[l].ctypes.data,
+                                            self.v[l].ctypes.data, DECODE_POS,
+                                            self.th.ctypes.data, N_HEADS, N_KV,
+                                            self.out[l].ctypes.data)
+            if self.lib.mia_dropin_status() != 0:
+                raise mia.MiattnError(self.lib.mia_dropin_status(),
+                                      self.lib.mia_last_error().decode())
+
+
+def wall_ms(fn, steps: int, warmup: int) -> float:
+    """Mean wall-clock ms per call of a synchronous fn."""
+    for _ in range(warmup):
+        fn()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    return (time.perf_counter() - t0) * 1e3 / steps
 
 
 class Prefill:
@@ -265,12 +307,20 @@ def main() -> int:
         check(lib.mia_device_sync())
         del src, dst
     dec_ms = kern_ms = float("nan")
+    dropin = None
     if not args.skip_decode:
         log("decode: allocating 32 x 32768-slot rings (4 GiB)")
         dec = Decode(lib)
         dec_ms = timed(lib, dec.step, args.steps, args.warmup)
         kern_ms = kernel_avg_ms(lib, dec.step, args.steps, 0)
-        del dec
+        dd = DropinDecode(lib, dec)
+        di_ms = wall_ms(dd.step, args.steps, args.warmup)
+        dropin = {"value": round(N_LAYERS * DECODE_BYTES_PER_LAYER / (di_ms * 1e-3) / 1e9, 2),
+                  "unit": "GB/s", "ms_per_step": round(di_ms, 4),
+                  "path": "mia_dropin_decode_step per layer, host q/k/v/out (PCIe), "
+                          "synchronous, wall clock"}
+        log(f"decode via drop-in (host buffers): {di_ms:.3f} ms/step")
+        del dd, dec
     achieved = DECODE_BYTES_PER_LAYER / (kern_ms * 1e-3) / 1e9
     value = N_LAYERS * DECODE_BYTES_PER_LAYER / (dec_ms * 1e-3) / 1e9
     log(f"decode: {dec_ms:.3f} ms/step, {value:.1f} GB/s; decode kernel {kern_ms * 1e3:.2f} us "
@@ -319,7 +369,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 storage, f32 math",
+        "dtype": "f16",
         "data": "synthetic (seeded N(0,1) fp16 rings generated on the GPU)",
         "config": {
             "workload": "decode attention step x 32 layers: 32768-slot fp16 ring full, new "
@@ -328,11 +378,13 @@ def main() -> int:
             "layers": N_LAYERS, "ctx": DECODE_L, "max_seq": DECODE_M,
             "bytes_per_layer": DECODE_BYTES_PER_LAYER,
             "decode_kernel_us": round(kern_ms * 1e3, 2),
+            "arithmetic": "fp16 MFMA operands (q split hi+lo), fp32 accumulate and softmax",
         },
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic("decode_32k")},
         "cpu_baseline": cpu,
+        "dropin": dropin,
         "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
