@@ -7,7 +7,10 @@
 // query heads of a group share every K/V tile.  A workgroup holds SL row slabs
 // of 32 rows and KH key groups; wave w works on slab w % SL over the key range
 // of group w / SL, and the KH partial results are merged in LDS at the end.
-// Per 32-key tile (double-buffered in LDS per key group):
+// K/V tiles go from global memory straight into LDS (global_load_lds, no
+// register staging), double-buffered per key group; the tile loop is software
+// pipelined so that the scores of tile i+1 are computed on MFMA while the
+// exponentials of tile i are formed.  Per 32-key tile:
 //   S^T[key][row] = K . Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS
 //                             (ds_read_b128), B = Q^T held in registers
 //   online softmax per row    each lane owns one row (the D column), so the
@@ -32,11 +35,15 @@ namespace mia {
 namespace {
 
 constexpr int kKT = 32;         // keys per tile
-constexpr int kPitch = HD + 8;  // LDS row pitch in halfs (272 B)
+// K/V tiles live in LDS unpadded, one 256 B row per key, with the 16-byte
+// chunk c of row r stored at chunk c ^ swz(r): rows r..r+15 then hit distinct
+// bank groups for the K operand reads (same chunk, 16 rows), and the 4 rows x
+// 2 chunks of a transposing V read are distinct too.
+__device__ __forceinline__ int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
 template <int SL, int KH>
 struct FlashLayout {
-  static constexpr int kTileHalfs = kKT * kPitch;
+  static constexpr int kTileHalfs = kKT * HD;
   // [KH][2 buffers][K, V] tiles
   static constexpr size_t kTiles = (size_t)KH * 2 * 2 * kTileHalfs * sizeof(_Float16);
   static constexpr size_t kRope = (size_t)8 * SL * 64 * sizeof(float2);
@@ -56,17 +63,74 @@ typedef short s4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) _Float16 lds_half;
 typedef __attribute__((address_space(3))) s4 lds_s4;
 typedef __attribute__((address_space(3))) h8 lds_h8;
-typedef __attribute__((address_space(3))) u4 lds_u4;
 
-// Four consecutive keys k0..k0+3 of dim d0 + (lane % 16) from a row-major
-// [key][kPitch] fp16 tile: input lane i of each 16-lane group points at
+// Four consecutive keys k0..k0+3 of dim d0 + (lane % 16) from a swizzled
+// [key][128] fp16 tile: input lane i of each 16-lane group points at
 // (k0 + i/4, d0 + 4*(i%4)); the transposing read returns, in output lane j,
 // elements (k0 + e, d0 + j) for e = 0..3.
 __device__ __forceinline__ h4 read_vt4(lds_half *tile, int k0, int d0, int lane) {
   const int i = lane & 15;
-  lds_half *src = tile + (k0 + (i >> 2)) * kPitch + d0 + 4 * (i & 3);
-  s4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)src);
-  return __builtin_bit_cast(h4, r);
+  const int r = k0 + (i >> 2);
+  const int c = (d0 >> 3) + ((i & 3) >> 1);
+  lds_half *src = tile + r * HD + 8 * (c ^ swz(r)) + 4 * (i & 1);
+  s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)src);
+  return __builtin_bit_cast(h4, v);
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane i's data
+// lands at byte 16*i of the wave's 1 KB block at `l` (wave-uniform).  Inline
+// assembly, so that the compiler neither orders later LDS reads of the other
+// buffer behind it nor waits for it; completion is awaited explicitly (vmcnt)
+// before the workgroup barrier that publishes the tile.
+__device__ __forceinline__ void lds_dma16(const void *g, lds_half *l) {
+  const unsigned m = __builtin_amdgcn_readfirstlane((unsigned)(__UINTPTR_TYPE__)l);
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %0, off" ::"v"(g),
+      "s"(m)
+      : "m0");
+}
+// Same with a wave-uniform base address and a per-lane 32-bit byte offset.
+__device__ __forceinline__ void lds_dma16_sb(const void *base, unsigned voff, lds_half *l) {
+  const unsigned m = __builtin_amdgcn_readfirstlane((unsigned)(__UINTPTR_TYPE__)l);
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %0, %1" ::"v"(voff),
+      "s"(base), "s"(m)
+      : "m0");
+}
+
+// Issues this wave's share of the direct loads of one tensor (K or V) of the
+// 32-key tile kb..kb+31 (range ending at ke) into the tile buffer dst.  A tile
+// of 32 consecutive ring slots takes a uniform base plus the lane's constant
+// offset; tiles that wrap or reach into the staging buffer take per-lane
+// addresses.
+template <int IPW, int SL>
+__device__ __forceinline__ void load_tensor(const _Float16 *ring, const _Float16 *stage, int kb,
+                                            int ke, int start_pos, int max_seq, int kv_dim,
+                                            const int *lane_row, const int *lane_off,
+                                            const unsigned *lane_boff, int slab, lds_half *dst) {
+  const bool full = kb + kKT <= ke;
+  const int slot0 = kb % max_seq;  // uniform, once per tile
+  const bool contiguous =
+      full && slot0 + kKT <= max_seq && (stage == nullptr || kb + kKT <= start_pos);
+  if (contiguous) {
+    const _Float16 *base = ring + (size_t)slot0 * kv_dim;
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) lds_dma16_sb(base, lane_boff[j], dst + (slab + SL * j) * 4 * HD);
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < IPW; ++j) {
+    const int r = lane_row[j];
+    const int kp = min(kb + r, ke - 1);
+    const bool staged = stage != nullptr && kp >= start_pos;
+    int slot = slot0 + (kp - kb);
+    slot = slot >= max_seq ? slot - max_seq : slot;
+    const _Float16 *src = (staged ? stage : ring) +
+                          (size_t)(staged ? kp - start_pos : slot) * kv_dim + lane_off[j];
+    lds_dma16(src, dst + (slab + SL * j) * 4 * HD);
+  }
 }
 
 template <int G, int SL, int KH>
@@ -75,14 +139,13 @@ __global__ void __launch_bounds__(64 * SL * KH) flash_kernel(FlashParams p) {
   constexpr int NW = SL * KH;
   constexpr int RT = 32 * SL;     // rows per workgroup
   constexpr int QT = RT / G;      // queries per workgroup
-  constexpr int LT = 64 * SL;     // threads per key group
   extern __shared__ __attribute__((aligned(16))) char smem[];
   lds_half *tiles = (lds_half *)smem;
   float2 *rope = reinterpret_cast<float2 *>(smem + (Lay::kBytes - Lay::kRope));
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int slab = w % SL;
   const int kg = w / SL;
   const int half = lane >> 5;
@@ -122,6 +185,44 @@ __global__ void __launch_bounds__(64 * SL * KH) flash_kernel(FlashParams p) {
   const int g_count = (int)((long)(kg + 1) * nt / KH) - g_first;
   const int n_iter = (nt + KH - 1) / KH;
 
+  // Tile buffers (per key group: K ring and V ring of 2) and this lane's
+  // share of the direct loads.  One wave instruction moves 4 keys (64 lanes x
+  // 16 B); the SL waves of a key group share the 8 instructions per tensor of
+  // a 32-key tile.  Lane i of instruction j loads key row 4j + i/16, logical
+  // chunk (i%16) ^ swz(row), which the hardware writes at byte 16*i of the
+  // instruction's 1 KB block.
+  constexpr int IPW = (kKT / 4) / SL;  // instructions per wave per tensor
+  lds_half *ktile[2], *vtile[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    ktile[b] = tiles + ((size_t)(kg * 2 + b) * 2 + 0) * Lay::kTileHalfs;
+    vtile[b] = tiles + ((size_t)(kg * 2 + b) * 2 + 1) * Lay::kTileHalfs;
+  }
+  int lane_row[IPW], lane_off[IPW];
+  unsigned lane_boff[IPW];  // byte offset from the tile's first slot
+#pragma unroll
+  for (int j = 0; j < IPW; ++j) {
+    const int r = 4 * (slab + SL * j) + (lane >> 4);
+    lane_row[j] = r;
+    lane_off[j] = kvh * HD + 8 * ((lane & 15) ^ swz(r));
+    lane_boff[j] = (unsigned)(r * kv_dim + lane_off[j]) * 2u;
+  }
+  const _Float16 *const kc = p.kc, *const vc = p.vc;
+  const _Float16 *const kst = p.kstage, *const vst = p.vstage;
+  const int kb0 = ks + kKT * g_first;  // first key of this group's tile 0
+#define MIA_LOAD_K(i, buf)                                                                    \
+  load_tensor<IPW, SL>(kc, kst, kb0 + kKT * (i), ke, p.start_pos, p.max_seq, kv_dim, lane_row, \
+                       lane_off, lane_boff, slab, ktile[buf])
+#define MIA_LOAD_V(i, buf)                                                                    \
+  load_tensor<IPW, SL>(vc, vst, kb0 + kKT * (i), ke, p.start_pos, p.max_seq, kv_dim, lane_row, \
+                       lane_off, lane_boff, slab, vtile[buf])
+  // K of tiles 0 and 1 and V of tile 0 go out before the query loads.
+  if (g_count > 0) {
+    MIA_LOAD_K(0, 0);
+    MIA_LOAD_V(0, 0);
+  }
+  if (g_count > 1) MIA_LOAD_K(1, 1);
+
   // RoPE (cos, sin) for the workgroup's queries, fl32(theta_inv[i] * pos) as
   // vDSP_vsmul (mistral_model.h:87-88).
   if (p.theta_inv != nullptr) {
@@ -158,71 +259,6 @@ __global__ void __launch_bounds__(64 * SL * KH) flash_kernel(FlashParams p) {
     }
   }
 
-  // Tile loading by the LT threads of this key group: 32 keys x 16 chunks of
-  // 16 B per tensor.
-  constexpr int CPT = kKT * 16 / LT;  // chunks per thread per tensor
-  const int lt = slab * 64 + lane;
-  lds_half *ktile[2], *vtile[2];
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    ktile[b] = tiles + ((size_t)(kg * 2 + b) * 2 + 0) * Lay::kTileHalfs;
-    vtile[b] = tiles + ((size_t)(kg * 2 + b) * 2 + 1) * Lay::kTileHalfs;
-  }
-  u4 rk[CPT], rv[CPT];
-  // Lane offsets inside a tile are loop invariant; the tile base is uniform.
-  int lane_off[CPT], lane_row[CPT];
-#pragma unroll
-  for (int c = 0; c < CPT; ++c) {
-    const int ch = lt + c * LT;
-    lane_row[c] = ch >> 4;
-    lane_off[c] = (ch >> 4) * kv_dim + kvh * HD + 8 * (ch & 15);
-  }
-  auto gload = [&](int tile_idx) {
-    const int kb = ks + kKT * tile_idx;
-    const bool full = kb + kKT <= ke;
-    const int slot0 = kb % p.max_seq;  // uniform, once per tile
-    const bool contiguous = full && slot0 + kKT <= p.max_seq &&
-                            (p.kstage == nullptr || kb + kKT <= p.start_pos);
-    if (contiguous) {  // wave-uniform fast path: all 32 keys in consecutive ring slots
-      const _Float16 *kt = p.kc + (size_t)slot0 * kv_dim;
-      const _Float16 *vt = p.vc + (size_t)slot0 * kv_dim;
-#pragma unroll
-      for (int c = 0; c < CPT; ++c) {
-        rk[c] = *reinterpret_cast<const u4 *>(kt + lane_off[c]);
-        rv[c] = *reinterpret_cast<const u4 *>(vt + lane_off[c]);
-      }
-      return;
-    }
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int kp = min(kb + lane_row[c], ke - 1);
-      const int in_tile = lane_off[c] - lane_row[c] * kv_dim;
-      const _Float16 *ksrc, *vsrc;
-      if (p.kstage != nullptr && kp >= p.start_pos) {
-        size_t off = (size_t)(kp - p.start_pos) * kv_dim + in_tile;
-        ksrc = p.kstage + off;
-        vsrc = p.vstage + off;
-      } else {
-        int slot = slot0 + (kp - kb);
-        slot = slot >= p.max_seq ? slot - p.max_seq : slot;
-        size_t off = (size_t)slot * kv_dim + in_tile;
-        ksrc = p.kc + off;
-        vsrc = p.vc + off;
-      }
-      rk[c] = *reinterpret_cast<const u4 *>(ksrc);
-      rv[c] = *reinterpret_cast<const u4 *>(vsrc);
-    }
-  };
-  auto lstore = [&](int b) {
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int ch = lt + c * LT;
-      const int kr = ch >> 4, cc = ch & 15;
-      *(lds_u4 *)(ktile[b] + kr * kPitch + 8 * cc) = rk[c];
-      *(lds_u4 *)(vtile[b] + kr * kPitch + 8 * cc) = rv[c];
-    }
-  };
-
   f16v o[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -230,52 +266,66 @@ __global__ void __launch_bounds__(64 * SL * KH) flash_kernel(FlashParams p) {
     for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  if (g_count > 0) {
-    gload(g_first);
-    lstore(0);
-  }
+  // S^T block of one tile: keys x this slab's 32 rows; s[i] is key
+  // kb + (i/4)*8 + 4*half + (i%4) for row `row`.
+  auto qk = [&](lds_half *kt) {
+    f16v s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      h8 a = *(lds_h8 *)(kt + col * HD + 8 * ((2 * st + half) ^ swz(col)));
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[st], s, 0, 0, 0);
+    }
+    return s;
+  };
+  // Window mask (only for tiles crossing a window edge of the slab) and the
+  // row max over the tile.
+  auto mask_max = [&](f16v &s, int kb) {
+    const bool inside = slab_full && kb >= lo_max && kb + kKT - 1 <= hi_min && kb + kKT <= ke;
+    if (!inside) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kb + (i >> 2) * 8 + 4 * half + (i & 3);
+        const bool ok = row_valid && key >= lo_t && key <= hi_t && key < ke;
+        s[i] = ok ? s[i] : -INFINITY;
+      }
+    }
+    float m = s[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) m = fmaxf(m, s[i]);
+    return fmaxf(m, __shfl_xor(m, 32));
+  };
+
+  // Software pipeline over this group's tiles: iteration it holds the masked
+  // scores of tile it (s_cur, row max m_cur), computes the scores of tile
+  // it+1 on MFMA while the exponentials of tile it are formed, then adds
+  // P.V of tile it.  Buffers: K(i) in ktile[i&1], V(i) in vtile[i&1]; during
+  // iteration it the loads of K(it+2) and V(it+1) are in flight.
+  asm volatile("s_waitcnt vmcnt(0)");
   __syncthreads();
+  f16v s_cur = qk(ktile[0]);
+  float m_cur = mask_max(s_cur, kb0);
 
   for (int it = 0; it < n_iter; ++it) {
-    const bool more = it + 1 < g_count;
-    if (more) gload(g_first + it + 1);
+    // this wave's loads of K(it+1) and V(it) have landed; after the barrier
+    // every wave's have, and every wave is done with K(it) and V(it-1)
+    asm volatile("s_waitcnt vmcnt(0)");
+    __syncthreads();
+    if (it + 2 < g_count) MIA_LOAD_K(it + 2, it & 1);
+    if (it + 1 < g_count) MIA_LOAD_V(it + 1, (it + 1) & 1);
     if (it < g_count) {
-      const int b = it & 1;
-      const int kb = ks + kKT * (g_first + it);
-      // S^T block: keys kb..kb+31 x this slab's 32 rows.
-      f16v s;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] = 0.f;
-#pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        h8 a = *(lds_h8 *)(ktile[b] + col * kPitch + 16 * st + 8 * half);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[st], s, 0, 0, 0);
-      }
-      // s[i]: key kb + (i/4)*8 + 4*half + (i%4) for row `row`.
-      const bool inside = slab_full && kb >= lo_max && kb + kKT - 1 <= hi_min && kb + kKT <= ke;
-      if (!inside) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = kb + (i >> 2) * 8 + 4 * half + (i & 3);
-          const bool ok = row_valid && key >= lo_t && key <= hi_t && key < ke;
-          s[i] = ok ? s[i] : -INFINITY;
-        }
-      }
-      float mloc = s[0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, s[i]);
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-      // Lazy rescale: m_run is the reference max of the row's exponentials and
-      // moves only when a score exceeds it by more than 8 (log2 domain), so
-      // every p = 2^(s - m_run) stays <= 256 (exact range for fp16) and the
-      // accumulators are rescaled rarely.  Normalisation by l at the end is
-      // unaffected by the choice of reference.
-      const bool move = mloc > m_run + 8.0f;
+      // Lazy rescale: m_run is the reference max of the row's exponentials
+      // and moves only when a score exceeds it by more than 8 (log2 domain),
+      // so every p = 2^(s - m_run) stays <= 256 (exact range for fp16) and
+      // the accumulators are rescaled rarely.  Normalisation by l at the end
+      // is unaffected by the choice of reference.
+      const bool move = m_cur > m_run + 8.0f;
       if (__ballot(move) != 0) {  // wave-uniform
-        // rows that do not move keep alpha = 1 (also while still fully masked,
-        // m_run = -inf); the first move of a row gives alpha = 0
-        const float alpha = move ? fast_exp2(m_run - mloc) : 1.0f;
-        const float m_ref = move ? mloc : m_run;
+        // rows that do not move keep alpha = 1 (also while still fully
+        // masked, m_run = -inf); the first move of a row gives alpha = 0
+        const float alpha = move ? fast_exp2(m_run - m_cur) : 1.0f;
+        const float m_ref = move ? m_cur : m_run;
         l_run *= alpha;
 #pragma unroll
         for (int db = 0; db < 4; ++db)
@@ -284,33 +334,55 @@ __global__ void __launch_bounds__(64 * SL * KH) flash_kernel(FlashParams p) {
         m_run = m_ref;
       }
       const float m_use = m_run == -INFINITY ? 0.f : m_run;
-      h8 pb[2];  // P^T B operands for keys 0..15 and 16..31 of the tile
-      float lsum = 0.f;
+      // All LDS operands of the iteration are requested up front: K of tile
+      // it+1 (stale, unused data when it+1 == g_count) and V^T of tile it.
+      lds_half *kt = ktile[(it + 1) & 1];
+      lds_half *vt = vtile[it & 1];
+      h8 ka[8];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float pv = fast_exp2(s[i] - m_use);
-        lsum += pv;
-        pb[i >> 3][i & 7] = (_Float16)pv;
-      }
-      l_run += lsum;
-      // O^T += V^T P^T; k-step ks covers keys 16*ks .. +16, this half's 8 keys
-      // being {0-3, 8-11} + 4*half (the S^T row permutation).
+      for (int st = 0; st < 8; ++st)
+        ka[st] = *(lds_h8 *)(kt + col * HD + 8 * ((2 * st + half) ^ swz(col)));
+      // O^T += V^T P^T; k-step kst covers keys 16*kst .. +16, this half's 8
+      // keys being {0-3, 8-11} + 4*half (the S^T row permutation).
+      h8 va[2][4];
 #pragma unroll
       for (int kst = 0; kst < 2; ++kst) {
         const int k0 = 16 * kst + 4 * half;
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
           const int d0 = 32 * db + 16 * ((lane >> 4) & 1);
-          h4 lo = read_vt4(vtile[b], k0, d0, lane);
-          h4 hi = read_vt4(vtile[b], k0 + 8, d0, lane);
-          h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[kst], o[db], 0, 0, 0);
+          h4 lo = read_vt4(vt, k0, d0, lane);
+          h4 hi = read_vt4(vt, k0 + 8, d0, lane);
+          va[kst][db] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
       }
+      h8 pb[2];  // P^T B operands for keys 0..15 and 16..31 of the tile
+      float lsum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float pv = fast_exp2(s_cur[i] - m_use);
+        lsum += pv;
+        pb[i >> 3][i & 7] = (_Float16)pv;
+      }
+      l_run += lsum;
+      f16v s_next;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s_next[i] = 0.f;
+#pragma unroll
+      for (int st = 0; st < 8; ++st)
+        s_next = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[st], s_next, 0, 0, 0);
+#pragma unroll
+      for (int kst = 0; kst < 2; ++kst)
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[kst][db], pb[kst], o[db], 0, 0, 0);
+      m_cur = mask_max(s_next, kb0 + kKT * (it + 1));
+      s_cur = s_next;
     }
-    if (more) lstore((it + 1) & 1);
-    __syncthreads();
   }
+#undef MIA_LOAD_K
+#undef MIA_LOAD_V
+  __syncthreads();  // the merge below reuses the tile area
 
   // Merge the KH key groups (LDS; the tile area is free after the loop).
   const float l_tot = l_run + __shfl_xor(l_run, 32);
