@@ -112,6 +112,13 @@ int check_shape(int n_heads, int n_kv_heads, int hd, int max_seq) {
   return MIA_OK;
 }
 
+// The attention kernels move fp32 rows 16 bytes at a time.
+int check_align16(const void *a, const void *b, const void *c, const void *d) {
+  const uintptr_t bits = (uintptr_t)a | (uintptr_t)b | (uintptr_t)c | (uintptr_t)d;
+  if (bits & 15) return set_err(MIA_ERR_INVALID, "Q/K/V/out device pointers must be 16-byte aligned");
+  return MIA_OK;
+}
+
 int check_pos(int pos, int S) {
   if (pos < 0 || S < 1) return set_err(MIA_ERR_INVALID, "bad position %d / token count %d", pos, S);
   if ((long)pos + S >= (long)INT_MAX) return set_err(MIA_ERR_INVALID, "position %d + %d overflows", pos, S);
@@ -174,7 +181,7 @@ int decode_impl(const float *q, const float *k, const float *v, const float *the
   return MIA_OK;
 }
 
-int flash_impl(DevCtx *c, const float *Q, const float *theta_inv, const uint16_t *kst,
+int flash_impl(DevCtx *c, const float *Q, const float *rope_cs, const uint16_t *kst,
                const uint16_t *vst, const uint16_t *k_layer, const uint16_t *v_layer, float *out,
                int n_kv, int max_seq, int start_pos, int S, hipStream_t s) {
   mia::FlashParams p{};
@@ -182,7 +189,7 @@ int flash_impl(DevCtx *c, const float *Q, const float *theta_inv, const uint16_t
   mia::flash_plan(S, n_kv, kG, start_pos, max_seq, c->num_cus, &p.n_rtiles, &p.nsplit,
                   &p.split_keys, &rt);
   p.Q = Q;
-  p.theta_inv = theta_inv;
+  p.rope_cs = rope_cs;
   p.kc = reinterpret_cast<const _Float16 *>(k_layer);
   p.vc = reinterpret_cast<const _Float16 *>(v_layer);
   p.kstage = reinterpret_cast<const _Float16 *>(kst);
@@ -441,6 +448,7 @@ int mia_attention_batch(const float *Q, float *out, const uint16_t *k_layer, con
                         int n_heads, int n_kv_heads, int hd, int max_seq, int start_pos, int S,
                         void *stream) {
   if (!Q || !out || !k_layer || !v_layer) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (int rc = check_align16(Q, out, k_layer, v_layer)) return rc;
   if (int rc = check_shape(n_heads, n_kv_heads, hd, max_seq)) return rc;
   if (int rc = check_pos(start_pos, S)) return rc;
   DevCtx *c;
@@ -456,6 +464,10 @@ int mia_attention_step(const float *Q, const float *K, const float *V, const flo
     return set_err(MIA_ERR_INVALID, "NULL pointer");
   if (int rc = check_shape(n_heads, n_kv_heads, hd, max_seq)) return rc;
   if (int rc = check_pos(start_pos, S)) return rc;
+  if (S > 1) {
+    if (int rc = check_align16(Q, K, V, out)) return rc;
+    if (int rc = check_align16(k_layer, v_layer, nullptr, nullptr)) return rc;
+  }
   if (S == 1)
     return decode_impl(Q, K, V, theta_inv, k_layer, v_layer, out, n_heads, n_kv_heads, max_seq,
                        start_pos, true, stream);
@@ -465,21 +477,24 @@ int mia_attention_step(const float *Q, const float *K, const float *V, const flo
   const int kv_dim = n_kv_heads * kHD;
   // Drafts may go straight into the ring when no slot they take still holds
   // a position some query of the batch attends (start_pos + S <= max_seq).
-  // Q is rotated inside the attention kernel.
+  // The K rotation also leaves the (cos, sin) table of the positions in the
+  // work buffer, from which the attention kernel rotates Q.
   const bool direct = (long)start_pos + S <= (long)max_seq;
+  const size_t cs_bytes = (size_t)S * kHD * sizeof(float);  // S x 64 (cos, sin)
+  const size_t st_bytes = direct ? 0 : (size_t)S * kv_dim * sizeof(uint16_t);
+  if (int rc = ensure_work(c, cs_bytes + 2 * st_bytes)) return rc;
+  float *cs = reinterpret_cast<float *>(c->work);
   if (direct) {
     HIP_TRY(mia::launch_rope_to_ring(K, V, theta_inv, S, start_pos, n_kv_heads,
                                      reinterpret_cast<_Float16 *>(k_layer),
-                                     reinterpret_cast<_Float16 *>(v_layer), max_seq, s));
-    return flash_impl(c, Q, theta_inv, nullptr, nullptr, k_layer, v_layer, out, n_kv_heads,
-                      max_seq, start_pos, S, s);
+                                     reinterpret_cast<_Float16 *>(v_layer), max_seq, cs, s));
+    return flash_impl(c, Q, cs, nullptr, nullptr, k_layer, v_layer, out, n_kv_heads, max_seq,
+                      start_pos, S, s);
   }
-  const size_t st_bytes = (size_t)S * kv_dim * sizeof(uint16_t);
-  if (int rc = ensure_work(c, 2 * st_bytes)) return rc;
-  _Float16 *kst = reinterpret_cast<_Float16 *>(c->work);
+  _Float16 *kst = reinterpret_cast<_Float16 *>(reinterpret_cast<char *>(c->work) + cs_bytes);
   _Float16 *vst = kst + (size_t)S * kv_dim;
-  HIP_TRY(mia::launch_rope_to_f16(K, V, theta_inv, S, start_pos, n_kv_heads, kst, vst, s));
-  if (int rc = flash_impl(c, Q, theta_inv, reinterpret_cast<uint16_t *>(kst),
+  HIP_TRY(mia::launch_rope_to_f16(K, V, theta_inv, S, start_pos, n_kv_heads, kst, vst, cs, s));
+  if (int rc = flash_impl(c, Q, cs, reinterpret_cast<uint16_t *>(kst),
                           reinterpret_cast<uint16_t *>(vst), k_layer, v_layer, out, n_kv_heads,
                           max_seq, start_pos, S, s))
     return rc;

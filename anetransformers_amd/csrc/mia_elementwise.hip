@@ -35,29 +35,50 @@ __global__ void rope_kernel(float *q, float *k, int S, int start_pos, const floa
   }
 }
 
-// Rotated K and plain V, rounded to fp16, into [S][kv_dim] destinations
-// (ring slots when kdst_ring, else a dense staging buffer).
-__global__ void rope_kv_f16_kernel(const float *K, const float *V, const float *theta_inv, int S,
-                                   int start_pos, int n_kv, _Float16 *kdst, _Float16 *vdst,
-                                   int max_seq, bool ring) {
+// One workgroup of 128 threads per token.  The 64 (cos, sin) pairs of the
+// token's position, fl32(theta_inv[i] * pos) as vDSP_vsmul + vvsincosf
+// (mistral_model.h:87-90), are formed once and optionally stored to cs_out for
+// the attention kernel's Q rotation.  Each thread then rotates 8 consecutive
+// dims (4 adjacent pairs, mistral_model.h:100-105) of one kv head of K, rounds
+// K and V to fp16 (RNE, mistral_model.h:160-169) and writes them to the ring
+// slot pos % max_seq (kv_write, kv_cache.h:53-57) or to a dense staging row.
+__global__ void __launch_bounds__(128)
+    rope_kv_f16_kernel(const float *K, const float *V, const float *theta_inv, int S, int start_pos,
+                       int n_kv, _Float16 *kdst, _Float16 *vdst, int max_seq, bool ring,
+                       float *cs_out) {
+  __shared__ float2 cs[HD / 2];
   const int t = blockIdx.x;
-  const int i = threadIdx.x;
-  if (t >= S || i >= HD / 2) return;
-  float ang = theta_inv[i] * (float)(start_pos + t);
-  float sn, cs;
-  sincosf(ang, &sn, &cs);
+  const int tid = threadIdx.x;
+  const int pos = start_pos + t;
+  if (tid < HD / 2) {
+    const float ang = theta_inv[tid] * (float)pos;
+    float sn, c;
+    sincosf(ang, &sn, &c);
+    cs[tid] = make_float2(c, sn);
+    if (cs_out) reinterpret_cast<float2 *>(cs_out)[(size_t)t * (HD / 2) + tid] = make_float2(c, sn);
+  }
+  __syncthreads();
   const int kv_dim = n_kv * HD;
-  const size_t drow = ring ? (size_t)((start_pos + t) % max_seq) : (size_t)t;
-  for (int h = 0; h < n_kv; ++h) {
-    const size_t so = (size_t)t * kv_dim + h * HD + 2 * i;
-    const size_t dof = drow * kv_dim + h * HD + 2 * i;
-    float2 kv = *reinterpret_cast<const float2 *>(K + so);
-    rope_pair(kv.x, kv.y, cs, sn);
-    float2 vv = *reinterpret_cast<const float2 *>(V + so);
-    kdst[dof] = (_Float16)kv.x;
-    kdst[dof + 1] = (_Float16)kv.y;
-    vdst[dof] = (_Float16)vv.x;
-    vdst[dof + 1] = (_Float16)vv.y;
+  const size_t drow = ring ? (size_t)(pos % max_seq) : (size_t)t;
+  for (int c = tid; c < n_kv * (HD / 8); c += blockDim.x) {
+    const int e0 = (c >> 4) * HD + 8 * (c & 15);
+    const f4 *ks = reinterpret_cast<const f4 *>(K + (size_t)t * kv_dim + e0);
+    const f4 *vs = reinterpret_cast<const f4 *>(V + (size_t)t * kv_dim + e0);
+    const f4 k0 = ks[0], k1 = ks[1], v0 = vs[0], v1 = vs[1];
+    float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    const int p0 = 4 * (c & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float2 q = cs[p0 + i];
+      rope_pair(kk[2 * i], kk[2 * i + 1], q.x, q.y);
+    }
+    h8 kh, vh;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kh[i] = (_Float16)kk[i];
+    vh[0] = (_Float16)v0.x; vh[1] = (_Float16)v0.y; vh[2] = (_Float16)v0.z; vh[3] = (_Float16)v0.w;
+    vh[4] = (_Float16)v1.x; vh[5] = (_Float16)v1.y; vh[6] = (_Float16)v1.z; vh[7] = (_Float16)v1.w;
+    *reinterpret_cast<h8 *>(kdst + drow * kv_dim + e0) = kh;
+    *reinterpret_cast<h8 *>(vdst + drow * kv_dim + e0) = vh;
   }
 }
 
@@ -129,19 +150,19 @@ hipError_t launch_rope(float *q, float *k, int S, int start_pos, const float *th
 
 hipError_t launch_rope_to_f16(const float *K, const float *V, const float *theta_inv, int S,
                               int start_pos, int n_kv, _Float16 *kdst, _Float16 *vdst,
-                              hipStream_t s) {
+                              float *cs_out, hipStream_t s) {
   if (S <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rope_kv_f16_kernel, dim3(S), dim3(64), 0, s, K, V, theta_inv, S, start_pos,
-                     n_kv, kdst, vdst, 1, false);
+  hipLaunchKernelGGL(rope_kv_f16_kernel, dim3(S), dim3(128), 0, s, K, V, theta_inv, S, start_pos,
+                     n_kv, kdst, vdst, 1, false, cs_out);
   return hipGetLastError();
 }
 
 hipError_t launch_rope_to_ring(const float *K, const float *V, const float *theta_inv, int S,
                                int start_pos, int n_kv, _Float16 *kc, _Float16 *vc, int max_seq,
-                               hipStream_t s) {
+                               float *cs_out, hipStream_t s) {
   if (S <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rope_kv_f16_kernel, dim3(S), dim3(64), 0, s, K, V, theta_inv, S, start_pos,
-                     n_kv, kc, vc, max_seq, true);
+  hipLaunchKernelGGL(rope_kv_f16_kernel, dim3(S), dim3(128), 0, s, K, V, theta_inv, S, start_pos,
+                     n_kv, kc, vc, max_seq, true, cs_out);
   return hipGetLastError();
 }
 

@@ -3,30 +3,38 @@
 // Replaces mistral/mistral_ane_prefill.h:207-275 (attention_batch) and, with
 // staged drafts, the sequential verify of mistral/speculative.h:92-101.
 //
-// Rows are (query t, head g) pairs of one kv head, row = t*G + g, so the G
-// query heads of a group share every K/V tile.  A workgroup holds SL row slabs
-// of 32 rows and KH key groups; wave w works on slab w % SL over the key range
-// of group w / SL, and the KH partial results are merged in LDS at the end.
-// K/V tiles go from global memory straight into LDS (global_load_lds, no
-// register staging), double-buffered per key group; the tile loop is software
-// pipelined so that the scores of tile i+1 are computed on MFMA while the
-// exponentials of tile i are formed.  Per 32-key tile:
-//   S^T[key][row] = K . Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS
-//                             (ds_read_b128), B = Q^T held in registers
-//   online softmax per row    each lane owns one row (the D column), so the
-//                             running max / sum / rescale stay lane-local
-//   O^T[dim][row] += V^T . P^T  P^T is the B operand straight from the S^T
-//                             accumulator (same key permutation on both
-//                             operands); V^T comes from the row-major V tile
-//                             by the transposing LDS read ds_read_b64_tr_b16.
+// Rows are (query t, head g) pairs of one kv head, row = 4t + g, so the four
+// query heads of a group share every K/V tile.  A workgroup owns RT = 32*NB
+// rows (NB = 2 for prefill: 16 queries x 4 heads) and has four waves, one per
+// SIMD.  Every wave works on all RT rows over its own quarter of the key range
+// (a key group), so K/V tiles are private to a wave: no barrier in the tile
+// loop, and each fp16 K/V byte read from LDS feeds 64 rows of MFMA work.  The
+// four partial results are merged through LDS at the end.
+//
+// Per wave and 32-key tile:
+//   K, V tiles        global -> LDS directly (global_load_lds, 16 B per lane),
+//                     double-buffered, issued one tile ahead of use
+//   S^T = K . Q^T     v_mfma_f32_32x32x16_f16, A = K rows (ds_read_b128),
+//                     B = Q^T held in registers (fp16, RoPE and scale applied)
+//   online softmax    one row per lane (the D column): running max and sum
+//                     stay lane-local; the two key halves of a row meet via
+//                     a lane exchange; P rounded to fp16 with v_cvt_pk and
+//                     summed in fp32 with v_dot2 (the same P feeds P.V)
+//   O^T += V^T . P^T  P^T straight from the S^T accumulator layout, V^T via
+//                     the transposing LDS read ds_read_b64_tr_b16
+// The scores of tile i+1 are computed on MFMA while the exponentials of tile
+// i are formed.  The running max moves lazily (only when a score exceeds it
+// by more than 8 in log2 units), so the accumulators are rarely rescaled.
+//
 // Query t at position start+t attends the window [pos-L+1, pos], L =
 // min(pos+1, max_seq) (mistral_ane_prefill.h:220-241); positions >= start come
 // from the staging buffer when one is given, which keeps the ring untouched
 // until the caller commits (sequential-verify semantics on a wrapped ring).
-// With p.theta_inv set, the adjacent-pair RoPE of Q (mistral_model.h:79-122)
-// is applied while the Q operand is built.  Masks are applied only to tiles
-// that cross a window edge of the slab.  Very long key ranges over few rows
-// are additionally split over workgroups and merged by a second kernel.
+// With p.rope_cs set, Q is rotated by the adjacent-pair RoPE of
+// mistral_model.h:79-122 using the per-position (cos, sin) table the K rotation
+// kernel wrote.  Masks are applied only to tiles that cross a window edge.
+// Very long key ranges over few rows are also split over workgroups and merged
+// by flash_merge_kernel.
 #include "mia_device.h"
 #include "mia_kernels.h"
 
@@ -34,24 +42,13 @@ namespace mia {
 
 namespace {
 
-constexpr int kKT = 32;         // keys per tile
-// K/V tiles live in LDS unpadded, one 256 B row per key, with the 16-byte
-// chunk c of row r stored at chunk c ^ swz(r): rows r..r+15 then hit distinct
-// bank groups for the K operand reads (same chunk, 16 rows), and the 4 rows x
-// 2 chunks of a transposing V read are distinct too.
-__device__ __forceinline__ int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+constexpr int kKT = 32;     // keys per tile
+constexpr int kWaves = 4;   // key groups per workgroup, one wave each
 
-template <int SL, int KH>
-struct FlashLayout {
-  static constexpr int kTileHalfs = kKT * HD;
-  // [KH][2 buffers][K, V] tiles
-  static constexpr size_t kTiles = (size_t)KH * 2 * 2 * kTileHalfs * sizeof(_Float16);
-  static constexpr size_t kRope = (size_t)8 * SL * 64 * sizeof(float2);
-  // after the loop the tile area holds [KH][SL][32 rows][HD] partial outputs
-  // and [KH][SL][32][2] (max, sum)
-  static constexpr size_t kMerge = (size_t)KH * SL * 32 * (HD + 2) * sizeof(float);
-  static constexpr size_t kBytes = (kTiles > kMerge ? kTiles : kMerge) + kRope;
-};
+// K/V/Q tiles live in LDS unpadded, one 256 B row per key (or query row),
+// with the 16-byte chunk c of row r stored at chunk c ^ swz(r): 16 rows read
+// at the same logical chunk then hit 16 distinct bank groups.
+__device__ __forceinline__ int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
 __device__ __forceinline__ int window_lo(int pos, int max_seq) {
   // pos - min(pos+1, M) + 1
@@ -59,95 +56,193 @@ __device__ __forceinline__ int window_lo(int pos, int max_seq) {
 }
 
 typedef short s4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 // LDS (address space 3) pointers: 32-bit addressing, no generic-pointer checks.
 typedef __attribute__((address_space(3))) _Float16 lds_half;
 typedef __attribute__((address_space(3))) s4 lds_s4;
 typedef __attribute__((address_space(3))) h8 lds_h8;
+typedef __attribute__((address_space(3))) u4 lds_u4;
+typedef __attribute__((address_space(3))) f4 lds_f4;
+typedef __attribute__((address_space(3))) f2 lds_f2;
+typedef __attribute__((address_space(3))) float lds_float;
 
-// Four consecutive keys k0..k0+3 of dim d0 + (lane % 16) from a swizzled
-// [key][128] fp16 tile: input lane i of each 16-lane group points at
-// (k0 + i/4, d0 + 4*(i%4)); the transposing read returns, in output lane j,
-// elements (k0 + e, d0 + j) for e = 0..3.
-__device__ __forceinline__ h4 read_vt4(lds_half *tile, int k0, int d0, int lane) {
-  const int i = lane & 15;
-  const int r = k0 + (i >> 2);
-  const int c = (d0 >> 3) + ((i & 3) >> 1);
-  lds_half *src = tile + r * HD + 8 * (c ^ swz(r)) + 4 * (i & 1);
-  s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)src);
-  return __builtin_bit_cast(h4, v);
+template <int NB>
+struct Lay {
+  static constexpr int kRows = 32 * NB;
+  static constexpr int kTileHalfs = kKT * HD;                  // 8 KB
+  static constexpr int kBufBytes = kWaves * 4 * kTileHalfs * 2;  // [wave][K0 K1 V0 V1]
+  static constexpr int kQBytes = kRows * HD * 2;               // fp16 Q rows
+  static constexpr int kMLBytes = kWaves * kRows * 8;          // (max, sum) per wave, row
+  // After the loop the tile buffers hold the foreign partial outputs:
+  // [NB*4 (block, dim block)][3 source waves][4 chunks][64 lanes][4 floats].
+  static constexpr int kMergeBytes = NB * 4 * 3 * 4 * 64 * 16;
+  static_assert(kMergeBytes <= kBufBytes, "merge area must fit the tile buffers");
+  static constexpr int kBytes = kBufBytes + kQBytes + kMLBytes;
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// 16 bytes per lane from global memory straight into LDS: lane i's data
-// lands at byte 16*i of the wave's 1 KB block at `l` (wave-uniform).  Inline
-// assembly, so that the compiler neither orders later LDS reads of the other
-// buffer behind it nor waits for it; completion is awaited explicitly (vmcnt)
-// before the workgroup barrier that publishes the tile.
-__device__ __forceinline__ void lds_dma16(const void *g, lds_half *l) {
-  const unsigned m = __builtin_amdgcn_readfirstlane((unsigned)(__UINTPTR_TYPE__)l);
+__device__ __forceinline__ unsigned lds_addr(lds_half *p) {
+  return __builtin_amdgcn_readfirstlane((unsigned)(__UINTPTR_TYPE__)p);
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane i's data lands
+// at byte 16*i of the 1 KB block at LDS byte address `m` (wave-uniform, taken
+// from M0, which is restored afterwards).  Inline assembly, so that the
+// compiler neither orders later LDS reads of the other buffer behind it nor
+// waits for it; completion is awaited explicitly with vmcnt.  The s_nop covers
+// the SALU-writes-M0 -> LDS-DMA wait state.
+__device__ __forceinline__ void dma16(const void *g, unsigned m) {
+  unsigned saved;
   asm volatile(
-      "s_mov_b32 m0, %1\n\t"
-      "global_load_lds_dwordx4 %0, off" ::"v"(g),
-      "s"(m)
-      : "m0");
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(m)
+      : "memory");
 }
 // Same with a wave-uniform base address and a per-lane 32-bit byte offset.
-__device__ __forceinline__ void lds_dma16_sb(const void *base, unsigned voff, lds_half *l) {
-  const unsigned m = __builtin_amdgcn_readfirstlane((unsigned)(__UINTPTR_TYPE__)l);
+__device__ __forceinline__ void dma16_sb(const void *base, unsigned voff, unsigned m) {
+  unsigned saved;
   asm volatile(
-      "s_mov_b32 m0, %2\n\t"
-      "global_load_lds_dwordx4 %0, %1" ::"v"(voff),
-      "s"(base), "s"(m)
-      : "m0");
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(base), "s"(m)
+      : "memory");
 }
 
-// Issues this wave's share of the direct loads of one tensor (K or V) of the
-// 32-key tile kb..kb+31 (range ending at ke) into the tile buffer dst.  A tile
-// of 32 consecutive ring slots takes a uniform base plus the lane's constant
-// offset; tiles that wrap or reach into the staging buffer take per-lane
-// addresses.
-template <int IPW, int SL>
-__device__ __forceinline__ void load_tensor(const _Float16 *ring, const _Float16 *stage, int kb,
-                                            int ke, int start_pos, int max_seq, int kv_dim,
-                                            const int *lane_row, const int *lane_off,
-                                            const unsigned *lane_boff, int slab, lds_half *dst) {
-  const bool full = kb + kKT <= ke;
-  const int slot0 = kb % max_seq;  // uniform, once per tile
+// Issues the 8 direct loads of one tensor (K or V) of the 32-key tile kb..kb+31
+// (key range ending at ke) into the wave's tile at LDS byte address dst.
+// Instruction j moves keys 4j..4j+3: lane i fetches key 4j + i/16, logical
+// chunk (i%16) ^ swz(key), which the hardware writes at byte 16*i of the
+// instruction's 1 KB block.  swz(4j + i/16) only depends on j through j mod 4,
+// so a tile of 32 consecutive ring slots takes a uniform base (row 4j) plus one
+// of four per-lane offsets boff[j % 4]; tiles that wrap, end early or reach
+// into the staging buffer take per-lane addresses.
+__device__ __forceinline__ void load_tile(const _Float16 *ring, const _Float16 *stage, int kb,
+                                          int ke, int start_pos, int max_seq, int kv_dim,
+                                          int kv_off, const unsigned *boff, int lane,
+                                          unsigned dst) {
+  const int slot0 = kb % max_seq;
   const bool contiguous =
-      full && slot0 + kKT <= max_seq && (stage == nullptr || kb + kKT <= start_pos);
+      kb + kKT <= ke && slot0 + kKT <= max_seq && (stage == nullptr || kb + kKT <= start_pos);
   if (contiguous) {
     const _Float16 *base = ring + (size_t)slot0 * kv_dim;
 #pragma unroll
-    for (int j = 0; j < IPW; ++j) lds_dma16_sb(base, lane_boff[j], dst + (slab + SL * j) * 4 * HD);
+    for (int j = 0; j < 8; ++j)
+      dma16_sb(base + (size_t)4 * j * kv_dim, boff[j & 3], dst + 1024u * j);
     return;
   }
+  // kb through readfirstlane: keeps the per-lane keys of this rare path from
+  // being strength-reduced into loop-carried registers.
+  const int kbu = __builtin_amdgcn_readfirstlane(kb);
 #pragma unroll
-  for (int j = 0; j < IPW; ++j) {
-    const int r = lane_row[j];
-    const int kp = min(kb + r, ke - 1);
-    const bool staged = stage != nullptr && kp >= start_pos;
-    int slot = slot0 + (kp - kb);
-    slot = slot >= max_seq ? slot - max_seq : slot;
-    const _Float16 *src = (staged ? stage : ring) +
-                          (size_t)(staged ? kp - start_pos : slot) * kv_dim + lane_off[j];
-    lds_dma16(src, dst + (slab + SL * j) * 4 * HD);
+  for (int j = 0; j < 8; ++j) {
+    const int r = 4 * j + (lane >> 4);
+    const int kp = min(kbu + r, ke - 1);
+    const _Float16 *src;
+    if (stage != nullptr && kp >= start_pos) {
+      src = stage + (size_t)(kp - start_pos) * kv_dim;
+    } else {
+      int slot = slot0 + (kp - kbu);
+      slot = max_seq >= kKT ? (slot >= max_seq ? slot - max_seq : slot) : slot % max_seq;
+      src = ring + (size_t)slot * kv_dim;
+    }
+    dma16(src + kv_off + 8 * ((lane & 15) ^ swz(r)), dst + 1024u * j);
   }
 }
 
-template <int G, int SL, int KH>
-__global__ void __launch_bounds__(64 * SL * KH) flash_kernel(FlashParams p) {
-  using Lay = FlashLayout<SL, KH>;
-  constexpr int NW = SL * KH;
-  constexpr int RT = 32 * SL;     // rows per workgroup
-  constexpr int QT = RT / G;      // queries per workgroup
+__device__ __forceinline__ h8 lds_read_h8(unsigned addr) {
+  return *(const lds_h8 *)(__UINTPTR_TYPE__)addr;
+}
+__device__ __forceinline__ h4 lds_read_tr4(unsigned addr) {
+  return __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)(__UINTPTR_TYPE__)addr));
+}
+
+// Operand reads from a swizzled tile.  The swizzle XORs disjoint bit fields
+// of the byte address, so every read is a per-lane base XOR a compile-time
+// constant (plus an immediate offset), one VALU op instead of a register.
+//  K (A operand of S^T = K.Q^T), k-step st: row = col, logical chunk
+//    2*st + half -> byte ka_base ^ (st << 5), with
+//    ka_base = tile + col*256 + 16*(half ^ bit3(col)) + 32*(col & 7).
+//  V^T (A operand of O^T += V^T.P^T), k-step kst, dim block db, key half hi:
+//    the transposing read of keys 16*kst + 8*hi + 4*half + (i/4) (i = lane%16)
+//    at dims 32*db + 16*bit4(lane) + 4*(i%4) -> byte
+//    (va_base ^ (64*db ^ 16*hi)) + 2048*hi + 4096*kst, with
+//    va_base = tile + 256*u + 8*(i&1) + 16*((2*bit4(lane) + (i&3)/2) ^ 2u),
+//    u = 4*half + i/4.
+__device__ __forceinline__ unsigned ka_lane_base(int lane) {
+  const int col = lane & 31, half = lane >> 5;
+  return (unsigned)(col * 256 + 16 * (half ^ ((col >> 3) & 1)) + 32 * (col & 7));
+}
+__device__ __forceinline__ unsigned va_lane_base(int lane) {
+  const int i = lane & 15, half = lane >> 5, l4 = (lane >> 4) & 1;
+  const int u = 4 * half + (i >> 2);
+  const int c_lane = 2 * l4 + ((i & 3) >> 1);
+  return (unsigned)(256 * u + 8 * (i & 1) + 16 * (c_lane ^ (2 * u)));
+}
+// V^T operand (8 keys x this lane's dim) for k-step kst and dim block db:
+// keys {0-3, 8-11} + 4*half of the step, the S^T accumulator's key order.
+template <int KST, int DB>
+__device__ __forceinline__ h8 read_va(unsigned va_base) {
+  const unsigned b0 = va_base ^ (64u * DB);
+  const unsigned b1 = va_base ^ (64u * DB ^ 16u);
+  const h4 lo = lds_read_tr4(b0 + 4096u * KST);
+  const h4 hi = lds_read_tr4(b1 + 4096u * KST + 2048u);
+  return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// O^T += V^T . P^T with the accumulator pinned to AGPRs ("+a"): the 128
+// output accumulators of a 64-row wave then stay out of the VGPR file, which
+// holds the scores, the Q operands and prefetched LDS operands instead.  The
+// leading s_nop covers a VALU write of the P operand just before (the hazard
+// recognizer does not look inside inline assembly).
+__device__ __forceinline__ void mfma_pv(f16v &acc, const h8 &a, const h8 &b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// acc = 0 through the MFMA itself (0 x 0 + 0), so the accumulators are only
+// ever written by AGPR-destination MFMAs.
+__device__ __forceinline__ void mfma_zero(f16v &acc, const h8 &z) {
+  asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %1, 0" : "=a"(acc) : "v"(z));
+}
+// Before VALU reads of accumulators written by mfma_pv: the MFMA result
+// latency (wait states the compiler cannot see), and a data dependence on
+// every accumulator so that no read is scheduled above it.
+template <int NB>
+__device__ __forceinline__ void pv_drain(f16v (&o)[NB][4]) {
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+                 : "+a"(o[b][0]), "+a"(o[b][1]), "+a"(o[b][2]), "+a"(o[b][3]));
+}
+
+// Combine the two key halves of a row (lanes l and l^32).  ds_bpermute via
+// __shfl_xor: clang folds v_permlane32_swap with identical operands as if
+// both results were the input, so that builtin is not used here.
+__device__ __forceinline__ float half_swap_max(float m) { return fmaxf(m, __shfl_xor(m, 32)); }
+__device__ __forceinline__ float half_swap_sum(float x) { return x + __shfl_xor(x, 32); }
+
+template <int NB>
+__global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
+  using L = Lay<NB>;
+  constexpr int RT = 32 * NB;  // rows per workgroup
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  lds_half *tiles = (lds_half *)smem;
-  float2 *rope = reinterpret_cast<float2 *>(smem + (Lay::kBytes - Lay::kRope));
+  lds_half *lds = (lds_half *)smem;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  const int slab = w % SL;
-  const int kg = w / SL;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // key group
   const int half = lane >> 5;
   const int col = lane & 31;
   const int kvh = blockIdx.x % p.n_kv;
@@ -155,290 +250,390 @@ __global__ void __launch_bounds__(64 * SL * KH) flash_kernel(FlashParams p) {
   const int rtile = rest % p.n_rtiles;
   const int split = rest / p.n_rtiles;
   const int kv_dim = p.n_kv * HD;
-  const int dim_model = p.n_kv * G * HD;
-
-  // This lane's row and its window.
+  const int dim_model = kv_dim * 4;
   const int row0 = rtile * RT;
-  const int row = row0 + slab * 32 + col;
-  const int t = row / G;
-  const int g = row % G;
-  const bool row_valid = t < p.S;
-  const int pos_t = p.start_pos + (row_valid ? t : p.S - 1);
-  const int lo_t = window_lo(pos_t, p.max_seq);
-  const int hi_t = pos_t;
-  // Slab-uniform bounds: keys in [lo_max, hi_min] are inside every row's window.
-  const int ts0 = (row0 + slab * 32) / G;
-  const int ts1 = (row0 + slab * 32 + 31) / G;
-  const bool slab_full = ts1 < p.S;
-  const int lo_max = window_lo(p.start_pos + min(ts1, p.S - 1), p.max_seq);
-  const int hi_min = p.start_pos + ts0;
 
-  // Key range of the workgroup (one split), then of this key group.
-  const int tq0 = row0 / G;
-  const int tq1 = min((row0 + RT - 1) / G, p.S - 1);
+  // Key range of the workgroup (one split), then of this wave.
+  const int tq0 = row0 >> 2;
+  const int tq1 = min(tq0 + RT / 4 - 1, p.S - 1);
   const int klo = window_lo(p.start_pos + tq0, p.max_seq);
   const int khi = p.start_pos + tq1;
   const int ks = klo + split * p.split_keys;
   const int ke = min(ks + p.split_keys, khi + 1);
   const int nt = ke > ks ? (ke - ks + kKT - 1) / kKT : 0;
-  const int g_first = (int)((long)kg * nt / KH);
-  const int g_count = (int)((long)(kg + 1) * nt / KH) - g_first;
-  const int n_iter = (nt + KH - 1) / KH;
+  const int g_first = (int)((long)w * nt / kWaves);
+  const int g_count = (int)((long)(w + 1) * nt / kWaves) - g_first;
+  const int kb0 = ks + kKT * g_first;
 
-  // Tile buffers (per key group: K ring and V ring of 2) and this lane's
-  // share of the direct loads.  One wave instruction moves 4 keys (64 lanes x
-  // 16 B); the SL waves of a key group share the 8 instructions per tensor of
-  // a 32-key tile.  Lane i of instruction j loads key row 4j + i/16, logical
-  // chunk (i%16) ^ swz(row), which the hardware writes at byte 16*i of the
-  // instruction's 1 KB block.
-  constexpr int IPW = (kKT / 4) / SL;  // instructions per wave per tensor
-  lds_half *ktile[2], *vtile[2];
+  // This lane's row in each 32-row block and its window; block-uniform bounds
+  // (keys in [lo_max, hi_min] are inside every row's window of the block).
+  int lo_t[NB], hi_t[NB], lo_max[NB], hi_min[NB];
+  bool valid[NB], bfull[NB];
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    ktile[b] = tiles + ((size_t)(kg * 2 + b) * 2 + 0) * Lay::kTileHalfs;
-    vtile[b] = tiles + ((size_t)(kg * 2 + b) * 2 + 1) * Lay::kTileHalfs;
+  for (int b = 0; b < NB; ++b) {
+    const int t = (row0 + 32 * b + col) >> 2;
+    valid[b] = t < p.S;
+    const int pos_t = p.start_pos + (valid[b] ? t : p.S - 1);
+    lo_t[b] = window_lo(pos_t, p.max_seq);
+    hi_t[b] = pos_t;
+    const int ts0 = (row0 + 32 * b) >> 2;
+    const int ts1 = (row0 + 32 * b + 31) >> 2;
+    bfull[b] = ts1 < p.S;
+    lo_max[b] = window_lo(p.start_pos + min(ts1, p.S - 1), p.max_seq);
+    hi_min[b] = p.start_pos + ts0;
   }
-  int lane_row[IPW], lane_off[IPW];
-  unsigned lane_boff[IPW];  // byte offset from the tile's first slot
+
+  // Wave-private tile buffers and this lane's direct-load offsets.
+  lds_half *kt[2], *vt[2];
 #pragma unroll
-  for (int j = 0; j < IPW; ++j) {
-    const int r = 4 * (slab + SL * j) + (lane >> 4);
-    lane_row[j] = r;
-    lane_off[j] = kvh * HD + 8 * ((lane & 15) ^ swz(r));
-    lane_boff[j] = (unsigned)(r * kv_dim + lane_off[j]) * 2u;
+  for (int s = 0; s < 2; ++s) {
+    kt[s] = lds + (w * 4 + s) * L::kTileHalfs;
+    vt[s] = lds + (w * 4 + 2 + s) * L::kTileHalfs;
   }
+  const unsigned kt_a[2] = {lds_addr(kt[0]), lds_addr(kt[1])};
+  const unsigned vt_a[2] = {lds_addr(vt[0]), lds_addr(vt[1])};
+  unsigned boff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 4 * j + (lane >> 4);
+    boff[j] = (unsigned)(r * kv_dim + kvh * HD + 8 * ((lane & 15) ^ swz(r))) * 2u -
+              (unsigned)(4 * j * kv_dim) * 2u;
+  }
+  const unsigned ka_b[2] = {kt_a[0] + ka_lane_base(lane), kt_a[1] + ka_lane_base(lane)};
+  const unsigned va_b[2] = {vt_a[0] + va_lane_base(lane), vt_a[1] + va_lane_base(lane)};
   const _Float16 *const kc = p.kc, *const vc = p.vc;
   const _Float16 *const kst = p.kstage, *const vst = p.vstage;
-  const int kb0 = ks + kKT * g_first;  // first key of this group's tile 0
-#define MIA_LOAD_K(i, buf)                                                                    \
-  load_tensor<IPW, SL>(kc, kst, kb0 + kKT * (i), ke, p.start_pos, p.max_seq, kv_dim, lane_row, \
-                       lane_off, lane_boff, slab, ktile[buf])
-#define MIA_LOAD_V(i, buf)                                                                    \
-  load_tensor<IPW, SL>(vc, vst, kb0 + kKT * (i), ke, p.start_pos, p.max_seq, kv_dim, lane_row, \
-                       lane_off, lane_boff, slab, vtile[buf])
-  // K of tiles 0 and 1 and V of tile 0 go out before the query loads.
-  if (g_count > 0) {
-    MIA_LOAD_K(0, 0);
-    MIA_LOAD_V(0, 0);
-  }
-  if (g_count > 1) MIA_LOAD_K(1, 1);
-
-  // RoPE (cos, sin) for the workgroup's queries, fl32(theta_inv[i] * pos) as
-  // vDSP_vsmul (mistral_model.h:87-88).
-  if (p.theta_inv != nullptr) {
-    for (int i = tid; i < QT * 64; i += 64 * NW) {
-      const int qi = i >> 6, pr = i & 63;
-      const int tq = min(tq0 + qi, p.S - 1);
-      float ang = p.theta_inv[pr] * (float)(p.start_pos + tq);
-      float sn, cs;
-      sincosf(ang, &sn, &cs);
-      rope[i] = make_float2(cs, sn);
+#define MIA_LOAD_K(i, buf)                                                                       \
+  load_tile(kc, kst, kb0 + kKT * (i), ke, p.start_pos, p.max_seq, kv_dim, kvh * HD, boff, lane, \
+            kt_a[buf])
+#define MIA_LOAD_V(i, buf)                                                                       \
+  load_tile(vc, vst, kb0 + kKT * (i), ke, p.start_pos, p.max_seq, kv_dim, kvh * HD, boff, lane, \
+            vt_a[buf])
+  auto issue_first_tiles = [&]() {
+    if (g_count > 0) {
+      MIA_LOAD_K(0, 0);
+      MIA_LOAD_V(0, 0);
     }
-    __syncthreads();
-  }
+    if (g_count > 1) MIA_LOAD_K(1, 1);
+  };
+  issue_first_tiles();
 
-  // Q^T operand: col = row, k-step st covers dims 16*st + 8*half .. +8.
-  h8 qb[8];
-  {
-    const float *qsrc = p.Q + (size_t)(row_valid ? t : 0) * dim_model + (size_t)(kvh * G + g) * HD;
-    const float2 *rt = rope + (row_valid ? t - tq0 : 0) * 64;
-#pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      const f4 *src = reinterpret_cast<const f4 *>(qsrc + 16 * st + 8 * half);
-      f4 a = src[0], b = src[1];
+  // Q rows -> fp16 in LDS, 8 dims per item: RoPE (table of fl32(theta_inv[i] *
+  // pos) cos/sin written by the K rotation, mistral_model.h:87-105) and the
+  // score scale folded in.  Rows past the last query are zero.
+  lds_half *qs = lds + L::kBufBytes / 2;
+  for (int u = tid; u < RT * 16; u += 256) {
+    const int rl = u >> 4, ch = u & 15;
+    const int row = row0 + rl;
+    const int t = row >> 2, g = row & 3;
+    u4 packed = {0u, 0u, 0u, 0u};
+    if (t < p.S) {
+      const f4 *src = reinterpret_cast<const f4 *>(p.Q + (size_t)t * dim_model +
+                                                   (size_t)(kvh * 4 + g) * HD + 8 * ch);
+      const f4 a = src[0], b = src[1];
       float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-      if (p.theta_inv != nullptr) {
-#pragma unroll
-        for (int pi = 0; pi < 4; ++pi) {
-          float2 cs = rt[8 * st + 4 * half + pi];
-          rope_pair(v[2 * pi], v[2 * pi + 1], cs.x, cs.y);
-        }
+      if (p.rope_cs != nullptr) {
+        const f4 *cs = reinterpret_cast<const f4 *>(p.rope_cs + ((size_t)t * 64 + 4 * ch) * 2);
+        const f4 c0 = cs[0], c1 = cs[1];
+        rope_pair(v[0], v[1], c0.x, c0.y);
+        rope_pair(v[2], v[3], c0.z, c0.w);
+        rope_pair(v[4], v[5], c1.x, c1.y);
+        rope_pair(v[6], v[7], c1.z, c1.w);
       }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qb[st][e] = (_Float16)(row_valid ? v[e] * p.qscale : 0.f);
+      for (int e = 0; e < 4; ++e)
+        packed[e] = __builtin_bit_cast(
+            unsigned, __builtin_convertvector(
+                          (f2){v[2 * e] * p.qscale, v[2 * e + 1] * p.qscale}, h2));
     }
+    *(lds_u4 *)(qs + rl * HD + 8 * (ch ^ swz(rl))) = packed;
   }
-
-  f16v o[4];
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
-
-  // S^T block of one tile: keys x this slab's 32 rows; s[i] is key
-  // kb + (i/4)*8 + 4*half + (i%4) for row `row`.
-  auto qk = [&](lds_half *kt) {
-    f16v s;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.f;
-#pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      h8 a = *(lds_h8 *)(kt + col * HD + 8 * ((2 * st + half) ^ swz(col)));
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[st], s, 0, 0, 0);
-    }
-    return s;
-  };
-  // Window mask (only for tiles crossing a window edge of the slab) and the
-  // row max over the tile.
-  auto mask_max = [&](f16v &s, int kb) {
-    const bool inside = slab_full && kb >= lo_max && kb + kKT - 1 <= hi_min && kb + kKT <= ke;
-    if (!inside) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = kb + (i >> 2) * 8 + 4 * half + (i & 3);
-        const bool ok = row_valid && key >= lo_t && key <= hi_t && key < ke;
-        s[i] = ok ? s[i] : -INFINITY;
-      }
-    }
-    float m = s[0];
-#pragma unroll
-    for (int i = 1; i < 16; ++i) m = fmaxf(m, s[i]);
-    return fmaxf(m, __shfl_xor(m, 32));
-  };
-
-  // Software pipeline over this group's tiles: iteration it holds the masked
-  // scores of tile it (s_cur, row max m_cur), computes the scores of tile
-  // it+1 on MFMA while the exponentials of tile it are formed, then adds
-  // P.V of tile it.  Buffers: K(i) in ktile[i&1], V(i) in vtile[i&1]; during
-  // iteration it the loads of K(it+2) and V(it+1) are in flight.
-  asm volatile("s_waitcnt vmcnt(0)");
   __syncthreads();
-  f16v s_cur = qk(ktile[0]);
-  float m_cur = mask_max(s_cur, kb0);
 
-  for (int it = 0; it < n_iter; ++it) {
-    // this wave's loads of K(it+1) and V(it) have landed; after the barrier
-    // every wave's have, and every wave is done with K(it) and V(it-1)
-    asm volatile("s_waitcnt vmcnt(0)");
-    __syncthreads();
-    if (it + 2 < g_count) MIA_LOAD_K(it + 2, it & 1);
-    if (it + 1 < g_count) MIA_LOAD_V(it + 1, (it + 1) & 1);
-    if (it < g_count) {
-      // Lazy rescale: m_run is the reference max of the row's exponentials
-      // and moves only when a score exceeds it by more than 8 (log2 domain),
-      // so every p = 2^(s - m_run) stays <= 256 (exact range for fp16) and
-      // the accumulators are rescaled rarely.  Normalisation by l at the end
-      // is unaffected by the choice of reference.
-      const bool move = m_cur > m_run + 8.0f;
-      if (__ballot(move) != 0) {  // wave-uniform
-        // rows that do not move keep alpha = 1 (also while still fully
-        // masked, m_run = -inf); the first move of a row gives alpha = 0
-        const float alpha = move ? fast_exp2(m_run - m_cur) : 1.0f;
-        const float m_ref = move ? m_cur : m_run;
-        l_run *= alpha;
+  // Q^T operands: column = row, k-step st covers dims 16*st + 8*half .. +8.
+  h8 qb[NB][8];
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
+  for (int b = 0; b < NB; ++b)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-        m_run = m_ref;
-      }
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;
-      // All LDS operands of the iteration are requested up front: K of tile
-      // it+1 (stale, unused data when it+1 == g_count) and V^T of tile it.
-      lds_half *kt = ktile[(it + 1) & 1];
-      lds_half *vt = vtile[it & 1];
-      h8 ka[8];
+    for (int st = 0; st < 8; ++st)
+      qb[b][st] = *(lds_h8 *)(qs + (32 * b + col) * HD + 8 * ((2 * st + half) ^ swz(col)));
+
+  // Softmax reference per row: fixed at the first tile with a finite score
+  // (so p <= 1 there) instead of a running max, so the accumulators are never
+  // rescaled inside the loop.  A later score more than 15 (log2 units) above
+  // it would overflow the fp16 P operand (2^15 is exact; fp16 ends at 65504):
+  // such a wave marks overflow and runs its key range once more with the
+  // true row max, which it tracks, as the reference.
+  f16v o[NB][4];
+  float m_ref[NB], m_max[NB], l_run[NB], m_cur[NB];
+  f16v s_cur[NB];
 #pragma unroll
-      for (int st = 0; st < 8; ++st)
-        ka[st] = *(lds_h8 *)(kt + col * HD + 8 * ((2 * st + half) ^ swz(col)));
-      // O^T += V^T P^T; k-step kst covers keys 16*kst .. +16, this half's 8
-      // keys being {0-3, 8-11} + 4*half (the S^T row permutation).
-      h8 va[2][4];
-#pragma unroll
-      for (int kst = 0; kst < 2; ++kst) {
-        const int k0 = 16 * kst + 4 * half;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-          const int d0 = 32 * db + 16 * ((lane >> 4) & 1);
-          h4 lo = read_vt4(vt, k0, d0, lane);
-          h4 hi = read_vt4(vt, k0 + 8, d0, lane);
-          va[kst][db] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-      }
-      h8 pb[2];  // P^T B operands for keys 0..15 and 16..31 of the tile
-      float lsum = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float pv = fast_exp2(s_cur[i] - m_use);
-        lsum += pv;
-        pb[i >> 3][i & 7] = (_Float16)pv;
-      }
-      l_run += lsum;
-      f16v s_next;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s_next[i] = 0.f;
-#pragma unroll
-      for (int st = 0; st < 8; ++st)
-        s_next = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[st], s_next, 0, 0, 0);
-#pragma unroll
-      for (int kst = 0; kst < 2; ++kst)
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[kst][db], pb[kst], o[db], 0, 0, 0);
-      m_cur = mask_max(s_next, kb0 + kKT * (it + 1));
-      s_cur = s_next;
-    }
+  for (int b = 0; b < NB; ++b) {
+    m_ref[b] = -INFINITY;
+    m_max[b] = -INFINITY;
   }
-#undef MIA_LOAD_K
-#undef MIA_LOAD_V
-  __syncthreads();  // the merge below reuses the tile area
+  const h8 zero8 = {};
 
-  // Merge the KH key groups (LDS; the tile area is free after the loop).
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  float *mo = reinterpret_cast<float *>(smem);             // [KH][SL][32][HD]
-  float *mml = mo + (size_t)KH * SL * 32 * HD;              // [KH][SL][32][2]
-  {
-    float *dst = mo + ((size_t)(kg * SL + slab) * 32 + col) * HD;
+  // Tile kb needs masking unless every key is inside every row's window.
+  auto needs_mask = [&](int kb) {
+    bool m = kb + kKT > ke;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      m = m || !bfull[b] || kb < lo_max[b] || kb + kKT - 1 > hi_min[b];
+    return m;
+  };
+  // Keys outside the row's window become -inf; s[i] is key
+  // kb + (i/4)*8 + 4*half + (i%4) for the lane's row.
+  auto mask_block = [&](f16v &s, int b, int kb) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = kb + (i >> 2) * 8 + 4 * half + (i & 3);
+      const bool ok = valid[b] && key >= lo_t[b] && key <= hi_t[b] && key < ke;
+      s[i] = ok ? s[i] : -INFINITY;
+    }
+  };
+  // Row max of a score block over both key halves.
+  auto block_max = [&](const f16v &s) {
+    float m = fmaxf(s[0], s[1]);
+#pragma unroll
+    for (int i = 2; i < 16; i += 2) m = fmaxf(m, fmaxf(s[i], s[i + 1]));
+    return half_swap_max(m);
+  };
+
+  const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+  // One tile step: P of tile it from s_cur, scores of tile it+1 into s_cur,
+  // O += P.V of tile it.  K(it+1) is in kt[(it+1)&1], V(it) in vt[it&1].  The
+  // K and V operands are streamed in halves (k-steps 0-3 / 4-7, keys 0-15 /
+  // 16-31) to keep the register footprint within one wave per SIMD.
+  auto step = [&](int it) {
+    float m_use[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) m_use[b] = m_ref[b] == -INFINITY ? 0.f : m_ref[b];
+    const unsigned kab = ka_b[(it + 1) & 1];
+    const unsigned vab = va_b[it & 1];
+    h8 ka[4], va[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) ka[st] = lds_read_h8(kab ^ (unsigned)(st << 5));
+    va[0] = read_va<0, 0>(vab);
+    va[1] = read_va<0, 1>(vab);
+    va[2] = read_va<0, 2>(vab);
+    va[3] = read_va<0, 3>(vab);
+    // P^T operands (keys 0..15 and 16..31 of the tile) and row sums.
+    h8 pb[NB][2];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      u4 pw[2];
+      float ls = l_run[b];
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        const float p0 = fast_exp2(s_cur[b][i] - m_use[b]);
+        const float p1 = fast_exp2(s_cur[b][i + 1] - m_use[b]);
+        const h2 pp = __builtin_convertvector((f2){p0, p1}, h2);
+        ls = __builtin_amdgcn_fdot2(pp, ones, ls, false);
+        pw[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(unsigned, pp);
+      }
+      l_run[b] = ls;
+      pb[b][0] = __builtin_bit_cast(h8, pw[0]);
+      pb[b][1] = __builtin_bit_cast(h8, pw[1]);
+    }
+    f16v s_next[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s_next[b][i] = 0.f;
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+        s_next[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st], s_next[b], 0, 0, 0);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) ka[st] = lds_read_h8(kab ^ (unsigned)((st + 4) << 5));
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4)
-        *reinterpret_cast<f4 *>(dst + 32 * db + 8 * i4 + 4 * half) =
-            f4{o[db][4 * i4 + 0], o[db][4 * i4 + 1], o[db][4 * i4 + 2], o[db][4 * i4 + 3]};
-    if (half == 0)
-      *reinterpret_cast<float2 *>(mml + ((size_t)(kg * SL + slab) * 32 + col) * 2) =
-          make_float2(m_run, l_tot);
-  }
-  __syncthreads();
+      for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pb[b][0]);
+    va[0] = read_va<1, 0>(vab);
+    va[1] = read_va<1, 1>(vab);
+    va[2] = read_va<1, 2>(vab);
+    va[3] = read_va<1, 3>(vab);
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+        s_next[b] =
+            __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st + 4], s_next[b], 0, 0, 0);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pb[b][1]);
+    // Window mask of tile it+1, only where it crosses a window edge.
+    const int kbn = kb0 + kKT * (it + 1);
+    if (needs_mask(kbn)) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) mask_block(s_next[b], b, kbn);
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      m_cur[b] = block_max(s_next[b]);
+      s_cur[b] = s_next[b];
+    }
+  };
 
-  // Thread -> (row, 4 dims) items of the workgroup's RT rows.
-  const size_t tile_id = (size_t)kvh * p.n_rtiles + rtile;
-  for (int itm = tid; itm < RT * (HD / 4); itm += 64 * NW) {
-    const int rl = itm / (HD / 4), d4 = itm % (HD / 4);
-    const int sl = rl / 32, rr = rl % 32;
-    const int rrow = row0 + rl;
-    const int tt = rrow / G, gg = rrow % G;
-    if (tt >= p.S) continue;
+  for (int pass = 0; pass < 2; ++pass) {
+    if (pass == 1) {
+      issue_first_tiles();
+#pragma unroll
+      for (int b = 0; b < NB; ++b) m_ref[b] = m_max[b];
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) mfma_zero(o[b][db], zero8);
+      l_run[b] = 0.f;
+      m_cur[b] = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s_cur[b][i] = -INFINITY;
+    }
+    // The first tile's scores.
+    if (g_count > 0) {
+      if (g_count > 1) wait_vmcnt<16>();
+      else wait_vmcnt<8>();
+      h8 ka[8];
+#pragma unroll
+      for (int st = 0; st < 8; ++st) ka[st] = lds_read_h8(ka_b[0] ^ (unsigned)(st << 5));
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s_cur[b][i] = 0.f;
+#pragma unroll
+        for (int st = 0; st < 8; ++st)
+          s_cur[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st], s_cur[b], 0, 0, 0);
+      }
+      if (needs_mask(kb0)) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) mask_block(s_cur[b], b, kb0);
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) m_cur[b] = block_max(s_cur[b]);
+    }
+
+    bool ovf = false;
+    for (int it = 0; it < g_count; ++it) {
+      // Buffers of K(it) and V(it-1) were consumed by the previous step:
+      // refill them with K(it+2) and V(it+1), then wait for K(it+1) and V(it).
+      const bool more1 = it + 1 < g_count, more2 = it + 2 < g_count;
+      if (more2) MIA_LOAD_K(it + 2, it & 1);
+      if (more1) MIA_LOAD_V(it + 1, (it + 1) & 1);
+      if (more2) wait_vmcnt<16>();
+      else if (more1) wait_vmcnt<8>();
+      else wait_vmcnt<0>();
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        m_ref[b] = m_ref[b] == -INFINITY ? m_cur[b] : m_ref[b];
+        m_max[b] = fmaxf(m_max[b], m_cur[b]);
+        ovf = ovf || m_cur[b] > m_ref[b] + 15.0f;
+      }
+      step(it);
+    }
+    if (__builtin_amdgcn_ballot_w64(ovf) == 0) break;
+  }
+#undef MIA_LOAD_K
+#undef MIA_LOAD_V
+
+  // ---- merge of the four key groups ----
+  pv_drain<NB>(o);
+  // (max, sum) of every row per wave; the sum covers both key halves.
+  lds_float *ml = (lds_float *)(smem + L::kBufBytes + L::kQBytes);  // [wave][RT][2]
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float lt = half_swap_sum(l_run[b]);
+    if (half == 0)
+      *(lds_f2 *)(ml + (w * RT + 32 * b + col) * 2) =
+          (f2){m_ref[b], lt};
+  }
+  __syncthreads();  // every wave is past its loop: tile buffers are free
+
+  float Mx[NB], Lsum[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    f2 mlw[kWaves];
     float M = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < KH; ++k) M = fmaxf(M, mml[((size_t)(k * SL + sl) * 32 + rr) * 2]);
-    const float Mu = M == -INFINITY ? 0.f : M;
-    float Ls = 0.f;
-    f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int k = 0; k < KH; ++k) {
-      const size_t r = (size_t)(k * SL + sl) * 32 + rr;
-      const float2 ml = *reinterpret_cast<const float2 *>(mml + r * 2);
-      const float e = fast_exp2(ml.x - Mu);
-      Ls = __builtin_fmaf(e, ml.y, Ls);
-      acc += e * *reinterpret_cast<const f4 *>(mo + r * HD + 4 * d4);
+    for (int k = 0; k < kWaves; ++k) {
+      mlw[k] = *(lds_f2 *)(ml + (k * RT + 32 * b + col) * 2);
+      M = fmaxf(M, mlw[k].x);
     }
-    if (p.nsplit == 1) {
-      *reinterpret_cast<f4 *>(p.out + (size_t)tt * dim_model + (size_t)(kvh * G + gg) * HD +
-                              4 * d4) = acc * (1.0f / Ls);
-    } else {
-      const size_t pidx = (tile_id * p.nsplit + split) * RT + rl;
-      *reinterpret_cast<f4 *>(p.part_o + pidx * HD + 4 * d4) = acc;
-      if (d4 == 0) *reinterpret_cast<float2 *>(p.part_ml + pidx * 2) = make_float2(M, Ls);
+    float Ls = 0.f, e_own = 0.f;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) {
+      const float e = mlw[k].x == -INFINITY ? 0.f : fast_exp2(mlw[k].x - M);
+      Ls = __builtin_fmaf(e, mlw[k].y, Ls);
+      if (k == w) e_own = e;
+    }
+    Mx[b] = M;
+    Lsum[b] = Ls;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[b][db][i] *= e_own;
+  }
+
+  // Wave w finalises dim block db = w of every row block; the other three
+  // dim blocks go to their owners through LDS, lane-linear (conflict-free).
+  lds_float *mg = (lds_float *)smem;
+  auto mg_at = [&](int c, int slot, int q) { return mg + ((((c * 3 + slot) * 4 + q) * 64 + lane) * 4); };
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      if (db == w) continue;
+      const int slot = w < db ? w : w - 1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *(lds_f4 *)mg_at(b * 4 + db, slot, q) =
+            (f4){o[b][db][4 * q], o[b][db][4 * q + 1], o[b][db][4 * q + 2], o[b][db][4 * q + 3]};
+    }
+  __syncthreads();
+
+  const size_t tile_id = (size_t)kvh * p.n_rtiles + rtile;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int rl = 32 * b + col;
+    const int row = row0 + rl;
+    const int t = row >> 2, g = row & 3;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      if (db != w) continue;
+      f4 acc[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[q] = (f4){o[b][db][4 * q], o[b][db][4 * q + 1], o[b][db][4 * q + 2], o[b][db][4 * q + 3]};
+#pragma unroll
+        for (int slot = 0; slot < 3; ++slot) acc[q] += *(lds_f4 *)mg_at(b * 4 + db, slot, q);
+      }
+      if (t < p.S) {
+        // dims 32*db + 8*q + 4*half .. +4 (the accumulator's dim order)
+        if (p.nsplit == 1) {
+          const float inv = 1.0f / Lsum[b];
+          float *dst = p.out + (size_t)t * dim_model + (size_t)(kvh * 4 + g) * HD + 32 * db + 4 * half;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) *reinterpret_cast<f4 *>(dst + 8 * q) = acc[q] * inv;
+        } else {
+          const size_t pidx = (tile_id * p.nsplit + split) * RT + rl;
+          float *dst = p.part_o + pidx * HD + 32 * db + 4 * half;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) *reinterpret_cast<f4 *>(dst + 8 * q) = acc[q];
+          if (db == 0 && half == 0)
+            *reinterpret_cast<float2 *>(p.part_ml + pidx * 2) = make_float2(Mx[b], Lsum[b]);
+        }
+      }
     }
   }
 }
 
 // Split merge: one workgroup per 8 rows of a tile, thread = (row, 4 dims).  A
 // separate launch, so the kernel boundary orders the partial writes before
-// these reads (no agent-scope fence in the attention kernel).
-template <int G>
+// these reads.
 __global__ void __launch_bounds__(256) flash_merge_kernel(FlashParams p, int rt) {
   const int tid = threadIdx.x;
   const int blocks_per_tile = rt / 8;
@@ -447,41 +642,41 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(FlashParams p, int rt)
   const int d4 = tid % 32;
   const int kvh = tile_id / p.n_rtiles, rtile = tile_id % p.n_rtiles;
   const int row = rtile * rt + rl;
-  const int t = row / G, g = row % G;
+  const int t = row >> 2, g = row & 3;
   if (t >= p.S) return;
-  const int dim_model = p.n_kv * G * HD;
+  const int dim_model = p.n_kv * 4 * HD;
   float M = -INFINITY;
   for (int sp = 0; sp < p.nsplit; ++sp)
     M = fmaxf(M, p.part_ml[(((size_t)tile_id * p.nsplit + sp) * rt + rl) * 2]);
-  const float Mu = M == -INFINITY ? 0.f : M;
   float Ls = 0.f;
   f4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int sp = 0; sp < p.nsplit; ++sp) {
     const size_t idx = ((size_t)tile_id * p.nsplit + sp) * rt + rl;
-    float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + idx * 2);
-    float e = fast_exp2(ml.x - Mu);
-    Ls = __builtin_fmaf(e, ml.y, Ls);
+    const float2 m_l = *reinterpret_cast<const float2 *>(p.part_ml + idx * 2);
+    const float e = m_l.x == -INFINITY ? 0.f : fast_exp2(m_l.x - M);
+    Ls = __builtin_fmaf(e, m_l.y, Ls);
     acc += e * *reinterpret_cast<const f4 *>(p.part_o + idx * HD + 4 * d4);
   }
-  *reinterpret_cast<f4 *>(p.out + (size_t)t * dim_model + (size_t)(kvh * G + g) * HD + 4 * d4) =
+  *reinterpret_cast<f4 *>(p.out + (size_t)t * dim_model + (size_t)(kvh * 4 + g) * HD + 4 * d4) =
       acc * (1.0f / Ls);
 }
 
-template <int SL, int KH>
+template <int NB>
 hipError_t launch_variant(const FlashParams &p, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
-  using Lay = FlashLayout<SL, KH>;
+  using L = Lay<NB>;
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void *)flash_kernel<4, SL, KH>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)Lay::kBytes);
+    hipError_t e = hipFuncSetAttribute((const void *)flash_kernel<NB>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   dim3 grid(p.n_kv * p.n_rtiles * p.nsplit);
-  hipExtLaunchKernelGGL((flash_kernel<4, SL, KH>), grid, dim3(64 * SL * KH), Lay::kBytes, s, ev0, ev1,
-                        0, p);
+  hipExtLaunchKernelGGL((flash_kernel<NB>), grid, dim3(256), L::kBytes, s, ev0, ev1, 0, p);
   return hipGetLastError();
 }
+
+int rows_per_tile(int S) { return S * 4 <= 32 ? 32 : 64; }
 
 }  // namespace
 
@@ -489,15 +684,14 @@ size_t flash_scratch_bytes(int n_kv, int n_rtiles, int nsplit, int rows_per_tile
   return (size_t)n_kv * n_rtiles * nsplit * rows_per_tile * (HD + 2) * sizeof(float);
 }
 
-// Few rows (S*G <= 32, e.g. speculative verify): one slab, 4 key groups, and
-// key splits over workgroups until about target_wgs workgroups.  Otherwise
-// (prefill): two slabs (64 rows) and 4 key groups per workgroup, no split
-// unless the row tiles alone leave the device mostly idle.
+// Few rows (S*G <= 32, e.g. speculative verify): one 32-row block, key splits
+// over workgroups until about target_wgs workgroups.  Otherwise (prefill):
+// 64-row tiles, no split unless the row tiles alone leave the device mostly
+// idle.  Every wave of a split keeps at least 4 tiles of 32 keys.
 void flash_plan(int S, int n_kv, int G, int start_pos, int max_seq, int target_wgs, int *n_rtiles,
-                int *nsplit, int *split_keys, int *rows_per_tile) {
-  const int rows = S * G;
-  const int rt = rows <= 32 ? 32 : 64;
-  const int ntiles = (rows + rt - 1) / rt;
+                int *nsplit, int *split_keys, int *rows_per_tile_out) {
+  const int rt = rows_per_tile(S);
+  const int ntiles = (S * G + rt - 1) / rt;
   long maxkeys = 0;
   for (int ti = 0; ti < ntiles; ++ti) {
     int t0 = (ti * rt) / G;
@@ -510,8 +704,7 @@ void flash_plan(int S, int n_kv, int G, int start_pos, int max_seq, int target_w
   }
   long want = (long)target_wgs / ((long)n_kv * ntiles);
   if (want < 1) want = 1;
-  // at least 4 tiles of 32 keys per key group and split
-  long max_split = maxkeys / (4L * 4 * kKT);
+  long max_split = maxkeys / (4L * kWaves * kKT);
   if (want > max_split) want = max_split > 0 ? max_split : 1;
   long sk = (maxkeys + want - 1) / want;
   sk = ((sk + kKT - 1) / kKT) * kKT;
@@ -520,20 +713,20 @@ void flash_plan(int S, int n_kv, int G, int start_pos, int max_seq, int target_w
   *n_rtiles = ntiles;
   *nsplit = (int)ns;
   *split_keys = (int)sk;
-  *rows_per_tile = rt;
+  *rows_per_tile_out = rt;
 }
 
 hipError_t launch_flash(const FlashParams &p, int G, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   if (G != 4) return hipErrorInvalidValue;
-  const int rt = p.S * G <= 32 ? 32 : 64;
-  return rt == 32 ? launch_variant<1, 4>(p, s, ev0, ev1) : launch_variant<2, 4>(p, s, ev0, ev1);
+  return rows_per_tile(p.S) == 32 ? launch_variant<1>(p, s, ev0, ev1)
+                                  : launch_variant<2>(p, s, ev0, ev1);
 }
 
 hipError_t launch_flash_merge(const FlashParams &p, hipStream_t s) {
-  const int rt = p.S * 4 <= 32 ? 32 : 64;
+  const int rt = rows_per_tile(p.S);
   if (p.nsplit > 1)
-    hipLaunchKernelGGL((flash_merge_kernel<4>), dim3(p.n_kv * p.n_rtiles * (rt / 8)), dim3(256), 0,
-                       s, p, rt);
+    hipLaunchKernelGGL(flash_merge_kernel, dim3(p.n_kv * p.n_rtiles * (rt / 8)), dim3(256), 0, s,
+                       p, rt);
   return hipGetLastError();
 }
 

@@ -41,7 +41,8 @@ hipError_t launch_decode_merge(const DecodeParams &p, hipStream_t s);
 // S>=1 causal attention on fp16 MFMA for the queries start_pos..start_pos+S-1.
 struct FlashParams {
   const float *Q;          // [S][n_heads*128] fp32 (scale applied in-kernel)
-  const float *theta_inv;  // [64]: apply RoPE to Q in-kernel; nullptr: Q already rotated
+  const float *rope_cs;    // [S][64] (cos, sin) of the query positions: rotate Q
+                           // in-kernel; nullptr: Q already rotated
   const _Float16 *kc;      // layer base [max_seq][kv_dim]
   const _Float16 *vc;
   const _Float16 *kstage;  // [S][kv_dim] staged new keys (nullptr: all keys in ring)
@@ -66,12 +67,14 @@ void flash_plan(int S, int n_kv, int G, int start_pos, int max_seq, int target_w
 // Elementwise helpers.
 hipError_t launch_rope(float *q, float *k, int S, int start_pos, const float *theta_inv,
                        int n_heads, int n_kv, hipStream_t s);
+// K rotated and K, V rounded to fp16 into a dense staging buffer or the ring;
+// cs_out (may be null) receives the [S][64] (cos, sin) table of the positions.
 hipError_t launch_rope_to_f16(const float *K, const float *V, const float *theta_inv, int S,
                               int start_pos, int n_kv, _Float16 *kdst, _Float16 *vdst,
-                              hipStream_t s);
+                              float *cs_out, hipStream_t s);
 hipError_t launch_rope_to_ring(const float *K, const float *V, const float *theta_inv, int S,
                                int start_pos, int n_kv, _Float16 *kc, _Float16 *vc, int max_seq,
-                               hipStream_t s);
+                               float *cs_out, hipStream_t s);
 hipError_t launch_kv_write(_Float16 *kc, _Float16 *vc, const float *K, const float *V, int S,
                            int start_pos, int max_seq, int kv_dim, hipStream_t s);
 hipError_t launch_commit(_Float16 *kc, _Float16 *vc, const _Float16 *kst, const _Float16 *vst,
