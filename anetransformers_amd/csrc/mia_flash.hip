@@ -314,7 +314,10 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       MIA_LOAD_K(0, 0);
       MIA_LOAD_V(0, 0);
     }
-    if (g_count > 1) MIA_LOAD_K(1, 1);
+    if (g_count > 1) {
+      MIA_LOAD_K(1, 1);
+      MIA_LOAD_V(1, 1);
+    }
   };
   issue_first_tiles();
 
@@ -358,21 +361,34 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     for (int st = 0; st < 8; ++st)
       qb[b][st] = *(lds_h8 *)(qs + (32 * b + col) * HD + 8 * ((2 * st + half) ^ swz(col)));
 
-  // Softmax reference per row: fixed at the first tile with a finite score
-  // (so p <= 1 there) instead of a running max, so the accumulators are never
-  // rescaled inside the loop.  A later score more than 15 (log2 units) above
-  // it would overflow the fp16 P operand (2^15 is exact; fp16 ends at 65504):
-  // such a wave marks overflow and runs its key range once more with the
-  // true row max, which it tracks, as the reference.
+  // Softmax reference per row, fixed for the whole key range of the wave:
+  // the max of the row's scores in its first tile (p <= 1 there), rounded to
+  // fp16 and subtracted inside the score MFMA by one extra k-step (a ones
+  // column in K against -m_ref in Q), so the loop neither subtracts nor
+  // tracks maxima and never rescales the accumulators.  P is fp16, so a later
+  // score more than ~16 (log2 units) above the reference overflows, and a row
+  // whose scores all sit far below an unset reference underflows: both show in
+  // the row sum at the end of the pass (not finite, or below 2^-8).  Such a
+  // wave sweeps its tiles for the exact row maxima and runs once more with
+  // them as the reference.
   f16v o[NB][4];
-  float m_ref[NB], m_max[NB], l_run[NB], m_cur[NB];
+  float m_ref[NB], l_run[NB];
   f16v s_cur[NB];
+  h8 qx[NB];  // extra k-step B operand: -m_ref in element 0 of the half-0 lanes
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    m_ref[b] = -INFINITY;
-    m_max[b] = -INFINITY;
-  }
+  for (int b = 0; b < NB; ++b) m_ref[b] = -INFINITY;
   const h8 zero8 = {};
+  h8 kx = {};  // extra k-step A operand: a ones column (k = 0) for every key
+  if (half == 0) kx[0] = (_Float16)1.0f;
+  auto set_ref = [&](int b, float m) {
+    // fp16 range; the rounded value is the one applied and reported
+    const float mc = m == -INFINITY ? 0.f : fminf(fmaxf(m, -60000.f), 60000.f);
+    const _Float16 mh = (_Float16)mc;
+    m_ref[b] = m == -INFINITY ? -INFINITY : (float)mh;
+    h8 x = {};
+    if (half == 0) x[0] = -mh;
+    qx[b] = x;
+  };
 
   // Tile kb needs masking unless every key is inside every row's window.
   auto needs_mask = [&](int kb) {
@@ -399,16 +415,38 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     for (int i = 2; i < 16; i += 2) m = fmaxf(m, fmaxf(s[i], s[i + 1]));
     return half_swap_max(m);
   };
+  // Unshifted scores of the tile in kt[buf] (first tile, max sweep).
+  auto scores = [&](f16v (&sc)[NB], int buf, int kb) {
+    h8 ka[8];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) ka[st] = lds_read_h8(ka_b[buf] ^ (unsigned)(st << 5));
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sc[b][i] = 0.f;
+#pragma unroll
+      for (int st = 0; st < 8; ++st)
+        sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st], sc[b], 0, 0, 0);
+    }
+    if (needs_mask(kb)) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) mask_block(sc[b], b, kb);
+    }
+  };
 
   const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
-  // One tile step: P of tile it from s_cur, scores of tile it+1 into s_cur,
-  // O += P.V of tile it.  K(it+1) is in kt[(it+1)&1], V(it) in vt[it&1].  The
-  // K and V operands are streamed in halves (k-steps 0-3 / 4-7, keys 0-15 /
-  // 16-31) to keep the register footprint within one wave per SIMD.
-  auto step = [&](int it) {
-    float m_use[NB];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) m_use[b] = m_ref[b] == -INFINITY ? 0.f : m_ref[b];
+  // One tile step: P of tile it from s_cur (already shifted by the
+  // reference), shifted scores of tile it+1 into s_cur, O += P.V of tile it.
+  // K(it+1) is in kt[(it+1)&1], V(it) in vt[it&1].  The K and V operands are
+  // streamed in halves (k-steps 0-3 / 4-7, keys 0-15 / 16-31) to keep the
+  // register footprint within one wave per SIMD.
+  // One tile step: P of tile it from s_cur (already shifted by the
+  // reference), shifted scores of tile it+1 into s_cur, O += P.V of tile it,
+  // and the direct loads of tile it+2 when more2.  K(it+1) is in
+  // kt[(it+1)&1], V(it) in vt[it&1].  The K and V operands are streamed in
+  // halves (k-steps 0-3 / 4-7, keys 0-15 / 16-31) to keep the register
+  // footprint within one wave per SIMD.
+  auto step = [&](int it, bool more2) {
     const unsigned kab = ka_b[(it + 1) & 1];
     const unsigned vab = va_b[it & 1];
     h8 ka[4], va[4];
@@ -426,8 +464,8 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       float ls = l_run[b];
 #pragma unroll
       for (int i = 0; i < 16; i += 2) {
-        const float p0 = fast_exp2(s_cur[b][i] - m_use[b]);
-        const float p1 = fast_exp2(s_cur[b][i + 1] - m_use[b]);
+        const float p0 = fast_exp2(s_cur[b][i]);
+        const float p1 = fast_exp2(s_cur[b][i + 1]);
         const h2 pp = __builtin_convertvector((f2){p0, p1}, h2);
         ls = __builtin_amdgcn_fdot2(pp, ones, ls, false);
         pw[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(unsigned, pp);
@@ -438,9 +476,11 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     }
     f16v s_next[NB];
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
+    for (int b = 0; b < NB; ++b) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) s_next[b][i] = 0.f;
+      s_next[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kx, qx[b], s_next[b], 0, 0, 0);
+    }
 #pragma unroll
     for (int st = 0; st < 4; ++st)
 #pragma unroll
@@ -448,6 +488,12 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
         s_next[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st], s_next[b], 0, 0, 0);
 #pragma unroll
     for (int st = 0; st < 4; ++st) ka[st] = lds_read_h8(kab ^ (unsigned)((st + 4) << 5));
+    // The direct loads of tile it+2 are issued inside the step, K here (its
+    // buffer held K(it), consumed by the previous step) and V after the
+    // P.V MFMAs (its buffer holds V(it)): issued at the top of the
+    // iteration they would stall the wave on the address queue before any
+    // MFMA is queued.
+    if (more2) MIA_LOAD_K(it + 2, it & 1);
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -466,6 +512,10 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pb[b][1]);
+    if (more2) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // V(it) reads done
+      MIA_LOAD_V(it + 2, it & 1);
+    }
     // Window mask of tile it+1, only where it crosses a window edge.
     const int kbn = kb0 + kKT * (it + 1);
     if (needs_mask(kbn)) {
@@ -473,69 +523,80 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       for (int b = 0; b < NB; ++b) mask_block(s_next[b], b, kbn);
     }
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      m_cur[b] = block_max(s_next[b]);
-      s_cur[b] = s_next[b];
-    }
+    for (int b = 0; b < NB; ++b) s_cur[b] = s_next[b];
   };
+
+  // Does the lane's row of block b have a key in this wave's range?
+  bool has_keys[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int k0 = max(lo_t[b], kb0);
+    const int k1 = min(min(hi_t[b], ke - 1), kb0 + kKT * g_count - 1);
+    has_keys[b] = valid[b] && g_count > 0 && k0 <= k1;
+  }
 
   for (int pass = 0; pass < 2; ++pass) {
     if (pass == 1) {
-      issue_first_tiles();
+      // Exact row maxima over the wave's tiles, then the same pass again.
+      float mt[NB];
 #pragma unroll
-      for (int b = 0; b < NB; ++b) m_ref[b] = m_max[b];
+      for (int b = 0; b < NB; ++b) mt[b] = -INFINITY;
+      for (int i = 0; i < g_count; ++i) {
+        MIA_LOAD_K(i, 0);
+        wait_vmcnt<0>();
+        f16v sc[NB];
+        scores(sc, 0, kb0 + kKT * i);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) mt[b] = fmaxf(mt[b], block_max(sc[b]));
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) set_ref(b, mt[b]);
+      issue_first_tiles();
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) mfma_zero(o[b][db], zero8);
       l_run[b] = 0.f;
-      m_cur[b] = -INFINITY;
 #pragma unroll
       for (int i = 0; i < 16; ++i) s_cur[b][i] = -INFINITY;
     }
-    // The first tile's scores.
+    // The first tile's scores set the reference (first pass) and are
+    // shifted by it.
     if (g_count > 0) {
-      if (g_count > 1) wait_vmcnt<16>();
+      if (g_count > 1) wait_vmcnt<24>();
       else wait_vmcnt<8>();
-      h8 ka[8];
-#pragma unroll
-      for (int st = 0; st < 8; ++st) ka[st] = lds_read_h8(ka_b[0] ^ (unsigned)(st << 5));
+      scores(s_cur, 0, kb0);
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
+        if (pass == 0) set_ref(b, block_max(s_cur[b]));
+        const float sh = m_ref[b] == -INFINITY ? 0.f : m_ref[b];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s_cur[b][i] = 0.f;
-#pragma unroll
-        for (int st = 0; st < 8; ++st)
-          s_cur[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st], s_cur[b], 0, 0, 0);
+        for (int i = 0; i < 16; ++i) s_cur[b][i] -= sh;
       }
-      if (needs_mask(kb0)) {
+    } else {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) mask_block(s_cur[b], b, kb0);
-      }
-#pragma unroll
-      for (int b = 0; b < NB; ++b) m_cur[b] = block_max(s_cur[b]);
+      for (int b = 0; b < NB; ++b) set_ref(b, -INFINITY);
     }
 
-    bool ovf = false;
+    // Tiles 0 and 1 came from issue_first_tiles; step it issues K(it+2),
+    // then V(it+2).  Before step it, K(it+1) and V(it) must have landed:
+    // only V(it+1), the last load issued (when it exists), may be pending.
     for (int it = 0; it < g_count; ++it) {
-      // Buffers of K(it) and V(it-1) were consumed by the previous step:
-      // refill them with K(it+2) and V(it+1), then wait for K(it+1) and V(it).
-      const bool more1 = it + 1 < g_count, more2 = it + 2 < g_count;
-      if (more2) MIA_LOAD_K(it + 2, it & 1);
-      if (more1) MIA_LOAD_V(it + 1, (it + 1) & 1);
-      if (more2) wait_vmcnt<16>();
-      else if (more1) wait_vmcnt<8>();
+      if (it + 1 < g_count) wait_vmcnt<8>();
       else wait_vmcnt<0>();
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        m_ref[b] = m_ref[b] == -INFINITY ? m_cur[b] : m_ref[b];
-        m_max[b] = fmaxf(m_max[b], m_cur[b]);
-        ovf = ovf || m_cur[b] > m_ref[b] + 15.0f;
-      }
-      step(it);
+      step(it, it + 2 < g_count);
     }
-    if (__builtin_amdgcn_ballot_w64(ovf) == 0) break;
+    // Row sums: overflow (not finite) or underflow (< 2^-8 with keys in range)
+    // means the reference did not suit the row.
+    bool bad = false;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float lt = half_swap_sum(l_run[b]);
+      l_run[b] = lt;
+      bad = bad || (has_keys[b] && !(lt >= 0.00390625f && lt <= 3.0e38f));
+    }
+    if (pass == 1 || __builtin_amdgcn_ballot_w64(bad) == 0) break;
   }
 #undef MIA_LOAD_K
 #undef MIA_LOAD_V
@@ -546,10 +607,10 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   lds_float *ml = (lds_float *)(smem + L::kBufBytes + L::kQBytes);  // [wave][RT][2]
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
-    const float lt = half_swap_sum(l_run[b]);
-    if (half == 0)
-      *(lds_f2 *)(ml + (w * RT + 32 * b + col) * 2) =
-          (f2){m_ref[b], lt};
+    // reference actually applied: m_ref, or 0 where it stayed unset although
+    // the row has keys here; rows without keys get weight 0 in the merge
+    const float mr = !has_keys[b] ? -INFINITY : (m_ref[b] == -INFINITY ? 0.f : m_ref[b]);
+    if (half == 0) *(lds_f2 *)(ml + (w * RT + 32 * b + col) * 2) = (f2){mr, l_run[b]};
   }
   __syncthreads();  // every wave is past its loop: tile buffers are free
 
