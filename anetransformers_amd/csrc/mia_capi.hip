@@ -166,7 +166,7 @@ int decode_impl(const float *q, const float *k, const float *v, const float *the
   p.start = (int)start;
   p.new_slot = pos % max_seq;
   p.n_kv = n_kv;
-  p.nchunk = mia::decode_pick_nchunk(L, n_kv, 2 * c->num_cus);
+  p.nchunk = mia::decode_pick_nchunk(L, n_kv, c->num_cus);
   p.qscale = qscale_log2();
   if (p.nchunk > 1) {
     if (int rc = ensure_scratch(c, mia::decode_scratch_bytes(n_kv, kG, p.nchunk))) return rc;

@@ -4,13 +4,15 @@
 // fused variant, steps 4-6 of mistral/mistral_model.h:849-863 (RoPE on q/k,
 // fp16 round of k/v, ring write at pos % max_seq, attention).
 //
-// Grid: one workgroup per (kv head, chunk of the window); blockIdx % n_kv is
-// the kv head, so with the hardware's round-robin workgroup dispatch over the
-// 8 XCDs every chunk of one kv head (and its partials) stays on one XCD.
+// Grid: one workgroup per (group of 8 kv heads, chunk of the window), one
+// wave per kv head.  The waves of a workgroup walk the same ring slots, so
+// each slot's full K and V rows (8 heads x 256 B, contiguous) are read
+// together: streaming one head's 256 B pieces per workgroup instead leaves
+// some heads' pieces consistently slower to fetch than others.
 //
-// Each of the 4 waves of a workgroup is an independent pipeline over 16-key
-// tiles (wave w takes tiles w, w+4, ...), held in a ring of register buffers
-// so that the next tiles' loads are in flight while one tile is computed:
+// Each wave is an independent pipeline over the 16-key tiles of its chunk,
+// held in a ring of register buffers so that the next tiles' loads are in
+// flight while one tile is computed:
 //   scores  v_mfma_f32_16x16x32_f16: A = 16 key rows straight from the
 //           loads (lane = key row, 64 contiguous bytes), B = the G=4 query
 //           heads of the group with q split into fp16 hi + lo parts along K
@@ -21,8 +23,11 @@
 //           operand layout with keys along K, so P (fp16 hi + lo) never
 //           leaves its lane; V^T comes from the 4 loaded V rows of the lane
 //           (4 keys x 8 dims) by byte permutes.
-// The 4 wave partials are merged in LDS; chunk partials are merged by a
-// second, small kernel (log-sum-exp merge).
+// A wave's result is final for its head and chunk: it is written as the
+// chunk partial (m, l, o) directly; a second, small kernel does the
+// log-sum-exp merge over chunks.
+#include <type_traits>
+
 #include "mia_device.h"
 #include "mia_kernels.h"
 
@@ -30,8 +35,8 @@ namespace mia {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;         // kv heads per workgroup, one wave each
+constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 16;        // keys per wave tile
 constexpr int kDepth = 2;        // register tile buffers per wave (3, 4 measured no faster)
 constexpr int kMaxChunks = 256;  // merge capacity per kv head
@@ -39,10 +44,8 @@ constexpr int G = 4;             // query heads per kv head
 
 struct DecodeSmem {
   float2 cs[64];                 // RoPE (cos, sin) for the 64 pair indices
-  _Float16 knew[HD];             // rotated fp16 new key of this kv head
-  _Float16 vnew[HD];
-  float ml[kWaves][2 * G];       // per-wave (max, sum)
-  float acc[kWaves][G][HD];      // per-wave partial outputs
+  _Float16 knew[kWaves][HD];     // rotated fp16 new key of each kv head
+  _Float16 vnew[kWaves][HD];
 };
 
 struct TileBuf {
@@ -61,60 +64,104 @@ __device__ __forceinline__ int ring_slot(int start, int t, int max_seq) {
 }
 
 template <bool FUSED>
-__global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
+__global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   __shared__ DecodeSmem sm;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lc = lane & 15;  // MFMA column / V dim block
   const int lg = lane >> 4;  // MFMA k group / V key group
-  const int kvh = blockIdx.x % p.n_kv;
-  const int chunk = blockIdx.x / p.n_kv;
+  const int hgroups = (p.n_kv + kWaves - 1) / kWaves;
+  const int kvh = (blockIdx.x % hgroups) * kWaves + w;
+  const bool active = kvh < p.n_kv;  // waves past the last head only join the barriers
+  const int chunk = blockIdx.x / hgroups;
+  const int kvh_c = active ? kvh : 0;  // idle waves keep in-bounds addresses
   const int kv_dim = p.n_kv * HD;
-  // Chunk = tiles [chunk*T/nchunk, (chunk+1)*T/nchunk) of the T 16-key tiles
-  // of the window, so workgroups differ by at most one tile.
-  const long n_tiles = (p.L + kTile - 1) / kTile;
-  const int c0 = (int)((long)chunk * n_tiles / p.nchunk) * kTile;
-  const int c1 = min((int)((long)(chunk + 1) * n_tiles / p.nchunk) * kTile, p.L);
-  const bool has_new = FUSED && (c1 == p.L);
+  // The new token (fused) is attended after the loop, from its fp16 copy in
+  // LDS, by the waves of the last chunk; the tiles cover keys [0, ce).
+  const int ce = FUSED ? p.L - 1 : p.L;
+  const int n_tiles = (ce + kTile - 1) / kTile;
+  const bool has_new = FUSED && chunk == p.nchunk - 1;
+  // Tiles of this wave: chunk `chunk` of an even split of all tiles.
+  int s_next = (int)((long)chunk * n_tiles / p.nchunk);
+  const int s_end = active ? (int)((long)(chunk + 1) * n_tiles / p.nchunk) : s_next;
+  auto next_tile = [&]() -> int { return s_next < s_end ? s_next++ : -1; };
 
-  // The new token (fused, last chunk) is attended after the loop from its
-  // fp16 copy in LDS, so the tiles cover [c0, ce).
-  const int ce = has_new ? p.L - 1 : c1;
-  // Tiles of this wave: global tile index tt = (c0/16) + w + 4*i.
-  const int first_tile = c0 / kTile + w;
-  const int end_tile = (ce + kTile - 1) / kTile;  // exclusive
-  const int n_my = first_tile < end_tile ? (end_tile - first_tile + kWaves - 1) / kWaves : 0;
-  const int last_tile = first_tile + kWaves * (n_my > 0 ? n_my - 1 : 0);
+  const _Float16 *kbase = p.kc + (size_t)kvh_c * HD;
+  const _Float16 *vbase = p.vc + (size_t)kvh_c * HD;
 
-  const _Float16 *kbase = p.kc + (size_t)kvh * HD;
-  const _Float16 *vbase = p.vc + (size_t)kvh * HD;
-
-  auto issue = [&](TileBuf &b, int i) {
-    const int tt = min(first_tile + kWaves * i, last_tile);  // clamp: re-read, L2 hit
+  // Tile loads.  A tile whose 16 slots are contiguous in the ring and inside
+  // the window (all but the tile across the ring's end and the window's last
+  // tile) is addressed as one wave-uniform row base plus fixed per-lane
+  // offsets; the others clamp and wrap per lane.
+  const unsigned koff = (unsigned)lc * kv_dim + 8 * lg;  // K: row lc, dims 8*lg (+32*s)
+  unsigned voff[4];                                       // V: row 4*lg+m, dims 8*lc
+#pragma unroll
+  for (int m = 0; m < 4; ++m) voff[m] = (unsigned)(4 * lg + m) * kv_dim + 8 * lc;
+  auto tile_row0 = [&](int tt, bool &linear) {
     const int t0 = tt * kTile;
-    {
-      int t = min(t0 + lc, ce - 1);
-      unsigned off = (unsigned)ring_slot(p.start, t, p.max_seq) * (unsigned)kv_dim + 8 * lg;
-      const _Float16 *src = kbase + off;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) b.k[s] = *reinterpret_cast<const u4 *>(src + 32 * s);
+    const int s0 = ring_slot(p.start, t0, p.max_seq);
+    linear = s0 + kTile <= p.max_seq && t0 + kTile <= ce;
+    return t0;
+  };
+  // Every refill issues its loads, also past the end of the wave's tiles
+  // (tt < 0: all lanes read one 16-byte piece, a cache hit): with the same
+  // number of loads on every path the compiler can wait for exactly the
+  // buffer it needs instead of for all outstanding loads.
+  // (Offsets rather than pointers are selected, so that every load keeps
+  // the global address space of the kernel argument.)
+  auto issue_k = [&](TileBuf &b, int tt) {
+    size_t off = 0;
+    if (tt >= 0) {
+      bool linear;
+      const int t0 = tile_row0(tt, linear);
+      if (linear) {
+        off = (size_t)ring_slot(p.start, t0, p.max_seq) * kv_dim + koff;
+      } else {
+        const int t = min(t0 + lc, ce - 1);
+        off = (unsigned)ring_slot(p.start, t, p.max_seq) * (unsigned)kv_dim + 8 * lg;
+      }
     }
+    const _Float16 *src = kbase + off;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      int t = min(t0 + 4 * lg + m, ce - 1);
-      unsigned off = (unsigned)ring_slot(p.start, t, p.max_seq) * (unsigned)kv_dim + 8 * lc;
-      b.v[m] = *reinterpret_cast<const u4 *>(vbase + off);
+    for (int s = 0; s < 4; ++s) b.k[s] = *reinterpret_cast<const u4 *>(src + 32 * s);
+  };
+  auto issue_v = [&](TileBuf &b, int tt) {
+    size_t row0 = 0;
+    unsigned off[4] = {0, 0, 0, 0};
+    if (tt >= 0) {
+      bool linear;
+      const int t0 = tile_row0(tt, linear);
+      if (linear) {
+        row0 = (size_t)ring_slot(p.start, t0, p.max_seq) * kv_dim;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) off[m] = voff[m];
+      } else {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int t = min(t0 + 4 * lg + m, ce - 1);
+          off[m] = (unsigned)ring_slot(p.start, t, p.max_seq) * (unsigned)kv_dim + 8 * lc;
+        }
+      }
     }
+    const _Float16 *src = vbase + row0;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) b.v[m] = *reinterpret_cast<const u4 *>(src + off[m]);
+  };
+  auto issue = [&](TileBuf &b, int tt) {
+    issue_k(b, tt);
+    issue_v(b, tt);
   };
 
   // The first kDepth tiles are requested before the prologue so that their
   // latency overlaps the RoPE table, the new-token write and the q set-up.
   TileBuf buf[kDepth];
-  if (n_my > 0) {
+  int tix[kDepth];
 #pragma unroll
-    for (int b = 0; b < kDepth; ++b) issue(buf[b], b);
+  for (int b = 0; b < kDepth; ++b) {
+    tix[b] = next_tile();
+    issue(buf[b], tix[b]);
   }
 
   if (FUSED) {
@@ -126,22 +173,22 @@ __global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
       sm.cs[tid] = make_float2(cs, sn);
     }
     __syncthreads();
-    if (has_new && tid < 64) {
-      // new k rotated (pair tid) and v, rounded to fp16 (mistral_model.h:854-857)
-      float2 kv = *reinterpret_cast<const float2 *>(p.knew + (size_t)kvh * HD + 2 * tid);
-      float2 cs = sm.cs[tid];
+    if (has_new && active) {
+      // new k rotated (pair `lane`) and v, rounded to fp16 (mistral_model.h:854-857)
+      float2 kv = *reinterpret_cast<const float2 *>(p.knew + (size_t)kvh * HD + 2 * lane);
+      float2 cs = sm.cs[lane];
       rope_pair(kv.x, kv.y, cs.x, cs.y);
-      float2 vv = *reinterpret_cast<const float2 *>(p.vnew + (size_t)kvh * HD + 2 * tid);
-      sm.knew[2 * tid] = (_Float16)kv.x;
-      sm.knew[2 * tid + 1] = (_Float16)kv.y;
-      sm.vnew[2 * tid] = (_Float16)vv.x;
-      sm.vnew[2 * tid + 1] = (_Float16)vv.y;
+      float2 vv = *reinterpret_cast<const float2 *>(p.vnew + (size_t)kvh * HD + 2 * lane);
+      sm.knew[w][2 * lane] = (_Float16)kv.x;
+      sm.knew[w][2 * lane + 1] = (_Float16)kv.y;
+      sm.vnew[w][2 * lane] = (_Float16)vv.x;
+      sm.vnew[w][2 * lane + 1] = (_Float16)vv.y;
     }
     __syncthreads();
-    if (has_new && tid < 16) {  // ring write of the new row (256 B per tensor)
-      size_t off = (size_t)p.new_slot * kv_dim + (size_t)kvh * HD + 8 * tid;
-      *reinterpret_cast<u4 *>(p.kc + off) = *reinterpret_cast<const u4 *>(&sm.knew[8 * tid]);
-      *reinterpret_cast<u4 *>(p.vc + off) = *reinterpret_cast<const u4 *>(&sm.vnew[8 * tid]);
+    if (has_new && active && lane < 16) {  // ring write of the new row (256 B per tensor)
+      size_t off = (size_t)p.new_slot * kv_dim + (size_t)kvh * HD + 8 * lane;
+      *reinterpret_cast<u4 *>(p.kc + off) = *reinterpret_cast<const u4 *>(&sm.knew[w][8 * lane]);
+      *reinterpret_cast<u4 *>(p.vc + off) = *reinterpret_cast<const u4 *>(&sm.vnew[w][8 * lane]);
     }
   }
 
@@ -150,7 +197,7 @@ __global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
   h8 qhi[4], qlo[4];
   {
     const bool col = lc < G;
-    const float *qsrc = p.q + (size_t)(kvh * G + (col ? lc : 0)) * HD + 8 * lg;
+    const float *qsrc = p.q + (size_t)(kvh_c * G + (col ? lc : 0)) * HD + 8 * lg;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const f4 *src = reinterpret_cast<const f4 *>(qsrc + 32 * s);
@@ -184,8 +231,10 @@ __global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = f4{0.f, 0.f, 0.f, 0.f};
 
-  // One 16-key tile starting at key t0; keys >= cend are masked.
-  auto process = [&](const TileBuf &b, int t0, int cend) {
+  // One 16-key tile starting at key t0; keys >= cend are masked.  With
+  // `refill` the buffer is refilled with tile `next`: its K half as soon as
+  // the score MFMAs have read the keys, its V half after the P.V MFMAs.
+  auto process = [&](TileBuf &b, int t0, int cend, int next, auto refill) {
     h8 ka[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) ka[s] = __builtin_bit_cast(h8, b.k[s]);
@@ -195,6 +244,7 @@ __global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
       d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s], qhi[s], d, 0, 0, 0);
       d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s], qlo[s], d, 0, 0, 0);
     }
+    if (refill) issue_k(b, next);
     // d[i]: score of key t0 + 4*lg + i for head lc (lanes lc < G).
     float sc[4];
     float mx = -INFINITY;
@@ -243,125 +293,105 @@ __global__ void __launch_bounds__(kThreads, 3) decode_kernel(DecodeParams p) {
       o[2 * j + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(ao, phi, o[2 * j + 1], 0, 0, 0);
       o[2 * j + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(ao, plo, o[2 * j + 1], 0, 0, 0);
     }
+    if (refill) issue_v(b, next);
   };
 
-  if (n_my > 0) {
-    // Ring of kDepth register buffers: tile i+kDepth is requested as soon as
-    // tile i has been consumed, so kDepth-1 tiles stay in flight.
-    for (int i = 0; i < n_my; i += kDepth) {
+  // Ring of kDepth register buffers: buffer b is refilled with the next tile
+  // of the stream while it is consumed, so kDepth-1 tiles stay in flight.
+  // Tiles come in stream order, so the first empty buffer ends the loop.
+  for (bool more = tix[0] >= 0; more;) {
 #pragma unroll
-      for (int b = 0; b < kDepth; ++b) {
-        if (i + b < n_my) process(buf[b], (first_tile + kWaves * (i + b)) * kTile, ce);
-        issue(buf[b], i + b + kDepth);
+    for (int b = 0; b < kDepth; ++b) {
+      if (tix[b] < 0) {
+        more = false;
+        break;
       }
+      const int nt = next_tile();
+      process(buf[b], tix[b] * kTile, ce, nt, std::true_type{});
+      tix[b] = nt;
     }
   }
-  if (has_new && w == 0) {
+  if (has_new && active) {
     // Every row of this tile is the new key / value; only key 0 is unmasked.
     TileBuf nb;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) nb.k[s] = *reinterpret_cast<const u4 *>(&sm.knew[32 * s + 8 * lg]);
+    for (int s = 0; s < 4; ++s) nb.k[s] = *reinterpret_cast<const u4 *>(&sm.knew[w][32 * s + 8 * lg]);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) nb.v[m] = *reinterpret_cast<const u4 *>(&sm.vnew[8 * lc]);
-    process(nb, p.L - 1, p.L);
+    for (int m = 0; m < 4; ++m) nb.v[m] = *reinterpret_cast<const u4 *>(&sm.vnew[w][8 * lc]);
+    process(nb, p.L - 1, p.L, -1, std::false_type{});
   }
 
   // Wave totals: l over the 4 key groups of column lc.
   l_part += __shfl_xor(l_part, 16);
   l_part += __shfl_xor(l_part, 32);
-  if (lane < G) {
-    sm.ml[w][lane] = m_lane;
-    sm.ml[w][G + lane] = l_part;
+  if (!active || lc >= G) return;
+  // Lane (lc, lg) holds dims 32*lg .. +32 of head lc: element i of o[e] is
+  // dim 8*(4*lg + i) + e.
+  const size_t row = p.nchunk == 1 ? (size_t)kvh * G + lc
+                                   : ((size_t)kvh * p.nchunk + chunk) * G + lc;
+  float *dst = (p.nchunk == 1 ? p.out : p.part_o) + row * HD + 32 * lg;
+  const float sc = p.nchunk == 1 ? 1.0f / l_part : 1.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    *reinterpret_cast<f4 *>(dst + 8 * i) = f4{o[0][i], o[1][i], o[2][i], o[3][i]} * sc;
+    *reinterpret_cast<f4 *>(dst + 8 * i + 4) = f4{o[4][i], o[5][i], o[6][i], o[7][i]} * sc;
   }
-  if (lc < G) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sm.acc[w][lc][8 * (4 * lg + i) + e] = o[e][i];
-  }
-  __syncthreads();
-
-  constexpr int kOuts = G * HD / kThreads;  // outputs per thread
-  float o_val[kOuts], m_wg[kOuts], l_wg[kOuts];
-#pragma unroll
-  for (int oi = 0; oi < kOuts; ++oi) {
-    const int o = tid + oi * kThreads;
-    const int g = o / HD, d = o % HD;
-    float M = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, sm.ml[ww][g]);
-    const float Mu = M == -INFINITY ? 0.f : M;
-    float Ls = 0.f, O = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) {
-      float e = fast_exp2(sm.ml[ww][g] - Mu);
-      Ls = __builtin_fmaf(e, sm.ml[ww][G + g], Ls);
-      O = __builtin_fmaf(e, sm.acc[ww][g][d], O);
-    }
-    o_val[oi] = O;
-    m_wg[oi] = M;
-    l_wg[oi] = Ls;
-  }
-
-  if (p.nchunk == 1) {
-#pragma unroll
-    for (int oi = 0; oi < kOuts; ++oi)
-      p.out[(size_t)kvh * G * HD + tid + oi * kThreads] = o_val[oi] / l_wg[oi];
-    return;
-  }
-
-  const size_t pbase = ((size_t)kvh * p.nchunk + chunk) * G;
-#pragma unroll
-  for (int oi = 0; oi < kOuts; ++oi) {
-    const int o = tid + oi * kThreads;
-    p.part_o[pbase * HD + o] = o_val[oi];
-    if ((o % HD) == 0)
-      *reinterpret_cast<float2 *>(p.part_ml + (pbase + o / HD) * 2) = make_float2(m_wg[oi], l_wg[oi]);
-  }
+  if (p.nchunk > 1 && lg == 0)
+    *reinterpret_cast<float2 *>(p.part_ml + row * 2) = make_float2(m_lane, l_part);
 }
 
-// Cross-chunk log-sum-exp merge.  Workgroup = (kv head, q head, 32-dim block);
-// its 256 threads = 8 chunk groups x 32 dims, so each thread sums about
-// nchunk/8 independent partials.  A separate launch: the kernel boundary
-// orders the partial writes before these reads, where an in-kernel
-// last-arriver merge would need an agent-scope fence (an L2 write-back) in
-// every workgroup.
+// Cross-chunk log-sum-exp merge.  Workgroup = (kv head, q head, 32-dim
+// block); thread = (chunk group cg of 8, dim d).  Every load (the chunk
+// maxima and sums, and the thread's partial outputs) is issued before the
+// first reduction, so the merge costs one memory round trip.  A separate
+// launch: the kernel boundary orders the partial writes before these reads.
 __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
-  __shared__ float wt[kMaxChunks];
+  constexpr int kPer = kMaxChunks / 8;  // chunks per thread at most
+  __shared__ float mx[8];
   __shared__ float red[8][32];
-  __shared__ float stat[2];
+  __shared__ float wt[kMaxChunks];
+  __shared__ float lsum[8];
   const int db = blockIdx.x % 4;
   const int hg = blockIdx.x / 4;  // kvh * G + g
   const int kvh = hg / G, g = hg % G;
-  const int tid = threadIdx.x;
-  const size_t hb = (size_t)kvh * p.nchunk * G;
-  if (tid < 64) {
-    float M = -INFINITY;
-    for (int c = tid; c < p.nchunk; c += 64) M = fmaxf(M, p.part_ml[(hb + (size_t)c * G + g) * 2]);
-    M = wave_max(M);
-    float Ls = 0.f;
-    for (int c = tid; c < p.nchunk; c += 64) {
-      float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + (hb + (size_t)c * G + g) * 2);
-      float e = fast_exp2(ml.x - M);
-      wt[c] = e;
-      Ls = __builtin_fmaf(e, ml.y, Ls);
-    }
-    Ls = wave_sum(Ls);
-    if (tid == 0) stat[0] = 1.0f / Ls;
-  }
-  __syncthreads();
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int cg = tid >> 5, d = 32 * db + (tid & 31);
-  const float *src = p.part_o + (hb + g) * HD + d;
+  const size_t hb = (size_t)kvh * p.nchunk * G;
+  float2 ml = make_float2(-INFINITY, 0.f);
+  if (tid < p.nchunk) ml = *reinterpret_cast<const float2 *>(p.part_ml + (hb + (size_t)tid * G + g) * 2);
+  float ov[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int c = cg + 8 * k;
+    ov[k] = c < p.nchunk ? p.part_o[(hb + (size_t)c * G + g) * HD + d] : 0.f;
+  }
+  // max over chunks
+  float m = wave_max(ml.x);
+  if (lane == 0) mx[wv] = m;
+  __syncthreads();
+  float M = mx[0];
+#pragma unroll
+  for (int k = 1; k < 4; ++k) M = fmaxf(M, mx[k]);
+  const float Mu = M == -INFINITY ? 0.f : M;
+  const float e = ml.x == -INFINITY ? 0.f : fast_exp2(ml.x - Mu);
+  if (tid < kMaxChunks) wt[tid] = e;
+  float l = wave_sum(e * ml.y);
+  if (lane == 0) lsum[wv] = l;
+  __syncthreads();
   float O = 0.f;
-#pragma unroll 4
-  for (int c = cg; c < p.nchunk; c += 8) O = __builtin_fmaf(wt[c], src[(size_t)c * G * HD], O);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int c = cg + 8 * k;
+    if (c < p.nchunk) O = __builtin_fmaf(wt[c], ov[k], O);
+  }
   red[cg][tid & 31] = O;
   __syncthreads();
   if (tid < 32) {
     float t = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) t += red[k][tid];
-    p.out[(size_t)hg * HD + d] = t * stat[0];
+    const float Ls = lsum[0] + lsum[1] + lsum[2] + lsum[3];
+    p.out[(size_t)hg * HD + d] = t / Ls;
   }
 }
 
@@ -373,9 +403,10 @@ size_t decode_scratch_bytes(int n_kv, int g, int nchunk) {
 
 int decode_pick_nchunk(int L, int n_kv, int target_wgs) {
   const int n_tiles = (L + kTile - 1) / kTile;
-  // at least one tile per wave, at most kMaxChunks chunks
-  int nchunk = (target_wgs + n_kv - 1) / n_kv;
-  if (nchunk > n_tiles / kWaves) nchunk = n_tiles / kWaves;
+  // at least one tile per chunk, at most kMaxChunks chunks
+  const int hgroups = (n_kv + kWaves - 1) / kWaves;
+  int nchunk = (target_wgs + hgroups - 1) / hgroups;
+  if (nchunk > n_tiles) nchunk = n_tiles;
   if (nchunk > kMaxChunks) nchunk = kMaxChunks;
   if (nchunk < 1) nchunk = 1;
   return nchunk;
@@ -385,7 +416,7 @@ hipError_t launch_decode(const DecodeParams &p, int g, bool fused, hipStream_t s
                          hipEvent_t ev1) {
   if (g != G) return hipErrorInvalidValue;
   if (p.nchunk < 1 || p.nchunk > kMaxChunks) return hipErrorInvalidValue;
-  dim3 grid(p.n_kv * p.nchunk), block(kThreads);
+  dim3 grid(((p.n_kv + kWaves - 1) / kWaves) * p.nchunk), block(kThreads);
   if (fused)
     hipExtLaunchKernelGGL(decode_kernel<true>, grid, block, 0, s, ev0, ev1, 0, p);
   else
