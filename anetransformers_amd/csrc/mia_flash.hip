@@ -6,10 +6,10 @@
 // Rows are (query t, head g) pairs of one kv head, row = 4t + g, so the four
 // query heads of a group share every K/V tile.  A workgroup owns RT = 32*NB
 // rows (NB = 2 for prefill: 16 queries x 4 heads) and has four waves, one per
-// SIMD.  Every wave works on all RT rows over its own quarter of the key range
-// (a key group), so K/V tiles are private to a wave: no barrier in the tile
-// loop, and each fp16 K/V byte read from LDS feeds 64 rows of MFMA work.  The
-// four partial results are merged through LDS at the end.
+// SIMD.  Every wave works on all RT rows over every fourth 32-key tile of the
+// key range (a key group), so K/V tiles are private to a wave: no barrier in
+// the tile loop, and each fp16 K/V byte read from LDS feeds 64 rows of MFMA
+// work.  The four partial results are merged through LDS at the end.
 //
 // Per wave and 32-key tile:
 //   K, V tiles        global -> LDS directly (global_load_lds, 16 B per lane),
@@ -35,6 +35,8 @@
 // kernel wrote.  Masks are applied only to tiles that cross a window edge.
 // Very long key ranges over few rows are also split over workgroups and merged
 // by flash_merge_kernel.
+#include <type_traits>
+
 #include "mia_device.h"
 #include "mia_kernels.h"
 
@@ -108,40 +110,54 @@ __device__ __forceinline__ void dma16(const void *g, unsigned m) {
       : "v"(g), "s"(m)
       : "memory");
 }
-// Same with a wave-uniform base address and a per-lane 32-bit byte offset.
-__device__ __forceinline__ void dma16_sb(const void *base, unsigned voff, unsigned m) {
+// The 8 direct loads of a tile whose 32 rows are consecutive: two groups of
+// four, each under one M0 value (the LDS block of its first instruction).
+// The immediate offset applies to both the global and the LDS address, so
+// instruction jj of a group lands at M0 + 1024 jj and reads base + off[jj] +
+// 1024 jj: off[] carries the per-lane row/chunk offset minus 1024 jj.
+// base1 is base0 advanced by 16 rows, the second group's M0 is m + 4096.
+__device__ __forceinline__ void dma8_sb(const void *base0, const void *base1,
+                                        const unsigned (&off)[4], unsigned m) {
   unsigned saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %3\n\t"
+      "s_mov_b32 m0, %5\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %2\n\t"
+      "global_load_lds_dwordx4 %1, %6\n\t"
+      "global_load_lds_dwordx4 %2, %6 offset:1024\n\t"
+      "global_load_lds_dwordx4 %3, %6 offset:2048\n\t"
+      "global_load_lds_dwordx4 %4, %6 offset:3072\n\t"
+      "s_add_u32 m0, %5, 0x1000\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %7\n\t"
+      "global_load_lds_dwordx4 %2, %7 offset:1024\n\t"
+      "global_load_lds_dwordx4 %3, %7 offset:2048\n\t"
+      "global_load_lds_dwordx4 %4, %7 offset:3072\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "v"(voff), "s"(base), "s"(m)
+      : "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(m), "s"(base0), "s"(base1)
       : "memory");
 }
 
 // Issues the 8 direct loads of one tensor (K or V) of the 32-key tile kb..kb+31
-// (key range ending at ke) into the wave's tile at LDS byte address dst.
+// (ring slot of key kb: slot0; key range ending at ke) into the wave's tile
+// at LDS byte address dst.
 // Instruction j moves keys 4j..4j+3: lane i fetches key 4j + i/16, logical
 // chunk (i%16) ^ swz(key), which the hardware writes at byte 16*i of the
 // instruction's 1 KB block.  swz(4j + i/16) only depends on j through j mod 4,
-// so a tile of 32 consecutive ring slots takes a uniform base (row 4j) plus one
-// of four per-lane offsets boff[j % 4]; tiles that wrap, end early or reach
-// into the staging buffer take per-lane addresses.
+// so a tile of 32 consecutive ring slots takes a uniform base (row 0 or 16)
+// plus one of four per-lane offsets boff[j % 4] (in the form dma8_sb takes);
+// tiles that wrap, end early or reach into the staging buffer take per-lane
+// addresses.
 __device__ __forceinline__ void load_tile(const _Float16 *ring, const _Float16 *stage, int kb,
-                                          int ke, int start_pos, int max_seq, int kv_dim,
-                                          int kv_off, const unsigned *boff, int lane,
-                                          unsigned dst) {
-  const int slot0 = kb % max_seq;
+                                          int slot0, int ke, int start_pos, int max_seq,
+                                          int kv_dim, int kv_off, const unsigned (&boff)[4],
+                                          int lane, unsigned dst) {
   const bool contiguous =
       kb + kKT <= ke && slot0 + kKT <= max_seq && (stage == nullptr || kb + kKT <= start_pos);
   if (contiguous) {
     const _Float16 *base = ring + (size_t)slot0 * kv_dim;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      dma16_sb(base + (size_t)4 * j * kv_dim, boff[j & 3], dst + 1024u * j);
+    dma8_sb(base, base + (size_t)16 * kv_dim, boff, dst);
     return;
   }
   // kb through readfirstlane: keeps the per-lane keys of this rare path from
@@ -264,6 +280,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   const int g_first = (int)((long)w * nt / kWaves);
   const int g_count = (int)((long)(w + 1) * nt / kWaves) - g_first;
   const int kb0 = ks + kKT * g_first;
+  constexpr int kStride = kKT;
 
   // This lane's row in each 32-row block and its window; block-uniform bounds
   // (keys in [lo_max, hi_min] are inside every row's window of the block).
@@ -296,28 +313,24 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = 4 * j + (lane >> 4);
-    boff[j] = (unsigned)(r * kv_dim + kvh * HD + 8 * ((lane & 15) ^ swz(r))) * 2u -
-              (unsigned)(4 * j * kv_dim) * 2u;
+    boff[j] = (unsigned)(r * kv_dim + kvh * HD + 8 * ((lane & 15) ^ swz(r))) * 2u - 1024u * j;
   }
   const unsigned ka_b[2] = {kt_a[0] + ka_lane_base(lane), kt_a[1] + ka_lane_base(lane)};
   const unsigned va_b[2] = {vt_a[0] + va_lane_base(lane), vt_a[1] + va_lane_base(lane)};
   const _Float16 *const kc = p.kc, *const vc = p.vc;
   const _Float16 *const kst = p.kstage, *const vst = p.vstage;
-#define MIA_LOAD_K(i, buf)                                                                       \
-  load_tile(kc, kst, kb0 + kKT * (i), ke, p.start_pos, p.max_seq, kv_dim, kvh * HD, boff, lane, \
-            kt_a[buf])
-#define MIA_LOAD_V(i, buf)                                                                       \
-  load_tile(vc, vst, kb0 + kKT * (i), ke, p.start_pos, p.max_seq, kv_dim, kvh * HD, boff, lane, \
-            vt_a[buf])
+  auto tile_slot = [&](int i) { return (kb0 + kStride * i) % p.max_seq; };
+#define MIA_LOAD_K(i, buf)                                                                  \
+  load_tile(kc, kst, kb0 + kStride * (i), tile_slot(i), ke, p.start_pos, p.max_seq, kv_dim, \
+            kvh * HD, boff, lane, kt_a[buf])
+#define MIA_LOAD_V(i, buf)                                                                  \
+  load_tile(vc, vst, kb0 + kStride * (i), tile_slot(i), ke, p.start_pos, p.max_seq, kv_dim, \
+            kvh * HD, boff, lane, vt_a[buf])
+  // K0, K1, then V0: V(i) is first needed one step after K(i+1).
   auto issue_first_tiles = [&]() {
-    if (g_count > 0) {
-      MIA_LOAD_K(0, 0);
-      MIA_LOAD_V(0, 0);
-    }
-    if (g_count > 1) {
-      MIA_LOAD_K(1, 1);
-      MIA_LOAD_V(1, 1);
-    }
+    if (g_count > 0) MIA_LOAD_K(0, 0);
+    if (g_count > 1) MIA_LOAD_K(1, 1);
+    if (g_count > 0) MIA_LOAD_V(0, 0);
   };
   issue_first_tiles();
 
@@ -408,6 +421,26 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       s[i] = ok ? s[i] : -INFINITY;
     }
   };
+  // The same when no row of the tile has its window's first key inside it
+  // (kb >= lo_max of every block): only the upper edge, min(pos, ke - 1),
+  // is left, one compare per score against a per-lane limit.
+  auto mask_hi = [&](f16v &s, int b, int kb) {
+    const int hr = (valid[b] ? min(hi_t[b], ke - 1) : kb - 1) - kb - 4 * half;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = (i >> 2) * 8 + (i & 3) <= hr ? s[i] : -INFINITY;
+  };
+  auto mask_tile = [&](f16v (&sc)[NB], int kb) {
+    bool lo_free = true;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) lo_free = lo_free && kb >= lo_max[b];
+    if (lo_free) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) mask_hi(sc[b], b, kb);
+    } else {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) mask_block(sc[b], b, kb);
+    }
+  };
   // Row max of a score block over both key halves.
   auto block_max = [&](const f16v &s) {
     float m = fmaxf(s[0], s[1]);
@@ -428,72 +461,151 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       for (int st = 0; st < 8; ++st)
         sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st], sc[b], 0, 0, 0);
     }
-    if (needs_mask(kb)) {
-#pragma unroll
-      for (int b = 0; b < NB; ++b) mask_block(sc[b], b, kb);
-    }
+    if (needs_mask(kb)) mask_tile(sc, kb);
   };
 
   const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
-  // One tile step: P of tile it from s_cur (already shifted by the
-  // reference), shifted scores of tile it+1 into s_cur, O += P.V of tile it.
-  // K(it+1) is in kt[(it+1)&1], V(it) in vt[it&1].  The K and V operands are
-  // streamed in halves (k-steps 0-3 / 4-7, keys 0-15 / 16-31) to keep the
-  // register footprint within one wave per SIMD.
-  // One tile step: P of tile it from s_cur (already shifted by the
-  // reference), shifted scores of tile it+1 into s_cur, O += P.V of tile it,
-  // and the direct loads of tile it+2 when more2.  K(it+1) is in
-  // kt[(it+1)&1], V(it) in vt[it&1].  The K and V operands are streamed in
-  // halves (k-steps 0-3 / 4-7, keys 0-15 / 16-31) to keep the register
-  // footprint within one wave per SIMD.
-  auto step = [&](int it, bool more2) {
+  // One tile step, with P.V one tile behind the scores: P of tile it from
+  // s_cur (already shifted by the reference) into pb_next, shifted scores of
+  // tile it+1 into s_cur, and (from it = 1 on) O += P.V of tile it-1 from
+  // pb.  The 34 MFMAs of a step (scores of it+1, P.V of it-1) are then
+  // independent of the step's exponentials, which fill the issue slots
+  // between them.  K(it+1) is in kt[(it+1)&1], V(it-1) in vt[(it+1)&1]; the
+  // step refills kt[it&1] with K(it+2) at its start (K(it) was consumed by
+  // the previous step) and vt[(it+1)&1] with V(it+1) after its P.V reads.
+  // The K and V operands are streamed in halves (k-steps 0-3 / 4-7, keys
+  // 0-15 / 16-31) to keep the register footprint within one wave per SIMD.
+  h8 pb[NB][2];
+  // A single wave per SIMD issues everything in program order, so the step
+  // is written in its issue order and fenced (sched_barrier) into small
+  // groups: one or two MFMAs, then a slice of the exponentials, which then
+  // execute on the VALU while the MFMAs run.
+  auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
+  auto step = [&](int it, auto with_pv) {
     const unsigned kab = ka_b[(it + 1) & 1];
-    const unsigned vab = va_b[it & 1];
+    const unsigned vab = va_b[(it + 1) & 1];
     h8 ka[4], va[4];
 #pragma unroll
     for (int st = 0; st < 4; ++st) ka[st] = lds_read_h8(kab ^ (unsigned)(st << 5));
-    va[0] = read_va<0, 0>(vab);
-    va[1] = read_va<0, 1>(vab);
-    va[2] = read_va<0, 2>(vab);
-    va[3] = read_va<0, 3>(vab);
-    // P^T operands (keys 0..15 and 16..31 of the tile) and row sums.
-    h8 pb[NB][2];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      u4 pw[2];
-      float ls = l_run[b];
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) {
-        const float p0 = fast_exp2(s_cur[b][i]);
-        const float p1 = fast_exp2(s_cur[b][i + 1]);
-        const h2 pp = __builtin_convertvector((f2){p0, p1}, h2);
-        ls = __builtin_amdgcn_fdot2(pp, ones, ls, false);
-        pw[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(unsigned, pp);
-      }
-      l_run[b] = ls;
-      pb[b][0] = __builtin_bit_cast(h8, pw[0]);
-      pb[b][1] = __builtin_bit_cast(h8, pw[1]);
+    if (with_pv) {
+      va[0] = read_va<0, 0>(vab);
+      va[1] = read_va<0, 1>(vab);
+      va[2] = read_va<0, 2>(vab);
+      va[3] = read_va<0, 3>(vab);
     }
+    fence();
+    // Exponential slice j (0 .. 4 NB - 1): scores 4(j%4) .. +3 of row block j/4.
+    u4 pw[NB][2];
+    float ls[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) ls[b] = l_run[b];
+    auto exp_slice = [&](int j) {
+      const int b = j >> 2, i = 4 * (j & 3);
+      const float p0 = fast_exp2(s_cur[b][i]), p1 = fast_exp2(s_cur[b][i + 1]);
+      const float p2 = fast_exp2(s_cur[b][i + 2]), p3 = fast_exp2(s_cur[b][i + 3]);
+      const h2 pp0 = __builtin_convertvector((f2){p0, p1}, h2);
+      const h2 pp1 = __builtin_convertvector((f2){p2, p3}, h2);
+      ls[b] = __builtin_amdgcn_fdot2(pp0, ones, ls[b], false);
+      ls[b] = __builtin_amdgcn_fdot2(pp1, ones, ls[b], false);
+      pw[b][i >> 3][(i & 7) >> 1] = __builtin_bit_cast(unsigned, pp0);
+      pw[b][i >> 3][((i & 7) >> 1) + 1] = __builtin_bit_cast(unsigned, pp1);
+      // used only by the next step: pinned here so that the work is not
+      // sunk to the end of the step
+      asm volatile("" ::"v"(pp0), "v"(pp1), "v"(ls[b]));
+    };
     f16v s_next[NB];
+    auto qk = [&](int st, int b) {
+      s_next[b] =
+          __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st & 3], qb[b][st], s_next[b], 0, 0, 0);
+    };
+    // scores of tile it+1: reference k-step, then k-steps 0-3
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) s_next[b][i] = 0.f;
       s_next[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kx, qx[b], s_next[b], 0, 0, 0);
     }
+    fence();
+    exp_slice(0);
+    fence();
 #pragma unroll
-    for (int st = 0; st < 4; ++st)
+    for (int b = 0; b < NB; ++b) qk(0, b);
+    fence();
+    // K(it) was consumed by the previous step: its buffer takes K(it+2)
+    if (it + 2 < g_count) MIA_LOAD_K(it + 2, it & 1);
+    exp_slice(1);
+    fence();
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
-        s_next[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st], s_next[b], 0, 0, 0);
+    for (int b = 0; b < NB; ++b) qk(1, b);
+    fence();
+    exp_slice(2);
+    fence();
+#pragma unroll
+    for (int b = 0; b < NB; ++b) qk(2, b);
+    fence();
+    exp_slice(3);
+    fence();
+#pragma unroll
+    for (int b = 0; b < NB; ++b) qk(3, b);
+    fence();
 #pragma unroll
     for (int st = 0; st < 4; ++st) ka[st] = lds_read_h8(kab ^ (unsigned)((st + 4) << 5));
-    // The direct loads of tile it+2 are issued inside the step, K here (its
-    // buffer held K(it), consumed by the previous step) and V after the
-    // P.V MFMAs (its buffer holds V(it)): issued at the top of the
-    // iteration they would stall the wave on the address queue before any
-    // MFMA is queued.
-    if (more2) MIA_LOAD_K(it + 2, it & 1);
+    fence();
+    // P.V of tile it-1, keys 0-15, interleaved with the rest of the slices
+    int sl = 4;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      if (with_pv) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pb[b][0]);
+      }
+      fence();
+      if (sl < 4 * NB) exp_slice(sl);  // NB = 1 has four slices only
+      ++sl;
+      fence();
+    }
+    if (with_pv) {
+      va[0] = read_va<1, 0>(vab);
+      va[1] = read_va<1, 1>(vab);
+      va[2] = read_va<1, 2>(vab);
+      va[3] = read_va<1, 3>(vab);
+    }
+    fence();
+    // k-steps 4-7 and P.V keys 16-31, alternating
+#pragma unroll
+    for (int st = 4; st < 8; ++st) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) qk(st, b);
+      if (with_pv) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) mfma_pv(o[b][st - 4], va[st - 4], pb[b][1]);
+      }
+      fence();
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      l_run[b] = ls[b];
+      pb[b][0] = __builtin_bit_cast(h8, pw[b][0]);
+      pb[b][1] = __builtin_bit_cast(h8, pw[b][1]);
+    }
+    if (it + 1 < g_count) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // V(it-1) reads done
+      MIA_LOAD_V(it + 1, (it + 1) & 1);
+    }
+    // Window mask of tile it+1, only where it crosses a window edge.
+    const int kbn = kb0 + kStride * (it + 1);
+    if (needs_mask(kbn)) mask_tile(s_next, kbn);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) s_cur[b] = s_next[b];
+  };
+  // O += P.V of the wave's last tile (its V in vt[(g_count-1)&1]).
+  auto last_pv = [&]() {
+    const unsigned vab = va_b[(g_count - 1) & 1];
+    h8 va[4];
+    va[0] = read_va<0, 0>(vab);
+    va[1] = read_va<0, 1>(vab);
+    va[2] = read_va<0, 2>(vab);
+    va[3] = read_va<0, 3>(vab);
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -503,36 +615,20 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     va[2] = read_va<1, 2>(vab);
     va[3] = read_va<1, 3>(vab);
 #pragma unroll
-    for (int st = 0; st < 4; ++st)
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-        s_next[b] =
-            __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st + 4], s_next[b], 0, 0, 0);
-#pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pb[b][1]);
-    if (more2) {
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // V(it) reads done
-      MIA_LOAD_V(it + 2, it & 1);
-    }
-    // Window mask of tile it+1, only where it crosses a window edge.
-    const int kbn = kb0 + kKT * (it + 1);
-    if (needs_mask(kbn)) {
-#pragma unroll
-      for (int b = 0; b < NB; ++b) mask_block(s_next[b], b, kbn);
-    }
-#pragma unroll
-    for (int b = 0; b < NB; ++b) s_cur[b] = s_next[b];
   };
 
   // Does the lane's row of block b have a key in this wave's range?
   bool has_keys[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
-    const int k0 = max(lo_t[b], kb0);
-    const int k1 = min(min(hi_t[b], ke - 1), kb0 + kKT * g_count - 1);
-    has_keys[b] = valid[b] && g_count > 0 && k0 <= k1;
+    // first tile of the wave ending at or after the row's first key
+    const int k0 = max(lo_t[b], ks), k1 = min(hi_t[b], ke - 1);
+    const int ahead = k0 - (kb0 + kKT - 1);
+    const int i0 = ahead <= 0 ? 0 : (ahead + kStride - 1) / kStride;
+    has_keys[b] = valid[b] && k0 <= k1 && i0 < g_count && kb0 + kStride * i0 <= k1;
   }
 
   for (int pass = 0; pass < 2; ++pass) {
@@ -545,7 +641,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
         MIA_LOAD_K(i, 0);
         wait_vmcnt<0>();
         f16v sc[NB];
-        scores(sc, 0, kb0 + kKT * i);
+        scores(sc, 0, kb0 + kStride * i);
 #pragma unroll
         for (int b = 0; b < NB; ++b) mt[b] = fmaxf(mt[b], block_max(sc[b]));
       }
@@ -564,7 +660,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     // The first tile's scores set the reference (first pass) and are
     // shifted by it.
     if (g_count > 0) {
-      if (g_count > 1) wait_vmcnt<24>();
+      if (g_count > 1) wait_vmcnt<16>();  // K1 and V0 may be pending
       else wait_vmcnt<8>();
       scores(s_cur, 0, kb0);
 #pragma unroll
@@ -579,13 +675,20 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       for (int b = 0; b < NB; ++b) set_ref(b, -INFINITY);
     }
 
-    // Tiles 0 and 1 came from issue_first_tiles; step it issues K(it+2),
-    // then V(it+2).  Before step it, K(it+1) and V(it) must have landed:
-    // only V(it+1), the last load issued (when it exists), may be pending.
-    for (int it = 0; it < g_count; ++it) {
-      if (it + 1 < g_count) wait_vmcnt<8>();
-      else wait_vmcnt<0>();
-      step(it, it + 2 < g_count);
+    // Loads are issued in the order K0 K1 V0 | K2 V1 | K3 V2 | ... (step it
+    // issues K(it+2), then V(it+1)).  Step it needs K(it+1) and V(it-1): only
+    // V(it), the last load issued, may still be pending.
+    if (g_count > 0) {
+      wait_vmcnt<8>();
+      step(0, std::false_type{});
+    }
+    for (int it = 1; it < g_count; ++it) {
+      wait_vmcnt<8>();
+      step(it, std::true_type{});
+    }
+    if (g_count > 0) {
+      wait_vmcnt<0>();
+      last_pv();
     }
     // Row sums: overflow (not finite) or underflow (< 2^-8 with keys in range)
     // means the reference did not suit the row.
