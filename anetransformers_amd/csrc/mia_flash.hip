@@ -338,24 +338,44 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   // pos) cos/sin written by the K rotation, mistral_model.h:87-105) and the
   // score scale folded in.  Rows past the last query are zero.
   lds_half *qs = lds + L::kBufBytes / 2;
-  for (int u = tid; u < RT * 16; u += 256) {
+  // All loads of the thread's items are issued before any is used (one
+  // memory round trip, not one per item); rows past the last query read the
+  // last query's row and store zeros.
+  constexpr int kQItems = RT * 16 / 256;
+  const bool rope = p.rope_cs != nullptr;
+  f4 qv[kQItems][2], cv[kQItems][2];
+#pragma unroll
+  for (int k = 0; k < kQItems; ++k) {
+    const int u = tid + 256 * k;
     const int rl = u >> 4, ch = u & 15;
     const int row = row0 + rl;
-    const int t = row >> 2, g = row & 3;
+    const int t = min(row >> 2, p.S - 1), g = row & 3;
+    const f4 *src = reinterpret_cast<const f4 *>(p.Q + (size_t)t * dim_model +
+                                                 (size_t)(kvh * 4 + g) * HD + 8 * ch);
+    qv[k][0] = src[0];
+    qv[k][1] = src[1];
+    if (rope) {
+      const f4 *cs = reinterpret_cast<const f4 *>(p.rope_cs + ((size_t)t * 64 + 4 * ch) * 2);
+      cv[k][0] = cs[0];
+      cv[k][1] = cs[1];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kQItems; ++k) {
+    const int u = tid + 256 * k;
+    const int rl = u >> 4, ch = u & 15;
+    const int t = (row0 + rl) >> 2;
+    const f4 a = qv[k][0], b = qv[k][1];
+    float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    if (rope) {
+      const f4 c0 = cv[k][0], c1 = cv[k][1];
+      rope_pair(v[0], v[1], c0.x, c0.y);
+      rope_pair(v[2], v[3], c0.z, c0.w);
+      rope_pair(v[4], v[5], c1.x, c1.y);
+      rope_pair(v[6], v[7], c1.z, c1.w);
+    }
     u4 packed = {0u, 0u, 0u, 0u};
     if (t < p.S) {
-      const f4 *src = reinterpret_cast<const f4 *>(p.Q + (size_t)t * dim_model +
-                                                   (size_t)(kvh * 4 + g) * HD + 8 * ch);
-      const f4 a = src[0], b = src[1];
-      float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-      if (p.rope_cs != nullptr) {
-        const f4 *cs = reinterpret_cast<const f4 *>(p.rope_cs + ((size_t)t * 64 + 4 * ch) * 2);
-        const f4 c0 = cs[0], c1 = cs[1];
-        rope_pair(v[0], v[1], c0.x, c0.y);
-        rope_pair(v[2], v[3], c0.z, c0.w);
-        rope_pair(v[4], v[5], c1.x, c1.y);
-        rope_pair(v[6], v[7], c1.z, c1.w);
-      }
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         packed[e] = __builtin_bit_cast(
