@@ -277,8 +277,17 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   const int ks = klo + split * p.split_keys;
   const int ke = min(ks + p.split_keys, khi + 1);
   const int nt = ke > ks ? (ke - ks + kKT - 1) / kKT : 0;
-  const int g_first = (int)((long)w * nt / kWaves);
-  const int g_count = (int)((long)(w + 1) * nt / kWaves) - g_first;
+  // When the range ends at the causal edge, its last key group holds the
+  // masked tiles, the short last tile with its per-lane loads and the keys
+  // just written by the K rotation, about two plain tiles' worth: the range
+  // is then split as if it had two tiles more, the last group's share ending
+  // at the real end.
+  const int extra = ke == khi + 1 ? 2 : 0;
+  auto group_start = [&](int g) {
+    return g == kWaves ? nt : min(nt, (int)((long)g * (nt + extra) / kWaves));
+  };
+  const int g_first = group_start(w);
+  const int g_count = group_start(w + 1) - g_first;
   const int kb0 = ks + kKT * g_first;
   constexpr int kStride = kKT;
 
