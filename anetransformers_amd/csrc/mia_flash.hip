@@ -35,6 +35,7 @@
 // kernel wrote.  Masks are applied only to tiles that cross a window edge.
 // Very long key ranges over few rows are also split over workgroups and merged
 // by flash_merge_kernel.
+#include <climits>
 #include <type_traits>
 
 #include "mia_device.h"
@@ -442,19 +443,25 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   };
   // Keys outside the row's window become -inf; s[i] is key
   // kb + (i/4)*8 + 4*half + (i%4) for the lane's row.
+  // (The row bounds pass through an empty asm so that the compiler cannot
+  // evaluate the per-score compares once for all tiles, ahead of the loop:
+  // masks are rare, and the hoisted lane masks would be spilled.)
   auto mask_block = [&](f16v &s, int b, int kb) {
+    int lo = valid[b] ? lo_t[b] - kb - 4 * half : INT_MAX;
+    int hi = min(hi_t[b], ke - 1) - kb - 4 * half;
+    asm volatile("" : "+v"(lo), "+v"(hi));
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int key = kb + (i >> 2) * 8 + 4 * half + (i & 3);
-      const bool ok = valid[b] && key >= lo_t[b] && key <= hi_t[b] && key < ke;
-      s[i] = ok ? s[i] : -INFINITY;
+      const int off = (i >> 2) * 8 + (i & 3);
+      s[i] = off >= lo && off <= hi ? s[i] : -INFINITY;
     }
   };
   // The same when no row of the tile has its window's first key inside it
   // (kb >= lo_max of every block): only the upper edge, min(pos, ke - 1),
   // is left, one compare per score against a per-lane limit.
   auto mask_hi = [&](f16v &s, int b, int kb) {
-    const int hr = (valid[b] ? min(hi_t[b], ke - 1) : kb - 1) - kb - 4 * half;
+    int hr = (valid[b] ? min(hi_t[b], ke - 1) : kb - 1) - kb - 4 * half;
+    asm volatile("" : "+v"(hr));
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[i] = (i >> 2) * 8 + (i & 3) <= hr ? s[i] : -INFINITY;
   };
