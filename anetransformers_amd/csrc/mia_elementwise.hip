@@ -50,6 +50,20 @@ __global__ void __launch_bounds__(128)
   const int t = blockIdx.x;
   const int tid = threadIdx.x;
   const int pos = start_pos + t;
+  const int kv_dim = n_kv * HD;
+  const int n_items = n_kv * (HD / 8);
+  // The K/V loads of the thread's first item are issued before the angles
+  // are formed, so that their latency overlaps the sincos and the barrier.
+  f4 k0 = {}, k1 = {}, v0 = {}, v1 = {};
+  if (tid < n_items) {
+    const int e0 = (tid >> 4) * HD + 8 * (tid & 15);
+    const f4 *ks = reinterpret_cast<const f4 *>(K + (size_t)t * kv_dim + e0);
+    const f4 *vs = reinterpret_cast<const f4 *>(V + (size_t)t * kv_dim + e0);
+    k0 = ks[0];
+    k1 = ks[1];
+    v0 = vs[0];
+    v1 = vs[1];
+  }
   if (tid < HD / 2) {
     const float ang = theta_inv[tid] * (float)pos;
     float sn, c;
@@ -58,13 +72,17 @@ __global__ void __launch_bounds__(128)
     if (cs_out) reinterpret_cast<float2 *>(cs_out)[(size_t)t * (HD / 2) + tid] = make_float2(c, sn);
   }
   __syncthreads();
-  const int kv_dim = n_kv * HD;
   const size_t drow = ring ? (size_t)(pos % max_seq) : (size_t)t;
-  for (int c = tid; c < n_kv * (HD / 8); c += blockDim.x) {
+  for (int c = tid; c < n_items; c += blockDim.x) {
     const int e0 = (c >> 4) * HD + 8 * (c & 15);
-    const f4 *ks = reinterpret_cast<const f4 *>(K + (size_t)t * kv_dim + e0);
-    const f4 *vs = reinterpret_cast<const f4 *>(V + (size_t)t * kv_dim + e0);
-    const f4 k0 = ks[0], k1 = ks[1], v0 = vs[0], v1 = vs[1];
+    if (c != tid) {
+      const f4 *ks = reinterpret_cast<const f4 *>(K + (size_t)t * kv_dim + e0);
+      const f4 *vs = reinterpret_cast<const f4 *>(V + (size_t)t * kv_dim + e0);
+      k0 = ks[0];
+      k1 = ks[1];
+      v0 = vs[0];
+      v1 = vs[1];
+    }
     float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
     const int p0 = 4 * (c & 15);
 #pragma unroll
