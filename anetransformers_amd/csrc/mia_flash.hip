@@ -81,7 +81,9 @@ struct Lay {
   // [NB*4 (block, dim block)][3 source waves][4 chunks][64 lanes][4 floats].
   static constexpr int kMergeBytes = NB * 4 * 3 * 4 * 64 * 16;
   static_assert(kMergeBytes <= kBufBytes, "merge area must fit the tile buffers");
-  static constexpr int kBytes = kBufBytes + kQBytes + kMLBytes;
+  // Prologue only: (cos, sin) rows of the wave's queries, 2 NB rows of 512 B.
+  static constexpr int kCSBytes = kWaves * 2 * NB * 512;
+  static constexpr int kBytes = kBufBytes + kQBytes + kMLBytes + kCSBytes;
 };
 
 template <int N>
@@ -309,6 +311,25 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     lo_max[b] = window_lo(p.start_pos + min(ts1, p.S - 1), p.max_seq);
     hi_min[b] = p.start_pos + ts0;
   }
+  // Does the lane's row of block b have a key in this wave's range?
+  bool has_keys[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    // first tile of the wave ending at or after the row's first key
+    const int k0 = max(lo_t[b], ks), k1 = min(hi_t[b], ke - 1);
+    const int ahead = k0 - (kb0 + kKT - 1);
+    const int i0 = ahead <= 0 ? 0 : (ahead + kStride - 1) / kStride;
+    has_keys[b] = valid[b] && k0 <= k1 && i0 < g_count && kb0 + kStride * i0 <= k1;
+  }
+  // The row bounds are formed here, before the first loads are issued, and
+  // not where they are first used (after the wait for Q): pinned, so that the
+  // compiler does not sink them into the critical path.
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    int hk = has_keys[b], vb = valid[b], bf = bfull[b];
+    asm volatile("" ::"v"(lo_t[b]), "v"(hi_t[b]), "v"(hk), "v"(vb), "s"(bf), "s"(lo_max[b]),
+                 "s"(hi_min[b]));
+  }
 
   // Wave-private tile buffers and this lane's direct-load offsets.
   lds_half *kt[2], *vt[2];
@@ -342,43 +363,49 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     if (g_count > 1) MIA_LOAD_K(1, 1);
     if (g_count > 0) MIA_LOAD_V(0, 0);
   };
-  issue_first_tiles();
-
-  // Q rows -> fp16 in LDS, 8 dims per item: RoPE (table of fl32(theta_inv[i] *
-  // pos) cos/sin written by the K rotation, mistral_model.h:87-105) and the
-  // score scale folded in.  Rows past the last query are zero.
+  // Q rows -> fp16 in LDS: RoPE (table of fl32(theta_inv[i] * pos) cos/sin
+  // written by the K rotation, mistral_model.h:87-105) and the score scale
+  // folded in; rows past the last query are zero.  Each wave stages its own
+  // 8 NB rows (queries 2 NB w ..) as fp32, and their (cos, sin) rows, with
+  // direct loads issued before the first tiles' (the Q rows then wait for
+  // nothing issued after them); V1's buffer holds the rows until V1 is loaded.
   lds_half *qs = lds + L::kBufBytes / 2;
-  // All loads of the thread's items are issued before any is used (one
-  // memory round trip, not one per item); rows past the last query read the
-  // last query's row and store zeros.
-  constexpr int kQItems = RT * 16 / 256;
   const bool rope = p.rope_cs != nullptr;
-  f4 qv[kQItems][2], cv[kQItems][2];
+  const unsigned qstage = kt_a[0] + 3u * L::kTileHalfs * 2u;  // == vt_a[1]
+  const unsigned csstage =
+      lds_addr(lds + (L::kBufBytes + L::kQBytes + L::kMLBytes) / 2) + (unsigned)w * 1024u * NB;
+  const int wq0 = tq0 + 2 * NB * w;  // first query of this wave's rows
 #pragma unroll
-  for (int k = 0; k < kQItems; ++k) {
-    const int u = tid + 256 * k;
-    const int rl = u >> 4, ch = u & 15;
-    const int row = row0 + rl;
-    const int t = min(row >> 2, p.S - 1), g = row & 3;
-    const f4 *src = reinterpret_cast<const f4 *>(p.Q + (size_t)t * dim_model +
-                                                 (size_t)(kvh * 4 + g) * HD + 8 * ch);
-    qv[k][0] = src[0];
-    qv[k][1] = src[1];
-    if (rope) {
-      const f4 *cs = reinterpret_cast<const f4 *>(p.rope_cs + ((size_t)t * 64 + 4 * ch) * 2);
-      cv[k][0] = cs[0];
-      cv[k][1] = cs[1];
+  for (int j = 0; j < 4 * NB; ++j) {  // query j/2, heads 2(j&1) .. +1
+    const int tq = min(wq0 + (j >> 1), p.S - 1);
+    dma16(p.Q + (size_t)tq * dim_model + (size_t)(kvh * 4 + 2 * (j & 1)) * HD + 4 * lane,
+          qstage + 1024u * j);
+  }
+  if (rope) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {  // queries 2j, 2j+1 of the wave
+      const int tq = min(wq0 + 2 * j + (lane >> 5), p.S - 1);
+      dma16(p.rope_cs + (size_t)tq * HD + 4 * (lane & 31), csstage + 1024u * j);
     }
   }
+  issue_first_tiles();
+  // the Q rows are in once at most the tile loads issued after them are pending
+  if (g_count > 1) wait_vmcnt<24>();
+  else if (g_count == 1) wait_vmcnt<16>();
+  else wait_vmcnt<0>();
 #pragma unroll
-  for (int k = 0; k < kQItems; ++k) {
-    const int u = tid + 256 * k;
-    const int rl = u >> 4, ch = u & 15;
+  for (int k = 0; k < 2 * NB; ++k) {
+    const int u = lane + 64 * k;
+    const int rw = u >> 4, ch = u & 15;  // row within the wave's rows, 8-dim chunk
+    const int rl = 8 * NB * w + rw;
     const int t = (row0 + rl) >> 2;
-    const f4 a = qv[k][0], b = qv[k][1];
+    const f4 a = *(const lds_f4 *)(__UINTPTR_TYPE__)(qstage + 512u * rw + 32u * ch);
+    const f4 b = *(const lds_f4 *)(__UINTPTR_TYPE__)(qstage + 512u * rw + 32u * ch + 16u);
     float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     if (rope) {
-      const f4 c0 = cv[k][0], c1 = cv[k][1];
+      const unsigned ca = csstage + 512u * (rw >> 2) + 32u * ch;
+      const f4 c0 = *(const lds_f4 *)(__UINTPTR_TYPE__)ca;
+      const f4 c1 = *(const lds_f4 *)(__UINTPTR_TYPE__)(ca + 16u);
       rope_pair(v[0], v[1], c0.x, c0.y);
       rope_pair(v[2], v[3], c0.z, c0.w);
       rope_pair(v[4], v[5], c1.x, c1.y);
@@ -655,17 +682,6 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
 #pragma unroll
       for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pb[b][1]);
   };
-
-  // Does the lane's row of block b have a key in this wave's range?
-  bool has_keys[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    // first tile of the wave ending at or after the row's first key
-    const int k0 = max(lo_t[b], ks), k1 = min(hi_t[b], ke - 1);
-    const int ahead = k0 - (kb0 + kKT - 1);
-    const int i0 = ahead <= 0 ? 0 : (ahead + kStride - 1) / kStride;
-    has_keys[b] = valid[b] && k0 <= k1 && i0 < g_count && kb0 + kStride * i0 <= k1;
-  }
 
   for (int pass = 0; pass < 2; ++pass) {
     if (pass == 1) {
