@@ -17,6 +17,10 @@ of one launch by the dominant kernel's average duration, taken from HIP event
 pairs that the kernel's own dispatch stamps (mia_profile_begin/end) during a
 second pass over the same timed loop.
 
+configs: the other config shapes (a 513-position single layer, a 4097-position
+32-layer decode, the 8-draft verify on a wrapped 65536-slot ring), each with
+its oracle CPU timing: reported beside the headline, not as it.
+
 dropin: the same decode step through the C drop-in (mia_dropin_decode_step)
 with host q/k/v/out buffers, synchronous per layer as the reference's call
 site is: the PCIe-inclusive rate, reported beside the headline, never as it.
@@ -269,6 +273,106 @@ def cpu_baseline_prefill(n_layers: int = 2):
     }
 
 
+class OtherConfigs:
+    """The remaining config shapes, reported beside the headline: a single
+    512-position decode layer (M 4096), a 32-layer decode at 4097 positions
+    (M 65536), and a 32-layer speculative verify of 8 drafts at positions
+    70000..70007 on a wrapped 65536-slot ring (staged drafts, then commit)."""
+
+    def __init__(self, lib, seed: int = 21):
+        self.lib = lib
+        g = np.random.default_rng(seed)
+        self.th = DeviceBuffer.from_array(theta_inv())
+        # config 1: one layer, M 4096, positions 0..511 filled
+        self.c1_kc = DeviceBuffer(4096 * KV_DIM * 2)
+        self.c1_vc = DeviceBuffer(4096 * KV_DIM * 2)
+        self.c1_kc.zero()
+        self.c1_vc.zero()
+        check(lib.mia_fill_normal_f16(self.c1_kc.ptr, 512 * KV_DIM, 31, None))
+        check(lib.mia_fill_normal_f16(self.c1_vc.ptr, 512 * KV_DIM, 32, None))
+        # configs 2 and 5: 32 layers of 65536-slot rings, every slot filled
+        self.big = N_LAYERS * 65536 * KV_DIM
+        self.kc = DeviceBuffer(self.big * 2)
+        self.vc = DeviceBuffer(self.big * 2)
+        check(lib.mia_fill_normal_f16(self.kc.ptr, self.big, 33, None))
+        check(lib.mia_fill_normal_f16(self.vc.ptr, self.big, 34, None))
+        self.q = DeviceBuffer.from_array(g.standard_normal((N_LAYERS, 8, N_HEADS * HD), np.float32))
+        self.k = DeviceBuffer.from_array(g.standard_normal((N_LAYERS, 8, KV_DIM), np.float32))
+        self.v = DeviceBuffer.from_array(g.standard_normal((N_LAYERS, 8, KV_DIM), np.float32))
+        self.out = DeviceBuffer(N_LAYERS * 8 * N_HEADS * HD * 4)
+        check(lib.mia_device_sync())
+
+    def _args(self, l, S):
+        return (self.q.ptr + l * 8 * N_HEADS * HD * 4, self.k.ptr + l * 8 * KV_DIM * 4,
+                self.v.ptr + l * 8 * KV_DIM * 4, self.th.ptr)
+
+    def c1(self) -> None:
+        q, k, v, th = self._args(0, 1)
+        check(self.lib.mia_decode_step(q, k, v, th, self.c1_kc.ptr, self.c1_vc.ptr, self.out.ptr,
+                                       N_HEADS, N_KV, HD, 4096, 512, None), "decode_step")
+
+    def c2(self) -> None:
+        lay = 65536 * KV_DIM * 2
+        for l in range(N_LAYERS):
+            q, k, v, th = self._args(l, 1)
+            check(self.lib.mia_decode_step(q, k, v, th, self.kc.ptr + l * lay, self.vc.ptr + l * lay,
+                                           self.out.ptr + l * N_HEADS * HD * 4, N_HEADS, N_KV, HD,
+                                           65536, 4096, None), "decode_step")
+
+    def c5(self) -> None:
+        lay = 65536 * KV_DIM * 2
+        for l in range(N_LAYERS):
+            q, k, v, th = self._args(l, 8)
+            check(self.lib.mia_attention_step(q, k, v, th, self.kc.ptr + l * lay,
+                                              self.vc.ptr + l * lay,
+                                              self.out.ptr + l * 8 * N_HEADS * HD * 4, N_HEADS,
+                                              N_KV, HD, 65536, 70000, 8, None), "attention_step")
+
+
+def cpu_other_configs():
+    """Oracle timing (same thread count as the headline baseline) on bounded
+    samples of configs 1, 2 and 5."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import _oracle as O
+
+    g = np.random.default_rng(13)
+    threads = O.num_threads(fast=True)
+    res = {}
+    # config 1: 1 layer, M 4096, pos 512 (L 513)
+    kc = g.standard_normal((1, 4096, KV_DIM), np.float32).astype(np.float16).view(np.uint16)
+    vc = g.standard_normal((1, 4096, KV_DIM), np.float32).astype(np.float16).view(np.uint16)
+    Q = g.standard_normal((1, N_HEADS * HD), np.float32)
+    O.decode_layers(Q, kc, vc, 1, N_HEADS, N_HEADS // N_KV, HD, 4096, 512, threads=threads)
+    t0 = time.perf_counter()
+    for _ in range(20):
+        O.decode_layers(Q, kc, vc, 1, N_HEADS, N_HEADS // N_KV, HD, 4096, 512, threads=threads)
+    dt = (time.perf_counter() - t0) / 20
+    res["1"] = {"value": round(4096 * 513 / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "kind": "port", "sample": "the whole config (1 layer), mean of 20"}
+    # config 2: 4 of 32 layers, M 65536, pos 4096 (L 4097)
+    n = 4
+    kc = g.standard_normal((n, 65536, KV_DIM), np.float32).astype(np.float16).view(np.uint16)
+    vc = g.standard_normal((n, 65536, KV_DIM), np.float32).astype(np.float16).view(np.uint16)
+    Q = g.standard_normal((n, N_HEADS * HD), np.float32)
+    t0 = time.perf_counter()
+    O.decode_layers(Q, kc, vc, n, N_HEADS, N_HEADS // N_KV, HD, 65536, 4096, threads=threads)
+    dt = time.perf_counter() - t0
+    res["2"] = {"value": round(n * 4096 * 4097 / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "kind": "port", "sample": f"{n} of 32 layers"}
+    # config 5: 1 of 32 layers, 8 queries over the wrapped 65536-slot window
+    Q = g.standard_normal((1, 8, N_HEADS * HD), np.float32)
+    t0 = time.perf_counter()
+    O.attention_batch_layers(Q, kc[:1], vc[:1], 1, N_HEADS, N_KV, HD, 65536, 70000, 8,
+                             threads=threads)
+    dt = time.perf_counter() - t0
+    res["5"] = {"value": round(4096 * 65536 / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "kind": "port",
+                "sample": "1 of 32 layers: attention of the 8 queries over the wrapped window "
+                          "(attention_batch on the same shape; the drafts' ring writes are not "
+                          "timed)"}
+    return res
+
+
 def load_traffic(name: str):
     """HBM bytes per launch measured with rocprofv3 --pmc (profiles/), or None."""
     path = os.path.join(REPO, "profiles", "traffic.json")
@@ -287,6 +391,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-decode", action="store_true", help="prefill only (profiling)")
+    ap.add_argument("--skip-configs", action="store_true",
+                    help="skip the side configs 1, 2 and 5 (profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 5 device-to-device copies of 512 MiB (a copy kernel of known "
                          "size, to scale HBM byte counters)")
@@ -350,6 +456,31 @@ def main() -> int:
         }
         del pf
 
+    configs = None
+    if not args.skip_configs and not args.skip_decode:
+        log("other configs: 1 (L 513), 2 (32 x L 4097), 5 (32 x verify S 8 on a wrapped ring)")
+        oc = OtherConfigs(lib)
+        c1 = timed(lib, oc.c1, 200, 20)
+        c2 = timed(lib, oc.c2, args.steps, args.warmup)
+        c5 = timed(lib, oc.c5, args.steps, args.warmup)
+        del oc
+        configs = {
+            "1": {"workload": "1 layer decode step, 512 filled positions + new token (L 513), M 4096",
+                  "value": round(4096 * 513 / (c1 * 1e-3) / 1e9, 2), "unit": "GB/s",
+                  "ms_per_step": round(c1, 5)},
+            "2": {"workload": "32-layer decode step, 4096 filled + new token (L 4097), M 65536",
+                  "value": round(N_LAYERS * 4096 * 4097 / (c2 * 1e-3) / 1e9, 2), "unit": "GB/s",
+                  "ms_per_step": round(c2, 4)},
+            "3": {"workload": "the headline (value)"},
+            "4": {"workload": "the prefill object"},
+            "5": {"workload": "32-layer speculative verify, 8 drafts at positions 70000..70007 "
+                              "on a wrapped 65536-slot ring (staged drafts, committed after "
+                              "attention)",
+                  "value": round(N_LAYERS * 4096 * 65536 / (c5 * 1e-3) / 1e9, 2), "unit": "GB/s",
+                  "ms_per_step": round(c5, 4)},
+        }
+        log(f"config 1: {c1 * 1e3:.1f} us; config 2: {c2:.3f} ms; config 5: {c5:.3f} ms")
+
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline: decode sample")
@@ -357,6 +488,10 @@ def main() -> int:
         if prefill is not None:
             log("cpu baseline: prefill sample")
             prefill["cpu_baseline"] = cpu_baseline_prefill()
+        if configs is not None:
+            log("cpu baseline: configs 1, 2, 5")
+            for k, v in cpu_other_configs().items():
+                configs[k]["cpu_baseline"] = v
 
     line = {
         "metric": "decode attn HBM GB/s (% peak) @32K ctx; prefill attn TFLOPS (% MFMA peak)",
@@ -386,6 +521,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "dropin": dropin,
         "prefill": prefill,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
     return 0
