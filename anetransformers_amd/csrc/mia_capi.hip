@@ -181,9 +181,12 @@ int decode_impl(const float *q, const float *k, const float *v, const float *the
   return MIA_OK;
 }
 
+// With commit, the staged drafts kst/vst are copied into the ring after the
+// attention: by the split merge kernel when there is one, else by a copy
+// kernel.
 int flash_impl(DevCtx *c, const float *Q, const float *rope_cs, const uint16_t *kst,
                const uint16_t *vst, const uint16_t *k_layer, const uint16_t *v_layer, float *out,
-               int n_kv, int max_seq, int start_pos, int S, hipStream_t s) {
+               int n_kv, int max_seq, int start_pos, int S, hipStream_t s, bool commit = false) {
   mia::FlashParams p{};
   int rt = 0;
   mia::flash_plan(S, n_kv, kG, start_pos, max_seq, c->num_cus, &p.n_rtiles, &p.nsplit,
@@ -209,8 +212,15 @@ int flash_impl(DevCtx *c, const float *Q, const float *rope_cs, const uint16_t *
   }
   hipEvent_t ev0, ev1;
   if (int rc = prof_pair(c, 1, &ev0, &ev1)) return rc;
+  if (commit && p.nsplit > 1) {
+    p.commit_k = reinterpret_cast<_Float16 *>(const_cast<uint16_t *>(k_layer));
+    p.commit_v = reinterpret_cast<_Float16 *>(const_cast<uint16_t *>(v_layer));
+  }
   HIP_TRY(mia::launch_flash(p, kG, s, ev0, ev1));
   HIP_TRY(mia::launch_flash_merge(p, s));
+  if (commit && p.nsplit == 1)
+    HIP_TRY(mia::launch_commit(const_cast<_Float16 *>(p.kc), const_cast<_Float16 *>(p.vc),
+                               p.kstage, p.vstage, S, start_pos, max_seq, n_kv * kHD, s));
   return MIA_OK;
 }
 
@@ -494,14 +504,9 @@ int mia_attention_step(const float *Q, const float *K, const float *V, const flo
   _Float16 *kst = reinterpret_cast<_Float16 *>(reinterpret_cast<char *>(c->work) + cs_bytes);
   _Float16 *vst = kst + (size_t)S * kv_dim;
   HIP_TRY(mia::launch_rope_to_f16(K, V, theta_inv, S, start_pos, n_kv_heads, kst, vst, cs, s));
-  if (int rc = flash_impl(c, Q, cs, reinterpret_cast<uint16_t *>(kst),
-                          reinterpret_cast<uint16_t *>(vst), k_layer, v_layer, out, n_kv_heads,
-                          max_seq, start_pos, S, s))
-    return rc;
-  HIP_TRY(mia::launch_commit(reinterpret_cast<_Float16 *>(k_layer),
-                             reinterpret_cast<_Float16 *>(v_layer), kst, vst, S, start_pos, max_seq,
-                             kv_dim, s));
-  return MIA_OK;
+  return flash_impl(c, Q, cs, reinterpret_cast<uint16_t *>(kst),
+                    reinterpret_cast<uint16_t *>(vst), k_layer, v_layer, out, n_kv_heads, max_seq,
+                    start_pos, S, s, true);
 }
 
 }  // extern "C"

@@ -847,34 +847,87 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   }
 }
 
-// Split merge: one workgroup per 8 rows of a tile, thread = (row, 4 dims).  A
-// separate launch, so the kernel boundary orders the partial writes before
-// these reads.
+// Split merge: one workgroup per row of a tile.  Thread = (split group sg of
+// 32, 16 dims): it holds splits sg, sg+32, ... of its dims, all loaded before
+// the first reduction (one memory round trip however many splits there
+// are), then the splits are reduced through LDS.  With p.commit_k set, the
+// first S workgroups also copy the staged drafts into their ring slots: the
+// kernel boundary orders that after every read of the ring by the attention
+// kernel.  A separate launch, so the boundary also orders the partial writes
+// before these reads.
+constexpr int kMergeSplitsPerThread = 8;  // 256 splits at most
 __global__ void __launch_bounds__(256) flash_merge_kernel(FlashParams p, int rt) {
-  const int tid = threadIdx.x;
-  const int blocks_per_tile = rt / 8;
-  const int tile_id = blockIdx.x / blocks_per_tile;
-  const int rl = (blockIdx.x % blocks_per_tile) * 8 + tid / 32;
-  const int d4 = tid % 32;
+  __shared__ float red[32][HD + 4];
+  __shared__ float wmax[4], wsum[4];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int kv_dim = p.n_kv * HD;
+  if (p.commit_k != nullptr && (int)blockIdx.x < p.S) {
+    const int t = blockIdx.x;
+    const size_t slot = (size_t)((p.start_pos + t) % p.max_seq);
+    for (int e = 4 * tid; e < kv_dim; e += 4 * 256) {
+      *reinterpret_cast<uint2 *>(p.commit_k + slot * kv_dim + e) =
+          *reinterpret_cast<const uint2 *>(p.kstage + (size_t)t * kv_dim + e);
+      *reinterpret_cast<uint2 *>(p.commit_v + slot * kv_dim + e) =
+          *reinterpret_cast<const uint2 *>(p.vstage + (size_t)t * kv_dim + e);
+    }
+  }
+  if ((int)blockIdx.x >= p.n_kv * p.n_rtiles * rt) return;  // commit-only workgroup
+  const int tile_id = blockIdx.x / rt, rl = blockIdx.x % rt;
   const int kvh = tile_id / p.n_rtiles, rtile = tile_id % p.n_rtiles;
   const int row = rtile * rt + rl;
   const int t = row >> 2, g = row & 3;
-  if (t >= p.S) return;
-  const int dim_model = p.n_kv * 4 * HD;
-  float M = -INFINITY;
-  for (int sp = 0; sp < p.nsplit; ++sp)
-    M = fmaxf(M, p.part_ml[(((size_t)tile_id * p.nsplit + sp) * rt + rl) * 2]);
-  float Ls = 0.f;
-  f4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int sp = 0; sp < p.nsplit; ++sp) {
-    const size_t idx = ((size_t)tile_id * p.nsplit + sp) * rt + rl;
-    const float2 m_l = *reinterpret_cast<const float2 *>(p.part_ml + idx * 2);
-    const float e = m_l.x == -INFINITY ? 0.f : fast_exp2(m_l.x - M);
-    Ls = __builtin_fmaf(e, m_l.y, Ls);
-    acc += e * *reinterpret_cast<const f4 *>(p.part_o + idx * HD + 4 * d4);
+  if (t >= p.S) return;  // whole workgroup
+  const int sg = tid >> 3, d16 = tid & 7;
+  const size_t base = (size_t)tile_id * p.nsplit * rt + rl;  // + sp * rt
+  float m[kMergeSplitsPerThread], l[kMergeSplitsPerThread];
+  f4 o[kMergeSplitsPerThread][4];
+#pragma unroll
+  for (int k = 0; k < kMergeSplitsPerThread; ++k) {
+    const int sp = sg + 32 * k;
+    m[k] = -INFINITY;
+    l[k] = 0.f;
+    if (sp < p.nsplit) {
+      const size_t idx = base + (size_t)sp * rt;
+      const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + idx * 2);
+      m[k] = ml.x;
+      l[k] = ml.y;
+      const f4 *src = reinterpret_cast<const f4 *>(p.part_o + idx * HD + 16 * d16);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[k][q] = src[q];
+    }
   }
-  *reinterpret_cast<f4 *>(p.out + (size_t)t * dim_model + (size_t)(kvh * 4 + g) * HD + 4 * d4) =
-      acc * (1.0f / Ls);
+  float M = m[0];
+#pragma unroll
+  for (int k = 1; k < kMergeSplitsPerThread; ++k) M = fmaxf(M, m[k]);
+  M = wave_max(M);
+  if (lane == 0) wmax[wv] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float Mu = M == -INFINITY ? 0.f : M;
+  f4 acc[4] = {};
+  float ls = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMergeSplitsPerThread; ++k) {
+    if (sg + 32 * k < p.nsplit) {
+      const float e = m[k] == -INFINITY ? 0.f : fast_exp2(m[k] - Mu);
+      ls = __builtin_fmaf(e, l[k], ls);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] += e * o[k][q];
+    }
+  }
+  // every split's l is held by the 8 threads of its group: count it once
+  ls = wave_sum(d16 == 0 ? ls : 0.f);
+  if (lane == 0) wsum[wv] = ls;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) *reinterpret_cast<f4 *>(&red[sg][16 * d16 + 4 * q]) = acc[q];
+  __syncthreads();
+  if (tid < HD) {
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) sum += red[k][tid];
+    const float Ls = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    p.out[(size_t)t * (kv_dim * 4) + (size_t)(kvh * 4 + g) * HD + tid] = sum / Ls;
+  }
 }
 
 template <int NB>
@@ -921,6 +974,7 @@ void flash_plan(int S, int n_kv, int G, int start_pos, int max_seq, int target_w
   long want = (long)target_wgs / ((long)n_kv * ntiles);
   if (want < 1) want = 1;
   long max_split = maxkeys / (4L * kWaves * kKT);
+  if (max_split > kMergeSplitsPerThread * 32) max_split = kMergeSplitsPerThread * 32;
   if (want > max_split) want = max_split > 0 ? max_split : 1;
   long sk = (maxkeys + want - 1) / want;
   sk = ((sk + kKT - 1) / kKT) * kKT;
@@ -940,9 +994,12 @@ hipError_t launch_flash(const FlashParams &p, int G, hipStream_t s, hipEvent_t e
 
 hipError_t launch_flash_merge(const FlashParams &p, hipStream_t s) {
   const int rt = rows_per_tile(p.S);
-  if (p.nsplit > 1)
-    hipLaunchKernelGGL(flash_merge_kernel, dim3(p.n_kv * p.n_rtiles * (rt / 8)), dim3(256), 0, s,
-                       p, rt);
+  if (p.nsplit > kMergeSplitsPerThread * 32) return hipErrorInvalidValue;
+  if (p.nsplit > 1) {
+    // one workgroup per row; with a commit, at least S of them
+    const int wgs = max(p.n_kv * p.n_rtiles * rt, p.commit_k != nullptr ? p.S : 0);
+    hipLaunchKernelGGL(flash_merge_kernel, dim3(wgs), dim3(256), 0, s, p, rt);
+  }
   return hipGetLastError();
 }
 

@@ -50,6 +50,8 @@ struct FlashParams {
   float *out;              // [S][n_heads*128]
   float *part_o;           // split-K partials (nsplit > 1)
   float *part_ml;
+  _Float16 *commit_k;      // nsplit > 1 with staged drafts: the merge kernel copies
+  _Float16 *commit_v;      // the staged rows into these ring layers (else null)
   int S, n_kv, max_seq, start_pos;
   int n_rtiles;            // row tiles per kv head
   int nsplit;              // key splits per row tile
