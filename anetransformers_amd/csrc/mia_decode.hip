@@ -8,7 +8,10 @@
 // wave per kv head.  The waves of a workgroup walk the same ring slots, so
 // each slot's full K and V rows (8 heads x 256 B, contiguous) are read
 // together: streaming one head's 256 B pieces per workgroup instead leaves
-// some heads' pieces consistently slower to fetch than others.
+// some heads' pieces consistently slower to fetch than others.  Chunk c is
+// the 16-key tiles c, c + nchunk, c + 2 nchunk, ... of the window: spread
+// over the whole ring rather than one contiguous block, every workgroup
+// draws on all memory channels alike, and the workgroups end closer together.
 //
 // Each wave is an independent pipeline over the 16-key tiles of its chunk,
 // held in a ring of register buffers so that the next tiles' loads are in
@@ -83,10 +86,10 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   const int ce = FUSED ? p.L - 1 : p.L;
   const int n_tiles = (ce + kTile - 1) / kTile;
   const bool has_new = FUSED && chunk == p.nchunk - 1;
-  // Tiles of this wave: chunk `chunk` of an even split of all tiles.
-  int s_next = (int)((long)chunk * n_tiles / p.nchunk);
-  const int s_end = active ? (int)((long)(chunk + 1) * n_tiles / p.nchunk) : s_next;
-  auto next_tile = [&]() -> int { return s_next < s_end ? s_next++ : -1; };
+  // Tiles of this wave: chunk, chunk + nchunk, chunk + 2 nchunk, ...
+  int s_next = 0;
+  const int s_end = active && chunk < n_tiles ? (n_tiles - 1 - chunk) / p.nchunk + 1 : 0;
+  auto next_tile = [&]() -> int { return s_next < s_end ? chunk + p.nchunk * s_next++ : -1; };
 
   const _Float16 *kbase = p.kc + (size_t)kvh_c * HD;
   const _Float16 *vbase = p.vc + (size_t)kvh_c * HD;
