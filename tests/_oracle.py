@@ -65,6 +65,10 @@ _SIGS = {
         [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
     ),
     "ora_num_threads": (c_int, []),
+    "ora_quantize_q8_0": (None, [_P, _P, c_int]),
+    "ora_q4_0_q8_0_matvec": (None, [_P, _P, _P, c_int, c_int]),
+    "ora_q4_0_q8_0_matvec_qkv": (None, [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int]),
+    "ora_q4_0_q8_0_matvec_parallel": (None, [_P, _P, _P, c_int, c_int, c_int]),
 }
 
 _libs: dict = {}
@@ -221,3 +225,67 @@ def attention_batch_layers(Q, kcache, vcache, n_layers, n_heads, n_kv, hd, max_s
 
 def num_threads(fast: bool = True) -> int:
     return int(load(fast).ora_num_threads())
+
+
+# --- Q4_0 x Q8_0 projections (oracle/q4_oracle.h) ---------------------------
+
+Q8_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", (32,))])   # 36 bytes
+Q4_BLOCK_BYTES = 18
+
+
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    """fp32 [n] -> Q8_0 blocks [n/32] (structured array of (d, qs[32]))."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert x.size % 32 == 0
+    out = np.zeros(x.size // 32, dtype=Q8_DTYPE)
+    load().ora_quantize_q8_0(_p(x), out.ctypes.data, x.size)
+    return out
+
+
+def q4_0_q8_0_matvec(W: np.ndarray, xq: np.ndarray, out_dim: int, in_dim: int) -> np.ndarray:
+    """W: uint8 [out_dim, in_dim/32*18] Q4_0 rows; xq: Q8_0 blocks [in_dim/32]."""
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    assert W.size == out_dim * in_dim // 32 * Q4_BLOCK_BYTES and xq.dtype == Q8_DTYPE
+    y = np.empty(out_dim, dtype=np.float32)
+    load().ora_q4_0_q8_0_matvec(_p(W), xq.ctypes.data, _p(y), out_dim, in_dim)
+    return y
+
+
+def q4_0_q8_0_matvec_qkv(Wq, Wk, Wv, xq, dim, kv_dim, in_dim):
+    Wq, Wk, Wv = (np.ascontiguousarray(w, dtype=np.uint8) for w in (Wq, Wk, Wv))
+    yq = np.empty(dim, np.float32)
+    yk = np.empty(kv_dim, np.float32)
+    yv = np.empty(kv_dim, np.float32)
+    load().ora_q4_0_q8_0_matvec_qkv(_p(Wq), _p(Wk), _p(Wv), xq.ctypes.data, _p(yq), _p(yk),
+                                    _p(yv), dim, kv_dim, in_dim)
+    return yq, yk, yv
+
+
+def q4_0_q8_0_matvec_parallel(W, xq, out_dim, in_dim, threads=0, fast=True):
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    y = np.empty(out_dim, dtype=np.float32)
+    load(fast).ora_q4_0_q8_0_matvec_parallel(_p(W), xq.ctypes.data, _p(y), out_dim, in_dim,
+                                             threads)
+    return y
+
+
+def make_q4_0(g: np.random.Generator, out_dim: int, in_dim: int) -> np.ndarray:
+    """Random Q4_0 rows: N(0, 0.02)-sized fp16 scales, uniform nibbles."""
+    nb = in_dim // 32
+    W = np.empty((out_dim, nb, Q4_BLOCK_BYTES), np.uint8)
+    d = (np.abs(g.standard_normal((out_dim, nb))) * 0.02 + 1e-3).astype(np.float16)
+    W[:, :, 0:2] = d.view(np.uint8).reshape(out_dim, nb, 2)
+    W[:, :, 2:] = g.integers(0, 256, (out_dim, nb, 16), dtype=np.uint8)
+    return W.reshape(out_dim, nb * Q4_BLOCK_BYTES)
+
+
+def dequant_q4_0(W: np.ndarray, out_dim: int, in_dim: int) -> np.ndarray:
+    """float64 weights [out_dim, in_dim] from Q4_0 rows (dequant.h:600-611 layout)."""
+    nb = in_dim // 32
+    B = np.ascontiguousarray(W, np.uint8).reshape(out_dim, nb, Q4_BLOCK_BYTES)
+    d = B[:, :, 0:2].copy().view(np.float16).reshape(out_dim, nb).astype(np.float64)
+    q = B[:, :, 2:].astype(np.int64)
+    lo = (q & 0x0F) - 8
+    hi = (q >> 4) - 8
+    vals = np.concatenate([lo, hi], axis=2)          # weights 0..15, then 16..31
+    return (vals * d[:, :, None]).reshape(out_dim, in_dim)
