@@ -101,6 +101,12 @@ _SIGS = {
         c_int,
         [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, _P],
     ),
+    "mia_quantize_q8_0": (c_int, [_P, _P, c_int, _P]),
+    "mia_q4_0_matvec": (c_int, [_P, _P, _P, c_int, c_int, _P]),
+    "mia_q4_0_matvec_qkv": (
+        c_int,
+        [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, _P],
+    ),
     # drop-in (reference signatures)
     "mia_dropin_set_abort": (None, [c_int]),
     "mia_dropin_status": (c_int, []),
@@ -122,6 +128,12 @@ _SIGS = {
     "mia_dropin_verify_step": (
         None,
         [POINTER(KVCache), c_int, _P, _P, _P, c_int, c_int, _P, c_int, c_int, _P],
+    ),
+    "mia_dropin_quantize_q8_0": (None, [_P, _P, c_int]),
+    "mia_dropin_q4_matvec_sdot_parallel": (None, [_P, ctypes.c_uint32, _P, _P, c_int, c_int]),
+    "mia_dropin_q4_matvec_sdot_parallel_fused_qkv": (
+        None,
+        [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int],
     ),
 }
 

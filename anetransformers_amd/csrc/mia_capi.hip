@@ -28,11 +28,11 @@ struct DevCtx {
   size_t scratch_bytes = 0;
   void *work = nullptr;  // fp16 draft staging for mia_attention_step
   size_t work_bytes = 0;
-  // Opt-in kernel timing: an event pair around the main attention kernel of
-  // each call (kind 0 = decode kernel, 1 = flash kernel).
+  // Opt-in kernel timing: an event pair around the main kernel of each call
+  // (kind 0 = decode kernel, 1 = flash kernel, 2 = Q4_0 matvec kernel).
   bool prof_on = false;
-  std::vector<hipEvent_t> prof_ev[2];
-  size_t prof_n[2] = {0, 0};
+  std::vector<hipEvent_t> prof_ev[3];
+  size_t prof_n[3] = {0, 0, 0};
 };
 
 DevCtx g_ctx[kMaxDevices];
@@ -269,13 +269,13 @@ int mia_init(int device) {
 int mia_profile_begin(void) {
   DevCtx *c;
   if (int rc = current_ctx(&c)) return rc;
-  c->prof_n[0] = c->prof_n[1] = 0;
+  c->prof_n[0] = c->prof_n[1] = c->prof_n[2] = 0;
   c->prof_on = true;
   return MIA_OK;
 }
 
 int mia_profile_end(int kind, int *count, double *total_ms) {
-  if (kind < 0 || kind > 1 || !count || !total_ms) return set_err(MIA_ERR_INVALID, "bad profile query");
+  if (kind < 0 || kind > 2 || !count || !total_ms) return set_err(MIA_ERR_INVALID, "bad profile query");
   DevCtx *c;
   if (int rc = current_ctx(&c)) return rc;
   c->prof_on = false;
@@ -507,6 +507,58 @@ int mia_attention_step(const float *Q, const float *K, const float *V, const flo
   return flash_impl(c, Q, cs, reinterpret_cast<uint16_t *>(kst),
                     reinterpret_cast<uint16_t *>(vst), k_layer, v_layer, out, n_kv_heads, max_seq,
                     start_pos, S, s, true);
+}
+
+int mia_quantize_q8_0(const float *x, void *out_q8, int n, void *stream) {
+  if (!x || !out_q8) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (n <= 0 || n % 32) return set_err(MIA_ERR_INVALID, "n %d must be a positive multiple of 32", n);
+  if ((uintptr_t)x & 15) return set_err(MIA_ERR_INVALID, "x must be 16-byte aligned");
+  if ((uintptr_t)out_q8 & 3) return set_err(MIA_ERR_INVALID, "out_q8 must be 4-byte aligned");
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  HIP_TRY(mia::launch_quantize_q8_0(x, reinterpret_cast<uint8_t *>(out_q8), n / 32,
+                                    pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_q4_0_matvec(const void *W, const void *x_q8, float *y, int out_dim, int in_dim,
+                    void *stream) {
+  return mia_q4_0_matvec_qkv(W, nullptr, nullptr, x_q8, y, nullptr, nullptr, out_dim, 0, in_dim,
+                             stream);
+}
+
+int mia_q4_0_matvec_qkv(const void *Wq, const void *Wk, const void *Wv, const void *x_q8,
+                        float *yq, float *yk, float *yv, int dim, int kv_dim, int in_dim,
+                        void *stream) {
+  if (!Wq || !x_q8 || !yq || (kv_dim && (!Wk || !Wv || !yk || !yv)))
+    return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (dim <= 0 || kv_dim < 0 || in_dim <= 0 || in_dim % 32)
+    return set_err(MIA_ERR_INVALID, "bad sizes (dim=%d kv_dim=%d in_dim=%d)", dim, kv_dim, in_dim);
+  if (in_dim % 64)
+    return set_err(MIA_ERR_UNSUPPORTED, "in_dim %d: the kernel needs an even number of blocks per row",
+                   in_dim);
+  if ((long)dim + 2L * kv_dim > (long)INT_MAX) return set_err(MIA_ERR_INVALID, "too many rows");
+  const uintptr_t bits = (uintptr_t)Wq | (uintptr_t)Wk | (uintptr_t)Wv | (uintptr_t)x_q8 |
+                         (uintptr_t)yq | (uintptr_t)yk | (uintptr_t)yv;
+  if (bits & 3) return set_err(MIA_ERR_INVALID, "weights, x_q8 and y must be 4-byte aligned");
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  mia::Q4MatvecParams p{};
+  p.w0 = reinterpret_cast<const uint8_t *>(Wq);
+  p.w1 = reinterpret_cast<const uint8_t *>(Wk);
+  p.w2 = reinterpret_cast<const uint8_t *>(Wv);
+  p.y0 = yq;
+  p.y1 = yk;
+  p.y2 = yv;
+  p.x = reinterpret_cast<const uint8_t *>(x_q8);
+  p.rows0 = dim;
+  p.rows01 = dim + kv_dim;
+  p.total_rows = dim + 2 * kv_dim;
+  p.bpr = in_dim / 32;
+  hipEvent_t ev0, ev1;
+  if (int rc = prof_pair(c, 2, &ev0, &ev1)) return rc;
+  HIP_TRY(mia::launch_q4_matvec(p, pick_stream(c, stream), ev0, ev1));
+  return MIA_OK;
 }
 
 }  // extern "C"

@@ -246,3 +246,58 @@ void mia_dropin_verify_step(KVCache *kv, int layer, const float *Q, const float 
     step_common("verify_step", kv, layer, Q, K, V, start_pos, S, theta_inv, n_heads, n_kv_heads,
                 out);
 }
+
+void mia_dropin_quantize_q8_0(const float *x, mia_block_q8_0 *out, int n) {
+    g_status = 0;
+    if (n <= 0 || n % 32) {
+        fail(MIA_ERR_INVALID, "quantize_f32_to_q8_0 (n not a positive multiple of 32)");
+        return;
+    }
+    size_t xb = (size_t)n * sizeof(float);
+    size_t qb = (size_t)(n / 32) * sizeof(mia_block_q8_0);
+    TRY("quantize_f32_to_q8_0", dbuf(align256(xb) + align256(qb)));
+    float *dx = (float *)g_dbuf;
+    void *dq = g_dbuf + align256(xb);
+    TRY("quantize_f32_to_q8_0", mia_memcpy_h2d(dx, x, xb));
+    TRY("quantize_f32_to_q8_0", mia_quantize_q8_0(dx, dq, n, NULL));
+    TRY("quantize_f32_to_q8_0", mia_stream_sync(NULL));
+    TRY("quantize_f32_to_q8_0", mia_memcpy_d2h(out, dq, qb));
+}
+
+void mia_dropin_q4_matvec_sdot_parallel_fused_qkv(const void *Wq, const void *Wk, const void *Wv,
+                                                  const mia_block_q8_0 *x_q8, float *yq,
+                                                  float *yk, float *yv, int dim, int kv_dim,
+                                                  int in_dim) {
+    const char *what = "q4_matvec_sdot_parallel";
+    g_status = 0;
+    if (dim <= 0 || kv_dim < 0 || in_dim <= 0 || in_dim % 32) {
+        fail(MIA_ERR_INVALID, "q4_matvec (bad sizes)");
+        return;
+    }
+    size_t xb = (size_t)(in_dim / 32) * sizeof(mia_block_q8_0);
+    size_t qb = (size_t)dim * sizeof(float), kb = (size_t)kv_dim * sizeof(float);
+    TRY(what, dbuf(align256(xb) + align256(qb) + 2 * align256(kb)));
+    void *dx = g_dbuf;
+    float *dyq = (float *)(g_dbuf + align256(xb));
+    float *dyk = kv_dim ? (float *)(g_dbuf + align256(xb) + align256(qb)) : NULL;
+    float *dyv = kv_dim ? (float *)(g_dbuf + align256(xb) + align256(qb) + align256(kb)) : NULL;
+    TRY(what, mia_memcpy_h2d(dx, x_q8, xb));
+    TRY(what, mia_q4_0_matvec_qkv(Wq, Wk, Wv, dx, dyq, dyk, dyv, dim, kv_dim, in_dim, NULL));
+    TRY(what, mia_stream_sync(NULL));
+    TRY(what, mia_memcpy_d2h(yq, dyq, qb));
+    if (kv_dim) {
+        TRY(what, mia_memcpy_d2h(yk, dyk, kb));
+        TRY(what, mia_memcpy_d2h(yv, dyv, kb));
+    }
+}
+
+void mia_dropin_q4_matvec_sdot_parallel(const void *W, uint32_t type, const mia_block_q8_0 *x_q8,
+                                        float *y, int out_dim, int in_dim) {
+    g_status = 0;
+    if (type != MIA_GGML_TYPE_Q4_0) {
+        fail(MIA_ERR_UNSUPPORTED, "q4_matvec_sdot_parallel (only Q4_0 weights)");
+        return;
+    }
+    mia_dropin_q4_matvec_sdot_parallel_fused_qkv(W, NULL, NULL, x_q8, y, NULL, NULL, out_dim, 0,
+                                                 in_dim);
+}

@@ -82,6 +82,23 @@ hipError_t launch_kv_write(_Float16 *kc, _Float16 *vc, const float *K, const flo
 hipError_t launch_commit(_Float16 *kc, _Float16 *vc, const _Float16 *kst, const _Float16 *vst,
                          int S, int start_pos, int max_seq, int kv_dim, hipStream_t s);
 hipError_t launch_fill_normal(_Float16 *dst, size_t n, uint64_t seed, hipStream_t s);
+
+// W4A8 projections (mistral/dequant.h).  x [nblocks*32] fp32, 16-byte aligned
+// -> nblocks Q8_0 blocks of 36 bytes.
+hipError_t launch_quantize_q8_0(const float *x, uint8_t *out, int nblocks, hipStream_t s);
+// y = W . x for up to three Q4_0 matrices stacked as virtual rows (w0's rows,
+// then w1's, then w2's); bpr = blocks per row, even; pointers 4-byte aligned.
+struct Q4MatvecParams {
+  const uint8_t *w0, *w1, *w2;
+  float *y0, *y1, *y2;
+  const uint8_t *x;  // Q8_0 blocks [bpr]
+  int rows0;         // rows of w0
+  int rows01;        // rows of w0 + w1
+  int total_rows;    // rows of w0 + w1 + w2
+  int bpr;
+};
+hipError_t launch_q4_matvec(const Q4MatvecParams &p, hipStream_t s, hipEvent_t ev0,
+                            hipEvent_t ev1);
 hipError_t launch_scale_rows(_Float16 *base, long n_rows, int row_elems, int every, int offset,
                              float factor, hipStream_t s);
 

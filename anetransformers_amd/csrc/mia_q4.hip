@@ -1,0 +1,178 @@
+// mia_q4.hip -- the W4A8 projections either side of the attention step:
+// fp32 -> Q8_0 quantisation of an activation vector (mistral/dequant.h:545-612)
+// and the Q4_0 x Q8_0 matvec (mistral/dequant.h:1022-1137), for one matrix or
+// for the Q, K and V matrices in one launch (mistral_model.h:676-745).
+//
+// Block formats (mistral/dequant.h:17-31, 535-541):
+//   Q4_0  18 B per 32 weights: fp16 scale, then 16 bytes; byte j holds weight j
+//         in its low nibble and weight j+16 in its high nibble, each stored +8.
+//   Q8_0  36 B per 32 values: fp32 scale, then 32 int8.
+//
+// Matvec layout: a row is bpr * 18 bytes with bpr even, so every pair of
+// blocks is 36 bytes at a 4-byte aligned offset.  Lane l of a wave takes block
+// pairs l, l+64, ... of each of the R rows the wave owns, loads all R rows and
+// the matching 72 bytes of x before using any of them, and forms each block's
+// integer dot with v_dot4 on the raw nibbles (0..15 are valid int8) minus
+// 8 * sum(x block): the same integer as sum((nibble - 8) * x).  Each block term
+// is (wd * xd) * (float)isum, rounded as in the reference; the terms of a row
+// are then summed per lane and across the wave (the reference sums them in
+// block order, so rows agree to fp32 reassociation, not bit for bit).
+#include "mia_device.h"
+#include "mia_kernels.h"
+
+namespace mia {
+namespace {
+
+constexpr int kQ4Threads = 256;
+constexpr int kQ4Waves = kQ4Threads / 64;
+constexpr unsigned kNib = 0x0F0F0F0Fu;
+
+__device__ __forceinline__ unsigned ld32(const uint8_t *p) {
+  return *reinterpret_cast<const unsigned *>(p);
+}
+
+__device__ __forceinline__ float f16_bits(unsigned h) {
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xFFFFu));
+}
+
+__device__ __forceinline__ int dot4(unsigned a, unsigned b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// 8 lanes per 32-value block, 4 values per lane.  amax is order-free (max of
+// absolute values), d = amax / 127 and id = 1 / d are IEEE-rounded divides,
+// q = round-half-even(x * id) saturated to int8, as vcvtnq_s32_f32 + vqmovn.
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x,
+                                                            uint8_t *__restrict__ out,
+                                                            int nblocks) {
+  const int gid = blockIdx.x * 256 + threadIdx.x;
+  const int blk = gid >> 3, sub = gid & 7;
+  if (blk >= nblocks) return;  // whole 8-lane groups leave together
+  const f4 v = *reinterpret_cast<const f4 *>(x + (size_t)blk * 32 + sub * 4);
+  float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  a = fmaxf(a, __shfl_xor(a, 1));
+  a = fmaxf(a, __shfl_xor(a, 2));
+  a = fmaxf(a, __shfl_xor(a, 4));
+  const float d = a / 127.0f;
+  unsigned packed = 0;
+  if (a != 0.0f) {
+    const float id = 1.0f / d;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float r = __builtin_rintf(v[i] * id);
+      r = fminf(fmaxf(r, -128.0f), 127.0f);
+      packed |= ((unsigned)(int)r & 0xFFu) << (8 * i);
+    }
+  }
+  uint8_t *ob = out + (size_t)blk * 36;
+  if (sub == 0) *reinterpret_cast<float *>(ob) = d;
+  *reinterpret_cast<unsigned *>(ob + 4 + 4 * sub) = packed;
+}
+
+template <int R>
+__global__ __launch_bounds__(kQ4Threads) void q4_matvec_kernel(Q4MatvecParams p) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = (blockIdx.x * kQ4Waves + wave) * R;
+  const size_t row_bytes = (size_t)p.bpr * 18;
+
+  // Virtual rows 0..rows0-1 are w0's, then w1's, then w2's.  Rows past the
+  // end load the last row (in bounds) and store nothing.
+  const uint8_t *wrow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int g = min(row0 + r, p.total_rows - 1);
+    const uint8_t *base = g < p.rows0 ? p.w0 : (g < p.rows01 ? p.w1 : p.w2);
+    const int lr = g < p.rows0 ? g : (g < p.rows01 ? g - p.rows0 : g - p.rows01);
+    wrow[r] = base + (size_t)lr * row_bytes;
+  }
+
+  const int npairs = p.bpr >> 1;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+
+  for (int p0 = 0; p0 < npairs; p0 += 64) {
+    const int pr = p0 + lane;
+    const bool on = pr < npairs;
+    const int pc = on ? pr : npairs - 1;
+    unsigned wv[R][9];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint8_t *wp = wrow[r] + (size_t)pc * 36;
+#pragma unroll
+      for (int j = 0; j < 9; ++j) wv[r][j] = ld32(wp + 4 * j);
+    }
+    unsigned xv[18];
+    const uint8_t *xp = p.x + (size_t)pc * 72;
+#pragma unroll
+    for (int j = 0; j < 18; ++j) xv[j] = ld32(xp + 4 * j);
+
+    // x block A: d = xv[0], qs = xv[1..8]; block B: d = xv[9], qs = xv[10..17]
+    int sxa = 0, sxb = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      sxa = dot4(xv[1 + i], 0x01010101u, sxa);
+      sxb = dot4(xv[10 + i], 0x01010101u, sxb);
+    }
+    const float xda = __builtin_bit_cast(float, xv[0]);
+    const float xdb = __builtin_bit_cast(float, xv[9]);
+
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const unsigned *w = wv[r];
+      // weight block A: scale in bytes 0-1, nibbles in bytes 2-17
+      int ia = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const unsigned q = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+        ia = dot4(q & kNib, xv[1 + i], ia);
+        ia = dot4((q >> 4) & kNib, xv[5 + i], ia);
+      }
+      ia -= 8 * sxa;
+      // weight block B: scale in bytes 18-19, nibbles in bytes 20-35
+      int ib = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const unsigned q = w[5 + i];
+        ib = dot4(q & kNib, xv[10 + i], ib);
+        ib = dot4((q >> 4) & kNib, xv[14 + i], ib);
+      }
+      ib -= 8 * sxb;
+      const float ta = (f16_bits(w[0]) * xda) * (float)ia;
+      const float tb = (f16_bits(w[4] >> 16) * xdb) * (float)ib;
+      acc[r] += on ? ta + tb : 0.0f;
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float s = wave_sum(acc[r]);
+    const int g = row0 + r;
+    if (lane == 0 && g < p.total_rows) {
+      float *y = g < p.rows0 ? p.y0 + g : (g < p.rows01 ? p.y1 + (g - p.rows0) : p.y2 + (g - p.rows01));
+      *y = s;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_quantize_q8_0(const float *x, uint8_t *out, int nblocks, hipStream_t s) {
+  const int threads = nblocks * 8;
+  hipLaunchKernelGGL(quantize_q8_0_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, x, out,
+                     nblocks);
+  return hipGetLastError();
+}
+
+hipError_t launch_q4_matvec(const Q4MatvecParams &p, hipStream_t s, hipEvent_t ev0,
+                            hipEvent_t ev1) {
+  constexpr int R = 2;
+  const int rows_per_wg = kQ4Waves * R;
+  const dim3 grid((p.total_rows + rows_per_wg - 1) / rows_per_wg);
+  hipExtLaunchKernelGGL(q4_matvec_kernel<R>, grid, dim3(kQ4Threads), 0, s, ev0, ev1, 0, p);
+  return hipGetLastError();
+}
+
+}  // namespace mia

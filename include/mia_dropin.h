@@ -24,6 +24,7 @@
 #define MIA_DROPIN_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #include "miattn.h"
 
@@ -58,6 +59,15 @@ typedef struct {
     float rms_eps;
     int sliding_window;
 } MistralConfig;
+
+/* mistral/dequant.h:537-541: 36 bytes, fp32 scale then 32 int8. */
+typedef struct {
+    float d;
+    int8_t qs[32];
+} mia_block_q8_0;
+
+/* mistral/gguf_loader.h:33 */
+#define MIA_GGML_TYPE_Q4_0 2
 
 void mia_dropin_set_abort(int abort_on_error);
 int mia_dropin_status(void); /* status of the last drop-in call on this thread */
@@ -95,6 +105,20 @@ void mia_dropin_decode_step(KVCache *kv, int layer, const float *q, const float 
 void mia_dropin_verify_step(KVCache *kv, int layer, const float *Q, const float *K, const float *V,
                             int start_pos, int S, const float *theta_inv, int n_heads,
                             int n_kv_heads, float *out);
+
+/* W4A8 projections.  Weights W* are device memory holding the Q4_0 blocks as
+ * GGUF stores them (the Metal backend re-homes the mmap'd weight file the same
+ * way, mistral/metal_matvec.h:185-192, 314); x, x_q8 and y are host buffers. */
+/* mistral/dequant.h:545-612 */
+void mia_dropin_quantize_q8_0(const float *x, mia_block_q8_0 *out, int n);
+/* mistral/mistral_model.h:649-668 for type Q4_0 (other types: MIA_ERR_UNSUPPORTED) */
+void mia_dropin_q4_matvec_sdot_parallel(const void *W, uint32_t type, const mia_block_q8_0 *x_q8,
+                                        float *y, int out_dim, int in_dim);
+/* mistral/mistral_model.h:676-745 */
+void mia_dropin_q4_matvec_sdot_parallel_fused_qkv(const void *Wq, const void *Wk, const void *Wv,
+                                                  const mia_block_q8_0 *x_q8, float *yq,
+                                                  float *yk, float *yv, int dim, int kv_dim,
+                                                  int in_dim);
 
 #ifndef MIA_DROPIN_NO_REFERENCE_NAMES
 /* Reference names (mistral/kv_cache.h, mistral_model.h, mistral_ane_prefill.h). */
@@ -146,6 +170,21 @@ static inline void attention_batch(const float *Q, float *attn_out, const KVCach
                                    int start_pos, const MistralConfig *c, int S,
                                    float *att_scratch) {
     mia_dropin_attention_batch(Q, attn_out, kv, layer, start_pos, c, S, att_scratch);
+}
+typedef mia_block_q8_0 block_q8_0;
+static inline void quantize_f32_to_q8_0(const float *x, block_q8_0 *out, int n) {
+    mia_dropin_quantize_q8_0(x, out, n);
+}
+static inline void q4_matvec_sdot_parallel(const void *W, uint32_t type, const block_q8_0 *x_q8,
+                                           float *y, int out_dim, int in_dim) {
+    mia_dropin_q4_matvec_sdot_parallel(W, type, x_q8, y, out_dim, in_dim);
+}
+static inline void q4_matvec_sdot_parallel_fused_qkv(const void *Wq, const void *Wk,
+                                                     const void *Wv, const block_q8_0 *x_q8,
+                                                     float *yq, float *yk, float *yv, int dim,
+                                                     int kv_dim, int in_dim) {
+    mia_dropin_q4_matvec_sdot_parallel_fused_qkv(Wq, Wk, Wv, x_q8, yq, yk, yv, dim, kv_dim,
+                                                 in_dim);
 }
 #endif /* MIA_DROPIN_NO_REFERENCE_NAMES */
 

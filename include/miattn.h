@@ -63,7 +63,8 @@ int mia_event_elapsed_ms(float *ms, void *start, void *stop);
  * every attention call is launched with a HIP event pair that the dispatch
  * stamps at its start and end (kind 0: the S=1 decode kernel of
  * mia_gqa_attention / mia_decode_step / mia_attention_step with S=1; kind 1:
- * the S>1 flash kernel); merge and RoPE kernels are not timed.
+ * the S>1 flash kernel; kind 2: the Q4_0 matvec kernel of mia_q4_0_matvec /
+ * mia_q4_0_matvec_qkv); merge, quantize and RoPE kernels are not timed.
  * mia_profile_end stops recording, synchronises and returns the number of
  * timed launches of that kind and their summed duration. */
 int mia_profile_begin(void);
@@ -125,6 +126,36 @@ int mia_attention_batch(const float *Q, float *out, const uint16_t *k_layer,
 int mia_attention_step(const float *Q, const float *K, const float *V, const float *theta_inv,
                        uint16_t *k_layer, uint16_t *v_layer, float *out, int n_heads,
                        int n_kv_heads, int hd, int max_seq, int start_pos, int S, void *stream);
+
+/* ---- W4A8 projections either side of the attention step ------------------ */
+/* Block formats of mistral/dequant.h: Q4_0 = 18 bytes per 32 weights (fp16
+ * scale, 16 bytes of nibbles: byte j low = weight j, high = weight j+16, each
+ * stored + 8; dequant.h:17-31); Q8_0 = 36 bytes per 32 values (fp32 scale,
+ * 32 int8; dequant.h:535-541).  A Q4_0 matrix [out_dim][in_dim] is out_dim
+ * rows of in_dim/32 blocks, as GGUF stores it. */
+
+/* x [n] fp32 dev (16-byte aligned, n a multiple of 32) -> n/32 Q8_0 blocks
+ * (4-byte aligned).  Replaces quantize_f32_to_q8_0 (mistral/dequant.h:
+ * 545-612): d = amax/127, q = round-half-even(x * (1/d)) saturated, d = 0 and q = 0
+ * for an all-zero block; bit-identical to it. */
+int mia_quantize_q8_0(const float *x, void *out_q8, int n, void *stream);
+
+/* y [out_dim] fp32 = W (Q4_0) . x_q8.  Replaces q4_matvec_sdot_parallel for
+ * Q4_0 weights (mistral/mistral_model.h:649-668 -> q4_0_q8_0_matvec_sdot_parallel,
+ * mistral/dequant.h:1022-1137), used for Wo at mistral_model.h:866-867.
+ * in_dim must be a multiple of 64 (an even number of blocks per row, as every
+ * Mistral-7B projection has); W, x_q8, y 4-byte aligned device memory.  Block
+ * terms are rounded as the reference's; their sum is reassociated. */
+int mia_q4_0_matvec(const void *W, const void *x_q8, float *y, int out_dim, int in_dim,
+                    void *stream);
+
+/* The Q, K and V projections against one quantised input in one launch.
+ * Replaces q4_matvec_sdot_parallel_fused_qkv (mistral/mistral_model.h:676-745,
+ * called at :840-842): yq [dim] = Wq . x, yk [kv_dim] = Wk . x,
+ * yv [kv_dim] = Wv . x, each row as in mia_q4_0_matvec. */
+int mia_q4_0_matvec_qkv(const void *Wq, const void *Wk, const void *Wv, const void *x_q8,
+                        float *yq, float *yk, float *yv, int dim, int kv_dim, int in_dim,
+                        void *stream);
 
 #ifdef __cplusplus
 }

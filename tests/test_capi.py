@@ -67,6 +67,15 @@ void prefill(KVCache *kv, float *Q, float *K, float *V, float *out, const float 
     kv_write_batch(kv, 0, start, K, V, kv->kv_dim, S);
     attention_batch(Q, out, kv, 0, start, c, S, 0);
 }
+/* the projections either side, mistral/mistral_model.h:833-842, 866-867 */
+void projections(const void *wq, const void *wk, const void *wv, const void *wo, float *xb,
+                 float *xb2, block_q8_0 *xb_q8, float *q, float *k, float *v, float *out) {
+    quantize_f32_to_q8_0(xb, xb_q8, 4096);
+    q4_matvec_sdot_parallel_fused_qkv(wq, wk, wv, xb_q8, q, k, v, 4096, 1024, 4096);
+    quantize_f32_to_q8_0(xb2, xb_q8, 4096);
+    q4_matvec_sdot_parallel(wo, 2, xb_q8, out, 4096, 4096);
+}
+_Static_assert(sizeof(block_q8_0) == 36, "block_q8_0 size");
 int main(void) { KVCache kv = kv_alloc(1, 8, 128, 16); kv_free(&kv); return kv_k_at(&kv, 0, 0) != 0; }
 ''')
     exe = tmp_path / "use_dropin"
@@ -100,6 +109,26 @@ def test_argument_errors_without_device_work():
     assert rc == mia.MIA_ERR_INVALID and b"overflow" in lib.mia_last_error()
     rc = lib.mia_rope_f32(p, p, 1, 0, p, 32, 8, 96, None)
     assert rc == mia.MIA_ERR_UNSUPPORTED
+
+
+def test_q4_argument_errors_without_device_work():
+    lib = mia.load()
+    buf = np.zeros(64, np.float32)
+    p = buf.ctypes.data
+    rc = lib.mia_q4_0_matvec(p, p, p, 64, 96, None)           # 3 blocks per row (odd)
+    assert rc == mia.MIA_ERR_UNSUPPORTED and b"even" in lib.mia_last_error()
+    rc = lib.mia_q4_0_matvec(p, p, p, 64, 100, None)          # not a multiple of 32
+    assert rc == mia.MIA_ERR_INVALID
+    rc = lib.mia_q4_0_matvec(p, p, p, 0, 128, None)
+    assert rc == mia.MIA_ERR_INVALID
+    rc = lib.mia_q4_0_matvec(p + 2, p, p, 64, 128, None)      # misaligned weights
+    assert rc == mia.MIA_ERR_INVALID and b"aligned" in lib.mia_last_error()
+    rc = lib.mia_q4_0_matvec_qkv(p, None, p, p, p, p, p, 64, 16, 128, None)
+    assert rc == mia.MIA_ERR_INVALID
+    rc = lib.mia_quantize_q8_0(p, p, 48, None)
+    assert rc == mia.MIA_ERR_INVALID
+    rc = lib.mia_quantize_q8_0(p + 4, p, 64, None)             # x needs 16-byte alignment
+    assert rc == mia.MIA_ERR_INVALID
 
 
 def test_no_device_is_reported(monkeypatch):
