@@ -107,6 +107,11 @@ _SIGS = {
         c_int,
         [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, _P],
     ),
+    "mia_q4_0_matvec_f32": (c_int, [_P, _P, _P, c_int, c_int, _P]),
+    "mia_q4_0_matvec_qkv_f32": (
+        c_int,
+        [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, _P],
+    ),
     # drop-in (reference signatures)
     "mia_dropin_set_abort": (None, [c_int]),
     "mia_dropin_status": (c_int, []),

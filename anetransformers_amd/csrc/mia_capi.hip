@@ -224,6 +224,46 @@ int flash_impl(DevCtx *c, const float *Q, const float *rope_cs, const uint16_t *
   return MIA_OK;
 }
 
+// Q4_0 matvec over up to three stacked matrices; exactly one of x_q8 (Q8_0
+// blocks) and xf (fp32, quantised in-kernel) is set.
+int q4_impl(const void *Wq, const void *Wk, const void *Wv, const void *x_q8, const float *xf,
+            float *yq, float *yk, float *yv, int dim, int kv_dim, int in_dim, void *stream) {
+  if (!Wq || !(x_q8 || xf) || !yq || (kv_dim && (!Wk || !Wv || !yk || !yv)))
+    return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (dim <= 0 || kv_dim < 0 || in_dim <= 0 || in_dim % 32)
+    return set_err(MIA_ERR_INVALID, "bad sizes (dim=%d kv_dim=%d in_dim=%d)", dim, kv_dim, in_dim);
+  if (in_dim % 64)
+    return set_err(MIA_ERR_UNSUPPORTED, "in_dim %d: the kernel needs an even number of blocks per row",
+                   in_dim);
+  if (xf && in_dim > mia::kQ4MaxF32InDim)
+    return set_err(MIA_ERR_UNSUPPORTED, "in_dim %d above %d for fp32 input (quantize first)", in_dim,
+                   mia::kQ4MaxF32InDim);
+  if ((long)dim + 2L * kv_dim > (long)INT_MAX) return set_err(MIA_ERR_INVALID, "too many rows");
+  const uintptr_t bits = (uintptr_t)Wq | (uintptr_t)Wk | (uintptr_t)Wv | (uintptr_t)x_q8 |
+                         (uintptr_t)yq | (uintptr_t)yk | (uintptr_t)yv;
+  if (bits & 3) return set_err(MIA_ERR_INVALID, "weights, x_q8 and y must be 4-byte aligned");
+  if ((uintptr_t)xf & 15) return set_err(MIA_ERR_INVALID, "x must be 16-byte aligned");
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  mia::Q4MatvecParams p{};
+  p.w0 = reinterpret_cast<const uint8_t *>(Wq);
+  p.w1 = reinterpret_cast<const uint8_t *>(Wk);
+  p.w2 = reinterpret_cast<const uint8_t *>(Wv);
+  p.y0 = yq;
+  p.y1 = yk;
+  p.y2 = yv;
+  p.x = reinterpret_cast<const uint8_t *>(x_q8);
+  p.xf = xf;
+  p.rows0 = dim;
+  p.rows01 = dim + kv_dim;
+  p.total_rows = dim + 2 * kv_dim;
+  p.bpr = in_dim / 32;
+  hipEvent_t ev0, ev1;
+  if (int rc = prof_pair(c, 2, &ev0, &ev1)) return rc;
+  HIP_TRY(mia::launch_q4_matvec(p, pick_stream(c, stream), ev0, ev1));
+  return MIA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -523,42 +563,25 @@ int mia_quantize_q8_0(const float *x, void *out_q8, int n, void *stream) {
 
 int mia_q4_0_matvec(const void *W, const void *x_q8, float *y, int out_dim, int in_dim,
                     void *stream) {
-  return mia_q4_0_matvec_qkv(W, nullptr, nullptr, x_q8, y, nullptr, nullptr, out_dim, 0, in_dim,
-                             stream);
+  return q4_impl(W, nullptr, nullptr, x_q8, nullptr, y, nullptr, nullptr, out_dim, 0, in_dim,
+                 stream);
 }
 
 int mia_q4_0_matvec_qkv(const void *Wq, const void *Wk, const void *Wv, const void *x_q8,
                         float *yq, float *yk, float *yv, int dim, int kv_dim, int in_dim,
                         void *stream) {
-  if (!Wq || !x_q8 || !yq || (kv_dim && (!Wk || !Wv || !yk || !yv)))
-    return set_err(MIA_ERR_INVALID, "NULL pointer");
-  if (dim <= 0 || kv_dim < 0 || in_dim <= 0 || in_dim % 32)
-    return set_err(MIA_ERR_INVALID, "bad sizes (dim=%d kv_dim=%d in_dim=%d)", dim, kv_dim, in_dim);
-  if (in_dim % 64)
-    return set_err(MIA_ERR_UNSUPPORTED, "in_dim %d: the kernel needs an even number of blocks per row",
-                   in_dim);
-  if ((long)dim + 2L * kv_dim > (long)INT_MAX) return set_err(MIA_ERR_INVALID, "too many rows");
-  const uintptr_t bits = (uintptr_t)Wq | (uintptr_t)Wk | (uintptr_t)Wv | (uintptr_t)x_q8 |
-                         (uintptr_t)yq | (uintptr_t)yk | (uintptr_t)yv;
-  if (bits & 3) return set_err(MIA_ERR_INVALID, "weights, x_q8 and y must be 4-byte aligned");
-  DevCtx *c;
-  if (int rc = current_ctx(&c)) return rc;
-  mia::Q4MatvecParams p{};
-  p.w0 = reinterpret_cast<const uint8_t *>(Wq);
-  p.w1 = reinterpret_cast<const uint8_t *>(Wk);
-  p.w2 = reinterpret_cast<const uint8_t *>(Wv);
-  p.y0 = yq;
-  p.y1 = yk;
-  p.y2 = yv;
-  p.x = reinterpret_cast<const uint8_t *>(x_q8);
-  p.rows0 = dim;
-  p.rows01 = dim + kv_dim;
-  p.total_rows = dim + 2 * kv_dim;
-  p.bpr = in_dim / 32;
-  hipEvent_t ev0, ev1;
-  if (int rc = prof_pair(c, 2, &ev0, &ev1)) return rc;
-  HIP_TRY(mia::launch_q4_matvec(p, pick_stream(c, stream), ev0, ev1));
-  return MIA_OK;
+  return q4_impl(Wq, Wk, Wv, x_q8, nullptr, yq, yk, yv, dim, kv_dim, in_dim, stream);
+}
+
+int mia_q4_0_matvec_f32(const void *W, const float *x, float *y, int out_dim, int in_dim,
+                        void *stream) {
+  return q4_impl(W, nullptr, nullptr, nullptr, x, y, nullptr, nullptr, out_dim, 0, in_dim, stream);
+}
+
+int mia_q4_0_matvec_qkv_f32(const void *Wq, const void *Wk, const void *Wv, const float *x,
+                            float *yq, float *yk, float *yv, int dim, int kv_dim, int in_dim,
+                            void *stream) {
+  return q4_impl(Wq, Wk, Wv, nullptr, x, yq, yk, yv, dim, kv_dim, in_dim, stream);
 }
 
 }  // extern "C"

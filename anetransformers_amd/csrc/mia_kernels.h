@@ -88,10 +88,14 @@ hipError_t launch_fill_normal(_Float16 *dst, size_t n, uint64_t seed, hipStream_
 hipError_t launch_quantize_q8_0(const float *x, uint8_t *out, int nblocks, hipStream_t s);
 // y = W . x for up to three Q4_0 matrices stacked as virtual rows (w0's rows,
 // then w1's, then w2's); bpr = blocks per row, even; pointers 4-byte aligned.
+// x is either Q8_0 blocks (x) or fp32 values quantised in-kernel (xf, 16-byte
+// aligned, bpr * 32 <= kQ4MaxF32InDim).
+constexpr int kQ4MaxF32InDim = 8192;
 struct Q4MatvecParams {
   const uint8_t *w0, *w1, *w2;
   float *y0, *y1, *y2;
-  const uint8_t *x;  // Q8_0 blocks [bpr]
+  const uint8_t *x;  // Q8_0 blocks [bpr], or null when xf is set
+  const float *xf;   // fp32 [bpr * 32], or null
   int rows0;         // rows of w0
   int rows01;        // rows of w0 + w1
   int total_rows;    // rows of w0 + w1 + w2

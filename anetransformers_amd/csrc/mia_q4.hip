@@ -23,7 +23,7 @@
 namespace mia {
 namespace {
 
-constexpr int kQ4Threads = 256;
+constexpr int kQ4Threads = 512;
 constexpr int kQ4Waves = kQ4Threads / 64;
 constexpr unsigned kNib = 0x0F0F0F0Fu;
 
@@ -39,16 +39,13 @@ __device__ __forceinline__ int dot4(unsigned a, unsigned b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// 8 lanes per 32-value block, 4 values per lane.  amax is order-free (max of
-// absolute values), d = amax / 127 and id = 1 / d are IEEE-rounded divides,
+// One Q8_0 block from an aligned group of 8 lanes holding 4 values each
+// (values 4*sub .. 4*sub+3 of the block).  amax is order-free (max of absolute
+// values), d = amax / 127 and id = 1 / d are IEEE-rounded divides, and
 // q = round-half-even(x * id) saturated to int8, as vcvtnq_s32_f32 + vqmovn.
-__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x,
-                                                            uint8_t *__restrict__ out,
-                                                            int nblocks) {
-  const int gid = blockIdx.x * 256 + threadIdx.x;
-  const int blk = gid >> 3, sub = gid & 7;
-  if (blk >= nblocks) return;  // whole 8-lane groups leave together
-  const f4 v = *reinterpret_cast<const f4 *>(x + (size_t)blk * 32 + sub * 4);
+// Writes d (lane sub 0) and this lane's 4 int8 to the 36-byte block at ob.
+template <typename Byte>
+__device__ __forceinline__ void q8_block_part(const f4 v, int sub, Byte *ob) {
   float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
   a = fmaxf(a, __shfl_xor(a, 1));
   a = fmaxf(a, __shfl_xor(a, 2));
@@ -64,14 +61,29 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
       packed |= ((unsigned)(int)r & 0xFFu) << (8 * i);
     }
   }
-  uint8_t *ob = out + (size_t)blk * 36;
   if (sub == 0) *reinterpret_cast<float *>(ob) = d;
   *reinterpret_cast<unsigned *>(ob + 4 + 4 * sub) = packed;
 }
 
-template <int R>
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x,
+                                                            uint8_t *__restrict__ out,
+                                                            int nblocks) {
+  const int gid = blockIdx.x * 256 + threadIdx.x;
+  const int blk = gid >> 3, sub = gid & 7;
+  if (blk >= nblocks) return;  // whole 8-lane groups leave together
+  const f4 v = *reinterpret_cast<const f4 *>(x + (size_t)blk * 32 + sub * 4);
+  q8_block_part(v, sub, out + (size_t)blk * 36);
+}
+
+// XP > 0: x is fp32 and every workgroup quantises it into LDS (the same
+// arithmetic as quantize_q8_0_kernel, so the blocks are bit-identical) while
+// its weight rows are in flight; each thread loads XP groups of 4 values, so
+// XP * kQ4Threads / 8 >= bpr.  XP = 0: x is Q8_0 blocks in global memory.
+template <int R, int XP>
 __global__ __launch_bounds__(kQ4Threads) void q4_matvec_kernel(Q4MatvecParams p) {
 #pragma clang fp contract(off)
+  constexpr bool kF32X = XP > 0;
+  __shared__ __attribute__((aligned(16))) uint8_t xq_lds[kF32X ? kQ4MaxF32InDim / 32 * 36 : 4];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row0 = (blockIdx.x * kQ4Waves + wave) * R;
@@ -92,22 +104,53 @@ __global__ __launch_bounds__(kQ4Threads) void q4_matvec_kernel(Q4MatvecParams p)
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-
-  for (int p0 = 0; p0 < npairs; p0 += 64) {
-    const int pr = p0 + lane;
-    const bool on = pr < npairs;
-    const int pc = on ? pr : npairs - 1;
-    unsigned wv[R][9];
+  unsigned wv[R][9];
+  auto load_rows = [&](int pc) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const uint8_t *wp = wrow[r] + (size_t)pc * 36;
 #pragma unroll
       for (int j = 0; j < 9; ++j) wv[r][j] = ld32(wp + 4 * j);
     }
-    unsigned xv[18];
-    const uint8_t *xp = p.x + (size_t)pc * 72;
+  };
+
+  if constexpr (kF32X) {
+    // Activation loads first (clamped in bounds), then the first weight
+    // rows: waiting for the activations then leaves the rows in flight.
+    f4 xr[XP];
 #pragma unroll
-    for (int j = 0; j < 18; ++j) xv[j] = ld32(xp + 4 * j);
+    for (int k = 0; k < XP; ++k) {
+      const int blk = min(k * (kQ4Threads / 8) + (int)(threadIdx.x >> 3), p.bpr - 1);
+      xr[k] = *reinterpret_cast<const f4 *>(p.xf + (size_t)blk * 32 + (threadIdx.x & 7) * 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_rows(min(lane, npairs - 1));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < XP; ++k) {
+      const int blk = k * (kQ4Threads / 8) + (int)(threadIdx.x >> 3);
+      if (blk < p.bpr)  // whole 8-lane groups
+        q8_block_part(xr[k], threadIdx.x & 7, xq_lds + blk * 36);
+    }
+    // LDS writes done and visible; the weight loads stay outstanding.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+
+  for (int p0 = 0; p0 < npairs; p0 += 64) {
+    const int pr = p0 + lane;
+    const bool on = pr < npairs;
+    const int pc = on ? pr : npairs - 1;
+    if (!kF32X || p0 > 0) load_rows(pc);
+    unsigned xv[18];
+    if constexpr (kF32X) {
+      const uint8_t *xp = xq_lds + pc * 72;
+#pragma unroll
+      for (int j = 0; j < 18; ++j) xv[j] = *reinterpret_cast<const unsigned *>(xp + 4 * j);
+    } else {
+      const uint8_t *xp = p.x + (size_t)pc * 72;
+#pragma unroll
+      for (int j = 0; j < 18; ++j) xv[j] = ld32(xp + 4 * j);
+    }
 
     // x block A: d = xv[0], qs = xv[1..8]; block B: d = xv[9], qs = xv[10..17]
     int sxa = 0, sxb = 0;
@@ -171,7 +214,20 @@ hipError_t launch_q4_matvec(const Q4MatvecParams &p, hipStream_t s, hipEvent_t e
   constexpr int R = 2;
   const int rows_per_wg = kQ4Waves * R;
   const dim3 grid((p.total_rows + rows_per_wg - 1) / rows_per_wg);
-  hipExtLaunchKernelGGL(q4_matvec_kernel<R>, grid, dim3(kQ4Threads), 0, s, ev0, ev1, 0, p);
+  constexpr int kBlocksPerPass = kQ4Threads / 8;
+  static_assert(8 * kBlocksPerPass * 32 >= kQ4MaxF32InDim, "fused passes cover kQ4MaxF32InDim");
+  if (!p.xf)
+    hipExtLaunchKernelGGL(q4_matvec_kernel<R, 0>, grid, dim3(kQ4Threads), 0, s, ev0, ev1, 0, p);
+  else if (p.bpr <= kBlocksPerPass)
+    hipExtLaunchKernelGGL(q4_matvec_kernel<R, 1>, grid, dim3(kQ4Threads), 0, s, ev0, ev1, 0, p);
+  else if (p.bpr <= 2 * kBlocksPerPass)
+    hipExtLaunchKernelGGL(q4_matvec_kernel<R, 2>, grid, dim3(kQ4Threads), 0, s, ev0, ev1, 0, p);
+  else if (p.bpr <= 4 * kBlocksPerPass)
+    hipExtLaunchKernelGGL(q4_matvec_kernel<R, 4>, grid, dim3(kQ4Threads), 0, s, ev0, ev1, 0, p);
+  else if (p.bpr * 32 <= kQ4MaxF32InDim)
+    hipExtLaunchKernelGGL(q4_matvec_kernel<R, 8>, grid, dim3(kQ4Threads), 0, s, ev0, ev1, 0, p);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

@@ -195,6 +195,19 @@ def timed(lib, fn, steps: int, warmup: int) -> float:
     return e0.elapsed_ms(e1) / steps
 
 
+def kernel_stats(lib, fn, steps: int, kind: int):
+    """(launch count, average duration in ms) of the kernels of this kind over
+    `steps` calls of fn, from the library's per-kernel HIP event pairs."""
+    check(lib.mia_device_sync())
+    check(lib.mia_profile_begin())
+    for _ in range(steps):
+        fn()
+    n = ctypes.c_int()
+    tot = ctypes.c_double()
+    check(lib.mia_profile_end(kind, ctypes.byref(n), ctypes.byref(tot)))
+    return n.value, tot.value / max(n.value, 1)
+
+
 def kernel_avg_ms(lib, fn, steps: int, kind: int) -> float:
     """Average duration of the main attention kernel (kind 0 decode, 1 flash)
     over `steps` calls of fn, from the library's per-kernel HIP event pairs on
@@ -329,6 +342,137 @@ class OtherConfigs:
                                               N_KV, HD, 65536, 70000, 8, None), "attention_step")
 
 
+DIM = N_HEADS * HD
+Q4_ROW_BYTES = DIM // 32 * 18                    # a 4096-wide Q4_0 row
+Q8_BYTES = DIM // 32 * 36                        # the quantised 4096-vector
+QKV_ROWS = DIM + 2 * KV_DIM
+# algorithmic bytes of one fused launch: Q4_0 weights + fp32 x + fp32 y
+QKV_BYTES = QKV_ROWS * Q4_ROW_BYTES + DIM * 4 + QKV_ROWS * 4
+WO_BYTES = DIM * Q4_ROW_BYTES + DIM * 4 + DIM * 4
+
+
+class Projections:
+    """The W4A8 projections either side of the attention step, 32 layers:
+    per layer quantize(xb) -> fused QKV matvec, quantize(attention out) -> Wo
+    (mistral_model.h:833-842, 866-867).  Each layer has its own Q4_0 weights
+    (755 MB in all, far beyond the caches), filled with a seeded fp16 N(0,1)
+    stream read as Q4_0 bytes (finite scales, uniform-looking nibbles), scaled
+    so that the outputs are O(1)."""
+
+    def __init__(self, lib, seed: int = 41):
+        self.lib = lib
+        g = np.random.default_rng(seed)
+        self.lw = QKV_ROWS * Q4_ROW_BYTES + DIM * Q4_ROW_BYTES   # per layer: Wq Wk Wv Wo
+        self.w = DeviceBuffer(N_LAYERS * self.lw)
+        check(lib.mia_fill_normal_f16(self.w.ptr, N_LAYERS * self.lw // 2, seed, None))
+        # x 2^-8 keeps the scales near 0.004, so q, k, v come out O(1) for the
+        # attention block below
+        check(lib.mia_scale_rows_f16(self.w.ptr, N_LAYERS * self.lw // 2048, 1024, 1, 0,
+                                     1.0 / 256, None))
+        self.x = DeviceBuffer.from_array(g.standard_normal((N_LAYERS, DIM), np.float32))
+        self.a = DeviceBuffer.from_array(g.standard_normal((N_LAYERS, DIM), np.float32))
+        self.q8 = DeviceBuffer(Q8_BYTES)
+        self.y = DeviceBuffer(N_LAYERS * (QKV_ROWS + DIM) * 4)
+        check(lib.mia_device_sync())
+
+    def _w(self, l):
+        base = self.w.ptr + l * self.lw
+        wq = base
+        wk = wq + DIM * Q4_ROW_BYTES
+        wv = wk + KV_DIM * Q4_ROW_BYTES
+        wo = wv + KV_DIM * Q4_ROW_BYTES
+        return wq, wk, wv, wo
+
+    def _y(self, l):
+        yq = self.y.ptr + l * (QKV_ROWS + DIM) * 4
+        yk = yq + DIM * 4
+        yv = yk + KV_DIM * 4
+        yo = yv + KV_DIM * 4
+        return yq, yk, yv, yo
+
+    def qkv(self, l, x_ptr):
+        wq, wk, wv, _ = self._w(l)
+        yq, yk, yv, _ = self._y(l)
+        check(self.lib.mia_quantize_q8_0(x_ptr, self.q8.ptr, DIM, None), "quantize")
+        check(self.lib.mia_q4_0_matvec_qkv(wq, wk, wv, self.q8.ptr, yq, yk, yv, DIM, KV_DIM, DIM,
+                                           None), "qkv")
+        return yq, yk, yv
+
+    def wo(self, l, a_ptr):
+        _, _, _, wo = self._w(l)
+        _, _, _, yo = self._y(l)
+        check(self.lib.mia_quantize_q8_0(a_ptr, self.q8.ptr, DIM, None), "quantize")
+        check(self.lib.mia_q4_0_matvec(wo, self.q8.ptr, yo, DIM, DIM, None), "wo")
+
+    def qkv_fused(self, l, x_ptr):
+        wq, wk, wv, _ = self._w(l)
+        yq, yk, yv, _ = self._y(l)
+        check(self.lib.mia_q4_0_matvec_qkv_f32(wq, wk, wv, x_ptr, yq, yk, yv, DIM, KV_DIM, DIM,
+                                               None), "qkv_f32")
+        return yq, yk, yv
+
+    def wo_fused(self, l, a_ptr):
+        _, _, _, wo = self._w(l)
+        _, _, _, yo = self._y(l)
+        check(self.lib.mia_q4_0_matvec_f32(wo, a_ptr, yo, DIM, DIM, None), "wo_f32")
+
+    def step_two_launch(self) -> None:
+        """The reference's call pattern: quantize, then the matvec."""
+        for l in range(N_LAYERS):
+            self.qkv(l, self.x.ptr + l * DIM * 4)
+            self.wo(l, self.a.ptr + l * DIM * 4)
+
+    def step(self) -> None:
+        """Quantize folded into the matvec launches."""
+        for l in range(N_LAYERS):
+            self.qkv_fused(l, self.x.ptr + l * DIM * 4)
+            self.wo_fused(l, self.a.ptr + l * DIM * 4)
+
+    def block_step(self, dec: "Decode") -> None:
+        """The attention block of the decode step on the device: projections
+        around the fused attention at 32K context (mia_decode_step)."""
+        lay = DECODE_M * KV_DIM * 2
+        for l in range(N_LAYERS):
+            yq, yk, yv = self.qkv_fused(l, self.x.ptr + l * DIM * 4)
+            out = dec.out.ptr + l * DIM * 4
+            check(self.lib.mia_decode_step(yq, yk, yv, dec.th.ptr, dec.kc.ptr + l * lay,
+                                           dec.vc.ptr + l * lay, out, N_HEADS, N_KV, HD, DECODE_M,
+                                           DECODE_POS, None), "decode_step")
+            self.wo_fused(l, out)
+
+
+def cpu_baseline_projections(n_layers: int = 4, reps: int = 3):
+    """The oracle's row-parallel W4A8 matvec (OpenMP) on n_layers layers of
+    the same projections: quantize + QKV + quantize + Wo."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import _oracle as O
+
+    g = np.random.default_rng(14)
+    Ws = [(O.make_q4_0(g, QKV_ROWS, DIM), O.make_q4_0(g, DIM, DIM)) for _ in range(n_layers)]
+    xs = g.standard_normal((n_layers, 2, DIM), np.float32)
+    threads = O.num_threads(fast=True)
+
+    def run():
+        for l in range(n_layers):
+            O.q4_0_q8_0_matvec_parallel(Ws[l][0], O.quantize_q8_0(xs[l, 0]), QKV_ROWS, DIM,
+                                        threads=threads)
+            O.q4_0_q8_0_matvec_parallel(Ws[l][1], O.quantize_q8_0(xs[l, 1]), DIM, DIM,
+                                        threads=threads)
+
+    run()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    dt = float(np.median(ts))
+    return {"value": round(n_layers * (QKV_BYTES + WO_BYTES) / dt / 1e9, 3), "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": f"{n_layers} of 32 layers (quantize + QKV rows 6144 + quantize + Wo rows "
+                      f"4096, in_dim 4096), median of {reps}; oracle timing build, OpenMP over "
+                      f"rows"}
+
+
 def cpu_other_configs():
     """Oracle timing (same thread count as the headline baseline) on bounded
     samples of configs 1, 2 and 5."""
@@ -391,6 +535,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-decode", action="store_true", help="prefill only (profiling)")
+    ap.add_argument("--skip-projections", action="store_true",
+                    help="skip the W4A8 projection line (profiling)")
     ap.add_argument("--skip-configs", action="store_true",
                     help="skip the side configs 1, 2 and 5 (profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -413,7 +559,7 @@ def main() -> int:
         check(lib.mia_device_sync())
         del src, dst
     dec_ms = kern_ms = float("nan")
-    dropin = None
+    dropin = projections = None
     if not args.skip_decode:
         log("decode: allocating 32 x 32768-slot rings (4 GiB)")
         dec = Decode(lib)
@@ -426,7 +572,38 @@ def main() -> int:
                   "path": "mia_dropin_decode_step per layer, host q/k/v/out (PCIe), "
                           "synchronous, wall clock"}
         log(f"decode via drop-in (host buffers): {di_ms:.3f} ms/step")
-        del dd, dec
+        del dd
+        if not args.skip_projections:
+            log("projections: 32 layers x (quantize, QKV 6144 x 4096, quantize, Wo 4096 x 4096)")
+            pj = Projections(lib)
+            pj_ms = timed(lib, pj.step, args.steps, args.warmup)
+            pj2_ms = timed(lib, pj.step_two_launch, args.steps, args.warmup)
+            mv_n, mv_ms = kernel_stats(lib, pj.step, args.steps, 2)
+            blk_ms = timed(lib, lambda: pj.block_step(dec), args.steps, args.warmup)
+            mv_bytes = (QKV_BYTES + WO_BYTES) / 2           # per launch, launches alternate
+            mv_gbs = mv_bytes / (mv_ms * 1e-3) / 1e9
+            log(f"projections: {pj_ms:.3f} ms/step ({pj2_ms:.3f} with separate quantize "
+                f"launches), matvec kernel {mv_ms * 1e3:.2f} us avg "
+                f"({mv_gbs:.0f} GB/s); attention block {blk_ms:.3f} ms/step")
+            projections = {
+                "workload": "W4A8 projections of the decode step, 32 layers: quantize + fused "
+                            "QKV (6144 x 4096 Q4_0) + quantize + Wo (4096 x 4096 Q4_0), own "
+                            "weights per layer (755 MB); quantize folded into each matvec "
+                            "launch (mia_q4_0_matvec_qkv_f32, mia_q4_0_matvec_f32)",
+                "value": round(N_LAYERS * (QKV_BYTES + WO_BYTES) / (pj_ms * 1e-3) / 1e9, 2),
+                "unit": "GB/s", "ms_per_step": round(pj_ms, 4),
+                "two_launch_ms_per_step": round(pj2_ms, 4),
+                "bytes_per_layer": QKV_BYTES + WO_BYTES,
+                "matvec_kernel_us": round(mv_ms * 1e3, 3), "matvec_launches": mv_n,
+                "roofline": {"bound": "hbm", "achieved": round(mv_gbs, 2), "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(mv_gbs / HBM_PEAK_GBS, 4),
+                             "traffic": load_traffic("q4_matvec")},
+                "attention_block_ms_per_step": round(blk_ms, 4),
+                "attention_block": "per layer: quantize, QKV, mia_decode_step at 32K context "
+                                   "(the headline's rings), quantize, Wo",
+            }
+            del pj
+        del dec
     achieved = DECODE_BYTES_PER_LAYER / (kern_ms * 1e-3) / 1e9
     value = N_LAYERS * DECODE_BYTES_PER_LAYER / (dec_ms * 1e-3) / 1e9
     log(f"decode: {dec_ms:.3f} ms/step, {value:.1f} GB/s; decode kernel {kern_ms * 1e3:.2f} us "
@@ -488,6 +665,9 @@ def main() -> int:
         if prefill is not None:
             log("cpu baseline: prefill sample")
             prefill["cpu_baseline"] = cpu_baseline_prefill()
+        if projections is not None:
+            log("cpu baseline: projections sample")
+            projections["cpu_baseline"] = cpu_baseline_projections()
         if configs is not None:
             log("cpu baseline: configs 1, 2, 5")
             for k, v in cpu_other_configs().items():
@@ -522,6 +702,7 @@ def main() -> int:
         "dropin": dropin,
         "prefill": prefill,
         "configs": configs,
+        "projections": projections,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -171,6 +171,14 @@ static inline void attention_batch(const float *Q, float *attn_out, const KVCach
                                    float *att_scratch) {
     mia_dropin_attention_batch(Q, attn_out, kv, layer, start_pos, c, S, att_scratch);
 }
+#endif /* MIA_DROPIN_NO_REFERENCE_NAMES */
+
+/* The W4A8 names live in mistral/dequant.h, which mistral_model.h includes for
+ * every other weight type as well, so they are opt-in: define
+ * MIA_DROPIN_Q4_REFERENCE_NAMES in a translation unit that does not include
+ * dequant.h.  Elsewhere call the mia_dropin_ forms; mia_block_q8_0 has
+ * block_q8_0's layout, so a pointer cast passes the reference's buffers. */
+#ifdef MIA_DROPIN_Q4_REFERENCE_NAMES
 typedef mia_block_q8_0 block_q8_0;
 static inline void quantize_f32_to_q8_0(const float *x, block_q8_0 *out, int n) {
     mia_dropin_quantize_q8_0(x, out, n);
@@ -186,7 +194,7 @@ static inline void q4_matvec_sdot_parallel_fused_qkv(const void *Wq, const void 
     mia_dropin_q4_matvec_sdot_parallel_fused_qkv(Wq, Wk, Wv, x_q8, yq, yk, yv, dim, kv_dim,
                                                  in_dim);
 }
-#endif /* MIA_DROPIN_NO_REFERENCE_NAMES */
+#endif /* MIA_DROPIN_Q4_REFERENCE_NAMES */
 
 #ifdef __cplusplus
 }

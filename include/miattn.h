@@ -157,6 +157,18 @@ int mia_q4_0_matvec_qkv(const void *Wq, const void *Wk, const void *Wv, const vo
                         float *yq, float *yk, float *yv, int dim, int kv_dim, int in_dim,
                         void *stream);
 
+/* quantize_f32_to_q8_0 followed by the matvec, as the decode layer calls
+ * them (mistral/mistral_model.h:866-867 for Wo; :833-842 for Q, K, V), in one
+ * launch: x [in_dim] fp32 dev, 16-byte aligned, in_dim <= 8192.  Every
+ * workgroup forms the Q8_0 blocks of x in LDS with mia_quantize_q8_0's
+ * arithmetic, so y is bit-identical to mia_quantize_q8_0 + mia_q4_0_matvec
+ * (resp. _qkv); the blocks themselves are not written out. */
+int mia_q4_0_matvec_f32(const void *W, const float *x, float *y, int out_dim, int in_dim,
+                        void *stream);
+int mia_q4_0_matvec_qkv_f32(const void *Wq, const void *Wk, const void *Wv, const float *x,
+                            float *yq, float *yk, float *yv, int dim, int kv_dim, int in_dim,
+                            void *stream);
+
 #ifdef __cplusplus
 }
 #endif

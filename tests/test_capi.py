@@ -51,6 +51,7 @@ def test_library_exports_nothing_unprefixed():
 def test_dropin_header_compiles_and_links(tmp_path):
     src = tmp_path / "use_dropin.c"
     src.write_text(r'''
+#define MIA_DROPIN_Q4_REFERENCE_NAMES
 #include "mia_dropin.h"
 /* the reference's call sequence, mistral/mistral_model.h:849-863 */
 void layer_attention(KVCache *kv, float *q, float *k, float *att, float *out, _Float16 *k16,
@@ -124,6 +125,10 @@ def test_q4_argument_errors_without_device_work():
     rc = lib.mia_q4_0_matvec(p + 2, p, p, 64, 128, None)      # misaligned weights
     assert rc == mia.MIA_ERR_INVALID and b"aligned" in lib.mia_last_error()
     rc = lib.mia_q4_0_matvec_qkv(p, None, p, p, p, p, p, 64, 16, 128, None)
+    assert rc == mia.MIA_ERR_INVALID
+    rc = lib.mia_q4_0_matvec_f32(p, p, p, 64, 16384, None)    # fused form: in_dim <= 8192
+    assert rc == mia.MIA_ERR_UNSUPPORTED
+    rc = lib.mia_q4_0_matvec_f32(p, p + 4, p, 64, 128, None)   # fp32 x needs 16-byte alignment
     assert rc == mia.MIA_ERR_INVALID
     rc = lib.mia_quantize_q8_0(p, p, 48, None)
     assert rc == mia.MIA_ERR_INVALID

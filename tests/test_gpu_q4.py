@@ -212,3 +212,44 @@ def test_dropin_projections():
                                          yo.ctypes.data, dim, dim)   # Q8_0 weights
     assert L.mia_dropin_status() == mia.MIA_ERR_UNSUPPORTED
     L.mia_dropin_set_abort(1)
+
+
+@pytest.mark.parametrize("out_dim,in_dim", [(4096, 4096), (37, 256), (130, 8192), (9, 64),
+                                            (20, 2112)])
+def test_fused_f32_input_is_bit_identical(out_dim, in_dim):
+    # mia_q4_0_matvec_f32 quantises in every workgroup: y must equal
+    # mia_quantize_q8_0 + mia_q4_0_matvec bit for bit, and the oracle's chain
+    # within the reassociation bound
+    G.say(f"q4: fused f32 {out_dim}x{in_dim}")
+    L = G.lib()
+    g = np.random.default_rng(out_dim + 3 * in_dim)
+    W = O.make_q4_0(g, out_dim, in_dim)
+    x = special_activation(g, in_dim) if in_dim >= 128 else g.standard_normal(in_dim).astype(
+        np.float32)
+    dw, dx, dy = DB.from_array(W), DB.from_array(x), DB(out_dim * 4)
+    check(L.mia_q4_0_matvec_f32(dw.ptr, dx.ptr, dy.ptr, out_dim, in_dim, None), "matvec_f32")
+    check(L.mia_stream_sync(None), "sync")
+    y = dy.download(out_dim, np.float32)
+    xq = gpu_quantize(x)
+    assert np.array_equal(y, gpu_matvec(W, xq, out_dim, in_dim))
+    assert_rows_close(y, O.q4_0_q8_0_matvec(W, O.quantize_q8_0(x), out_dim, in_dim), W, xq,
+                      out_dim, in_dim, "fused")
+
+
+@pytest.mark.parametrize("dim,kv_dim,in_dim", [(4096, 1024, 4096), (37, 5, 128)])
+def test_fused_f32_qkv_is_bit_identical(dim, kv_dim, in_dim):
+    G.say(f"q4: fused f32 qkv {dim}/{kv_dim}x{in_dim}")
+    L = G.lib()
+    g = np.random.default_rng(dim * 5 + kv_dim)
+    Wq, Wk, Wv = (O.make_q4_0(g, r, in_dim) for r in (dim, kv_dim, kv_dim))
+    x = g.standard_normal(in_dim).astype(np.float32)
+    dwq, dwk, dwv, dx = (DB.from_array(a) for a in (Wq, Wk, Wv, x))
+    dyq, dyk, dyv = DB(dim * 4), DB(kv_dim * 4), DB(kv_dim * 4)
+    check(L.mia_q4_0_matvec_qkv_f32(dwq.ptr, dwk.ptr, dwv.ptr, dx.ptr, dyq.ptr, dyk.ptr, dyv.ptr,
+                                    dim, kv_dim, in_dim, None), "qkv_f32")
+    check(L.mia_stream_sync(None), "sync")
+    got = (dyq.download(dim, np.float32), dyk.download(kv_dim, np.float32),
+           dyv.download(kv_dim, np.float32))
+    two = gpu_matvec_qkv(Wq, Wk, Wv, gpu_quantize(x), dim, kv_dim, in_dim)
+    for a, b in zip(got, two):
+        assert np.array_equal(a, b)
