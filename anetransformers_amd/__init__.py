@@ -101,6 +101,14 @@ _SIGS = {
         c_int,
         [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, _P],
     ),
+    "mia_attention_step_staged": (
+        c_int,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, _P],
+    ),
+    "mia_commit_staged": (
+        c_int,
+        [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, _P],
+    ),
     "mia_quantize_q8_0": (c_int, [_P, _P, c_int, _P]),
     "mia_q4_0_matvec": (c_int, [_P, _P, _P, c_int, c_int, _P]),
     "mia_q4_0_matvec_qkv": (
@@ -134,6 +142,11 @@ _SIGS = {
         None,
         [POINTER(KVCache), c_int, _P, _P, _P, c_int, c_int, _P, c_int, c_int, _P],
     ),
+    "mia_dropin_verify_stage": (
+        None,
+        [POINTER(KVCache), c_int, _P, _P, _P, c_int, c_int, _P, c_int, c_int, _P],
+    ),
+    "mia_dropin_verify_commit": (None, [POINTER(KVCache), c_int, c_int]),
     "mia_dropin_quantize_q8_0": (None, [_P, _P, c_int]),
     "mia_dropin_q4_matvec_sdot_parallel": (None, [_P, ctypes.c_uint32, _P, _P, c_int, c_int]),
     "mia_dropin_q4_matvec_sdot_parallel_fused_qkv": (

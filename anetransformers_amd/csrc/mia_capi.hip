@@ -145,9 +145,12 @@ int prof_pair(DevCtx *c, int kind, hipEvent_t *ev0, hipEvent_t *ev1) {
   return MIA_OK;
 }
 
+// new_k / new_v (fused only, may be null): where the new token's fp16 rows go
+// instead of its ring slot.
 int decode_impl(const float *q, const float *k, const float *v, const float *theta_inv,
                 uint16_t *k_layer, uint16_t *v_layer, float *out, int n_heads, int n_kv, int max_seq,
-                int pos, bool fused, void *stream) {
+                int pos, bool fused, void *stream, uint16_t *new_k = nullptr,
+                uint16_t *new_v = nullptr) {
   DevCtx *c;
   if (int rc = current_ctx(&c)) return rc;
   const int L = pos + 1 < max_seq ? pos + 1 : max_seq;
@@ -160,6 +163,8 @@ int decode_impl(const float *q, const float *k, const float *v, const float *the
   p.kc = reinterpret_cast<_Float16 *>(k_layer);
   p.vc = reinterpret_cast<_Float16 *>(v_layer);
   p.out = out;
+  p.new_k = reinterpret_cast<_Float16 *>(new_k);
+  p.new_v = reinterpret_cast<_Float16 *>(new_v);
   p.max_seq = max_seq;
   p.pos = pos;
   p.L = L;
@@ -547,6 +552,57 @@ int mia_attention_step(const float *Q, const float *K, const float *V, const flo
   return flash_impl(c, Q, cs, reinterpret_cast<uint16_t *>(kst),
                     reinterpret_cast<uint16_t *>(vst), k_layer, v_layer, out, n_kv_heads, max_seq,
                     start_pos, S, s, true);
+}
+
+int mia_attention_step_staged(const float *Q, const float *K, const float *V,
+                              const float *theta_inv, const uint16_t *k_layer,
+                              const uint16_t *v_layer, uint16_t *k_stage, uint16_t *v_stage,
+                              float *out, int n_heads, int n_kv_heads, int hd, int max_seq,
+                              int start_pos, int S, void *stream) {
+  if (!Q || !K || !V || !theta_inv || !out || !k_layer || !v_layer || !k_stage || !v_stage)
+    return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (int rc = check_shape(n_heads, n_kv_heads, hd, max_seq)) return rc;
+  if (int rc = check_pos(start_pos, S)) return rc;
+  if (int rc = check_align16(Q, K, V, out)) return rc;
+  if (int rc = check_align16(k_layer, v_layer, k_stage, v_stage)) return rc;
+  if (S == 1)
+    return decode_impl(Q, K, V, theta_inv, const_cast<uint16_t *>(k_layer),
+                       const_cast<uint16_t *>(v_layer), out, n_heads, n_kv_heads, max_seq,
+                       start_pos, true, stream, k_stage, v_stage);
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  hipStream_t s = pick_stream(c, stream);
+  const size_t cs_bytes = (size_t)S * kHD * sizeof(float);  // S x 64 (cos, sin)
+  if (int rc = ensure_work(c, cs_bytes)) return rc;
+  float *cs = reinterpret_cast<float *>(c->work);
+  HIP_TRY(mia::launch_rope_to_f16(K, V, theta_inv, S, start_pos, n_kv_heads,
+                                  reinterpret_cast<_Float16 *>(k_stage),
+                                  reinterpret_cast<_Float16 *>(v_stage), cs, s));
+  return flash_impl(c, Q, cs, k_stage, v_stage, k_layer, v_layer, out, n_kv_heads, max_seq,
+                    start_pos, S, s);
+}
+
+int mia_commit_staged(uint16_t *k_cache, uint16_t *v_cache, const uint16_t *k_stage,
+                      const uint16_t *v_stage, int n_layers, int S_staged, int n_keep,
+                      int start_pos, int max_seq, int kv_dim, void *stream) {
+  if (!k_cache || !v_cache || !k_stage || !v_stage) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (n_layers <= 0 || n_layers > 1024 || S_staged <= 0 || n_keep < 0 || n_keep > S_staged)
+    return set_err(MIA_ERR_INVALID, "bad counts (n_layers=%d S_staged=%d n_keep=%d)", n_layers,
+                   S_staged, n_keep);
+  if (kv_dim <= 0 || kv_dim % 8 || max_seq <= 0 || max_seq > kMaxSeq)
+    return set_err(MIA_ERR_INVALID, "bad kv_dim/max_seq");
+  if (n_keep > max_seq) return set_err(MIA_ERR_INVALID, "n_keep %d above max_seq %d", n_keep, max_seq);
+  if (int rc = check_pos(start_pos, S_staged)) return rc;
+  if (int rc = check_align16(k_cache, v_cache, k_stage, v_stage)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  HIP_TRY(mia::launch_commit(reinterpret_cast<_Float16 *>(k_cache),
+                             reinterpret_cast<_Float16 *>(v_cache),
+                             reinterpret_cast<const _Float16 *>(k_stage),
+                             reinterpret_cast<const _Float16 *>(v_stage), n_keep, start_pos,
+                             max_seq, kv_dim, pick_stream(c, stream), n_layers,
+                             (size_t)max_seq * kv_dim, (size_t)S_staged * kv_dim));
+  return MIA_OK;
 }
 
 int mia_quantize_q8_0(const float *x, void *out_q8, int n, void *stream) {

@@ -188,10 +188,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
       sm.vnew[w][2 * lane + 1] = (_Float16)vv.y;
     }
     __syncthreads();
-    if (has_new && active && lane < 16) {  // ring write of the new row (256 B per tensor)
-      size_t off = (size_t)p.new_slot * kv_dim + (size_t)kvh * HD + 8 * lane;
-      *reinterpret_cast<u4 *>(p.kc + off) = *reinterpret_cast<const u4 *>(&sm.knew[w][8 * lane]);
-      *reinterpret_cast<u4 *>(p.vc + off) = *reinterpret_cast<const u4 *>(&sm.vnew[w][8 * lane]);
+    if (has_new && active && lane < 16) {  // write of the new row (256 B per tensor)
+      const size_t row = p.new_k ? 0 : (size_t)p.new_slot * kv_dim;
+      _Float16 *kd = (p.new_k ? p.new_k : p.kc) + row, *vd = (p.new_v ? p.new_v : p.vc) + row;
+      const size_t off = (size_t)kvh * HD + 8 * lane;
+      *reinterpret_cast<u4 *>(kd + off) = *reinterpret_cast<const u4 *>(&sm.knew[w][8 * lane]);
+      *reinterpret_cast<u4 *>(vd + off) = *reinterpret_cast<const u4 *>(&sm.vnew[w][8 * lane]);
     }
   }
 

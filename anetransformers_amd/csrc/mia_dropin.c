@@ -197,15 +197,48 @@ void mia_dropin_attention_batch(const float *Q, float *attn_out, const KVCache *
     TRY("attention_batch", mia_memcpy_d2h(attn_out, dout, nb));
 }
 
+/* Staged verify rows: [n_layers][S][kv_dim] fp16 K, then the same for V, for
+ * one batch of drafts (start_pos, S) at a time. */
+static uint16_t *g_stage = NULL;
+static size_t g_stage_bytes = 0;
+static int g_stage_start = -1, g_stage_S = 0, g_stage_layers = 0;
+static unsigned char *g_stage_done = NULL; /* per layer: staged for this batch */
+
+static int stage_for(KVCache *kv, int start_pos, int S) {
+    size_t need = 2 * (size_t)kv->n_layers * S * kv->kv_dim * sizeof(uint16_t);
+    if (g_stage_start != start_pos || g_stage_S != S || g_stage_layers != kv->n_layers) {
+        if (need > g_stage_bytes) {
+            if (g_stage) {
+                int rc = mia_free(g_stage);
+                if (rc) return rc;
+            }
+            g_stage = NULL;
+            g_stage_bytes = 0;
+            int rc = mia_malloc((void **)&g_stage, need);
+            if (rc) return rc;
+            g_stage_bytes = need;
+        }
+        unsigned char *done = (unsigned char *)realloc(g_stage_done, (size_t)kv->n_layers);
+        if (!done) return MIA_ERR_INVALID;
+        g_stage_done = done;
+        memset(g_stage_done, 0, (size_t)kv->n_layers);
+        g_stage_start = start_pos;
+        g_stage_S = S;
+        g_stage_layers = kv->n_layers;
+    }
+    return MIA_OK;
+}
+
 static void step_common(const char *what, KVCache *kv, int layer, const float *Q, const float *K,
                         const float *V, int start_pos, int S, const float *theta_inv, int n_heads,
-                        int n_kv_heads, float *out) {
+                        int n_kv_heads, float *out, int staged) {
     g_status = 0;
     if (layer < 0 || layer >= kv->n_layers || S <= 0 || n_heads <= 0 || n_kv_heads <= 0 ||
         n_kv_heads * kv->head_dim != kv->kv_dim) {
         fail(MIA_ERR_INVALID, what);
         return;
     }
+    if (staged) TRY(what, stage_for(kv, start_pos, S));
     int hd = kv->head_dim;
     size_t qb = (size_t)S * n_heads * hd * sizeof(float);
     size_t kb = (size_t)S * kv->kv_dim * sizeof(float);
@@ -222,11 +255,25 @@ static void step_common(const char *what, KVCache *kv, int layer, const float *Q
     TRY(what, mia_memcpy_h2d(dv, V, kb));
     TRY(what, mia_memcpy_h2d(dt, theta_inv, tb));
     size_t lay = (size_t)layer * kv->max_seq * kv->kv_dim;
-    TRY(what, mia_attention_step(dq, dk, dv, dt, (uint16_t *)(kv->k_cache + lay),
-                                 (uint16_t *)(kv->v_cache + lay), dout, n_heads, n_kv_heads, hd,
-                                 kv->max_seq, start_pos, S, NULL));
+    if (staged) {
+        size_t rows = (size_t)S * kv->kv_dim;
+        uint16_t *ks = g_stage + (size_t)layer * rows;
+        uint16_t *vs = g_stage + (size_t)kv->n_layers * rows + (size_t)layer * rows;
+        TRY(what, mia_attention_step_staged(dq, dk, dv, dt, (uint16_t *)(kv->k_cache + lay),
+                                            (uint16_t *)(kv->v_cache + lay), ks, vs, dout,
+                                            n_heads, n_kv_heads, hd, kv->max_seq, start_pos, S,
+                                            NULL));
+    } else {
+        TRY(what, mia_attention_step(dq, dk, dv, dt, (uint16_t *)(kv->k_cache + lay),
+                                     (uint16_t *)(kv->v_cache + lay), dout, n_heads, n_kv_heads,
+                                     hd, kv->max_seq, start_pos, S, NULL));
+    }
     TRY(what, mia_stream_sync(NULL));
     TRY(what, mia_memcpy_d2h(out, dout, qb));
+    if (staged) {
+        g_stage_done[layer] = 1;
+        return; /* the ring and len change at commit */
+    }
     /* mistral_model.h:858, once per token as the sequential steps do */
     for (int i = 0; i < S; i++) {
         int pos = start_pos + i;
@@ -237,14 +284,14 @@ static void step_common(const char *what, KVCache *kv, int layer, const float *Q
 void mia_dropin_decode_step(KVCache *kv, int layer, const float *q, const float *k, const float *v,
                             int pos, const float *theta_inv, int n_heads, int n_kv_heads,
                             float *out) {
-    step_common("decode_step", kv, layer, q, k, v, pos, 1, theta_inv, n_heads, n_kv_heads, out);
+    step_common("decode_step", kv, layer, q, k, v, pos, 1, theta_inv, n_heads, n_kv_heads, out, 0);
 }
 
 void mia_dropin_verify_step(KVCache *kv, int layer, const float *Q, const float *K, const float *V,
                             int start_pos, int S, const float *theta_inv, int n_heads,
                             int n_kv_heads, float *out) {
     step_common("verify_step", kv, layer, Q, K, V, start_pos, S, theta_inv, n_heads, n_kv_heads,
-                out);
+                out, 0);
 }
 
 void mia_dropin_quantize_q8_0(const float *x, mia_block_q8_0 *out, int n) {
@@ -300,4 +347,39 @@ void mia_dropin_q4_matvec_sdot_parallel(const void *W, uint32_t type, const mia_
     }
     mia_dropin_q4_matvec_sdot_parallel_fused_qkv(W, NULL, NULL, x_q8, y, NULL, NULL, out_dim, 0,
                                                  in_dim);
+}
+
+void mia_dropin_verify_stage(KVCache *kv, int layer, const float *Q, const float *K, const float *V,
+                             int start_pos, int S, const float *theta_inv, int n_heads,
+                             int n_kv_heads, float *out) {
+    step_common("verify_stage", kv, layer, Q, K, V, start_pos, S, theta_inv, n_heads, n_kv_heads,
+                out, 1);
+}
+
+void mia_dropin_verify_commit(KVCache *kv, int start_pos, int n_accepted) {
+    const char *what = "verify_commit";
+    g_status = 0;
+    if (g_stage_start != start_pos || g_stage_layers != kv->n_layers || n_accepted < 0 ||
+        n_accepted > g_stage_S) {
+        fail(MIA_ERR_INVALID, "verify_commit (no staged batch at this start_pos, or n_accepted "
+                              "above its size)");
+        return;
+    }
+    for (int l = 0; l < kv->n_layers; l++) {
+        if (!g_stage_done[l]) {
+            fail(MIA_ERR_INVALID, "verify_commit (a layer of the batch was not staged)");
+            return;
+        }
+    }
+    size_t rows = (size_t)g_stage_S * kv->kv_dim;
+    TRY(what, mia_commit_staged((uint16_t *)kv->k_cache, (uint16_t *)kv->v_cache, g_stage,
+                                g_stage + (size_t)kv->n_layers * rows, kv->n_layers, g_stage_S,
+                                n_accepted, start_pos, kv->max_seq, kv->kv_dim, NULL));
+    TRY(what, mia_stream_sync(NULL));
+    /* mistral_model.h:858, once per committed token */
+    for (int i = 0; i < n_accepted; i++) {
+        int pos = start_pos + i;
+        if (kv->len < kv->max_seq && pos + 1 > kv->len) kv->len = pos + 1;
+    }
+    g_stage_start = -1; /* the batch is spent */
 }

@@ -111,10 +111,17 @@ __global__ void kv_write_kernel(_Float16 *kc, _Float16 *vc, const float *K, cons
   }
 }
 
+// Staged row t of layer blockIdx.z -> ring slot (start_pos + t) % max_seq of
+// that layer; layers are ring_stride / stage_stride elements apart.
 __global__ void commit_kernel(_Float16 *kc, _Float16 *vc, const _Float16 *kst,
-                              const _Float16 *vst, int S, int start_pos, int max_seq, int kv_dim) {
+                              const _Float16 *vst, int S, int start_pos, int max_seq, int kv_dim,
+                              size_t ring_stride, size_t stage_stride) {
   const int t = blockIdx.y;
   const size_t slot = (size_t)((start_pos + t) % max_seq);
+  kc += blockIdx.z * ring_stride;
+  vc += blockIdx.z * ring_stride;
+  kst += blockIdx.z * stage_stride;
+  vst += blockIdx.z * stage_stride;
   for (int e = (blockIdx.x * blockDim.x + threadIdx.x) * 8; e < kv_dim;
        e += gridDim.x * blockDim.x * 8) {
     *reinterpret_cast<u4 *>(kc + slot * kv_dim + e) =
@@ -194,11 +201,12 @@ hipError_t launch_kv_write(_Float16 *kc, _Float16 *vc, const float *K, const flo
 }
 
 hipError_t launch_commit(_Float16 *kc, _Float16 *vc, const _Float16 *kst, const _Float16 *vst,
-                         int S, int start_pos, int max_seq, int kv_dim, hipStream_t s) {
-  if (S <= 0) return hipSuccess;
+                         int S, int start_pos, int max_seq, int kv_dim, hipStream_t s,
+                         int n_layers, size_t ring_stride, size_t stage_stride) {
+  if (S <= 0 || n_layers <= 0) return hipSuccess;
   int bx = (kv_dim / 8 + 127) / 128;
-  hipLaunchKernelGGL(commit_kernel, dim3(bx, S), dim3(128), 0, s, kc, vc, kst, vst, S, start_pos,
-                     max_seq, kv_dim);
+  hipLaunchKernelGGL(commit_kernel, dim3(bx, S, n_layers), dim3(128), 0, s, kc, vc, kst, vst, S,
+                     start_pos, max_seq, kv_dim, ring_stride, stage_stride);
   return hipGetLastError();
 }
 

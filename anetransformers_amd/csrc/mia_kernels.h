@@ -17,6 +17,8 @@ struct DecodeParams {
   _Float16 *kc;            // layer base [max_seq][kv_dim]
   _Float16 *vc;
   float *out;              // [n_kv*G][128]
+  _Float16 *new_k;         // fused: where the new token's fp16 k / v rows go
+  _Float16 *new_v;         // ([kv_dim] each); null: ring slot new_slot
   float *part_o;           // [n_kv][nchunk][G][128] unnormalised partial outputs
   float *part_ml;          // [n_kv][nchunk][G][2] partial (max, sum), log2 domain
   int max_seq;             // ring capacity M
@@ -79,8 +81,11 @@ hipError_t launch_rope_to_ring(const float *K, const float *V, const float *thet
                                float *cs_out, hipStream_t s);
 hipError_t launch_kv_write(_Float16 *kc, _Float16 *vc, const float *K, const float *V, int S,
                            int start_pos, int max_seq, int kv_dim, hipStream_t s);
+// Staged rows 0..S-1 -> ring slots (start_pos + t) % max_seq, for n_layers
+// layers ring_stride / stage_stride elements apart.
 hipError_t launch_commit(_Float16 *kc, _Float16 *vc, const _Float16 *kst, const _Float16 *vst,
-                         int S, int start_pos, int max_seq, int kv_dim, hipStream_t s);
+                         int S, int start_pos, int max_seq, int kv_dim, hipStream_t s,
+                         int n_layers = 1, size_t ring_stride = 0, size_t stage_stride = 0);
 hipError_t launch_fill_normal(_Float16 *dst, size_t n, uint64_t seed, hipStream_t s);
 
 // W4A8 projections (mistral/dequant.h).  x [nblocks*32] fp32, 16-byte aligned

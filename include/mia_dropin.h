@@ -106,6 +106,18 @@ void mia_dropin_verify_step(KVCache *kv, int layer, const float *Q, const float 
                             int start_pos, int S, const float *theta_inv, int n_heads,
                             int n_kv_heads, float *out);
 
+/* Speculative verify with accept-only commit (mistral/speculative.h:81-105,
+ * 242-341): mia_dropin_verify_stage runs one layer's attention for the S
+ * verify tokens like mia_dropin_verify_step but leaves the ring untouched,
+ * keeping the drafts' K/V in a staging area; once acceptance is known,
+ * mia_dropin_verify_commit writes the first n_accepted of every layer and
+ * updates len.  Rejected drafts never reach the ring.  One batch at a time;
+ * staging a different (start_pos, S) discards an uncommitted batch. */
+void mia_dropin_verify_stage(KVCache *kv, int layer, const float *Q, const float *K, const float *V,
+                             int start_pos, int S, const float *theta_inv, int n_heads,
+                             int n_kv_heads, float *out);
+void mia_dropin_verify_commit(KVCache *kv, int start_pos, int n_accepted);
+
 /* W4A8 projections.  Weights W* are device memory holding the Q4_0 blocks as
  * GGUF stores them (the Metal backend re-homes the mmap'd weight file the same
  * way, mistral/metal_matvec.h:185-192, 314); x, x_q8 and y are host buffers. */

@@ -127,6 +127,29 @@ int mia_attention_step(const float *Q, const float *K, const float *V, const flo
                        uint16_t *k_layer, uint16_t *v_layer, float *out, int n_heads,
                        int n_kv_heads, int hd, int max_seq, int start_pos, int S, void *stream);
 
+/* The verify step without touching the ring: the result equals S calls of
+ * mia_decode_step at start_pos, start_pos+1, ... (as mia_attention_step), but
+ * the S rotated fp16 keys and values are left in k_stage / v_stage
+ * [S][n_kv_heads*128] (device) and the ring is only read.  After acceptance,
+ * mia_commit_staged writes the accepted drafts.  Replaces the per-layer body of
+ * spec_verify (mistral/speculative.h:92-101) so that rejected drafts never
+ * reach the ring: the reference leaves them in their slots
+ * (speculative.h:336-341), which on a wrapped ring are the oldest positions
+ * of the next step's window.  16-byte aligned pointers. */
+int mia_attention_step_staged(const float *Q, const float *K, const float *V,
+                              const float *theta_inv, const uint16_t *k_layer,
+                              const uint16_t *v_layer, uint16_t *k_stage, uint16_t *v_stage,
+                              float *out, int n_heads, int n_kv_heads, int hd, int max_seq,
+                              int start_pos, int S, void *stream);
+
+/* Writes staged rows 0..n_keep-1 (n_keep <= S_staged) to ring slots
+ * (start_pos + t) % max_seq, for n_layers layers at once: k_cache / v_cache
+ * are layer 0's ring (layers max_seq*kv_dim elements apart, kv_cache.h:2-4)
+ * and k_stage / v_stage hold [n_layers][S_staged][kv_dim]. */
+int mia_commit_staged(uint16_t *k_cache, uint16_t *v_cache, const uint16_t *k_stage,
+                      const uint16_t *v_stage, int n_layers, int S_staged, int n_keep,
+                      int start_pos, int max_seq, int kv_dim, void *stream);
+
 /* ---- W4A8 projections either side of the attention step ------------------ */
 /* Block formats of mistral/dequant.h: Q4_0 = 18 bytes per 32 weights (fp16
  * scale, 16 bytes of nibbles: byte j low = weight j, high = weight j+16, each

@@ -112,6 +112,30 @@ def test_argument_errors_without_device_work():
     assert rc == mia.MIA_ERR_UNSUPPORTED
 
 
+def test_staged_verify_argument_errors_without_device_work():
+    lib = mia.load()
+    buf = np.zeros(64, np.float32)
+    p = buf.ctypes.data
+    rc = lib.mia_attention_step_staged(p, p, p, p, p, p, None, p, p, 32, 8, 128, 64, 0, 4, None)
+    assert rc == mia.MIA_ERR_INVALID
+    rc = lib.mia_attention_step_staged(p, p, p, p, p, p, p, p, p, 32, 8, 64, 64, 0, 4, None)
+    assert rc == mia.MIA_ERR_UNSUPPORTED
+    rc = lib.mia_commit_staged(p, p, p, p, 1, 4, 5, 0, 64, 1024, None)     # n_keep > S_staged
+    assert rc == mia.MIA_ERR_INVALID
+    rc = lib.mia_commit_staged(p, p, p, p, 0, 4, 2, 0, 64, 1024, None)     # no layers
+    assert rc == mia.MIA_ERR_INVALID
+    rc = lib.mia_commit_staged(p, p, p, p, 1, 4, 2, -1, 64, 1024, None)    # negative position
+    assert rc == mia.MIA_ERR_INVALID
+    lib.mia_dropin_set_abort(0)
+    try:
+        kv = mia.KVCache()
+        kv.n_layers, kv.kv_dim, kv.max_seq = 2, 1024, 64
+        lib.mia_dropin_verify_commit(ctypes.byref(kv), 10, 2)           # nothing staged
+        assert lib.mia_dropin_status() == mia.MIA_ERR_INVALID
+    finally:
+        lib.mia_dropin_set_abort(1)
+
+
 def test_q4_argument_errors_without_device_work():
     lib = mia.load()
     buf = np.zeros(64, np.float32)
