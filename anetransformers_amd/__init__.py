@@ -66,6 +66,19 @@ class MistralConfig(ctypes.Structure):
     ]
 
 
+class GGUFTensor(ctypes.Structure):
+    """mia_gguf_tensor (include/mia_gguf.h): GGUFTensor (gguf_loader.h:43-49) + bytes."""
+
+    _fields_ = [
+        ("name", ctypes.c_char * 256),
+        ("n_dims", ctypes.c_uint32),
+        ("ne", ctypes.c_uint64 * 4),
+        ("type", ctypes.c_uint32),
+        ("offset", ctypes.c_uint64),
+        ("bytes", ctypes.c_uint64),
+    ]
+
+
 _P = c_void_p
 _SIGS = {
     # runtime plumbing
@@ -120,6 +133,25 @@ _SIGS = {
         c_int,
         [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, _P],
     ),
+    # GGUF weight files (include/mia_gguf.h); the config struct is MistralConfig's layout
+    "mia_gguf_open": (c_int, [ctypes.c_char_p, POINTER(c_void_p)]),
+    "mia_gguf_close": (None, [_P]),
+    "mia_gguf_get_config": (c_int, [_P, POINTER(MistralConfig)]),
+    "mia_gguf_get_header": (
+        c_int,
+        [_P, POINTER(ctypes.c_uint32), POINTER(c_int), POINTER(c_int), POINTER(c_int)],
+    ),
+    "mia_gguf_n_tensors": (c_int, [_P]),
+    "mia_gguf_tensor_at": (c_int, [_P, c_int, POINTER(GGUFTensor)]),
+    "mia_gguf_find": (c_int, [_P, ctypes.c_char_p, POINTER(GGUFTensor)]),
+    "mia_gguf_host_data": (c_void_p, [_P, POINTER(GGUFTensor)]),
+    "mia_gguf_data_offset": (c_size_t, [_P]),
+    "mia_gguf_data_bytes": (c_size_t, [_P]),
+    "mia_gguf_type_block": (
+        c_int,
+        [ctypes.c_uint32, POINTER(ctypes.c_uint32), POINTER(ctypes.c_uint32)],
+    ),
+    "mia_gguf_upload": (c_int, [_P, POINTER(c_void_p), POINTER(c_size_t)]),
     # drop-in (reference signatures)
     "mia_dropin_set_abort": (None, [c_int]),
     "mia_dropin_status": (c_int, []),

@@ -271,6 +271,12 @@ int q4_impl(const void *Wq, const void *Wk, const void *Wv, const void *x_q8, co
 
 }  // namespace
 
+// Error reporting for the library's C sources (not exported).
+extern "C" __attribute__((visibility("hidden"))) int mia_internal_set_error(int code,
+                                                                            const char *msg) {
+  return set_err(code, "%s", msg);
+}
+
 extern "C" {
 
 int mia_version(void) { return 100; }

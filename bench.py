@@ -491,6 +491,44 @@ def cpu_baseline_projections(n_layers: int = 4, reps: int = 3):
                       f"rows"}
 
 
+def gguf_upload(lib, n_layers: int = 8):
+    """A GGUF file holding n_layers layers of Mistral-7B attention weights
+    (Q4_0, written to a temp dir from the format): time to open (map + parse)
+    and to upload the data section to HBM (PCIe-inclusive)."""
+    import tempfile
+
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import _gguf as GW
+
+    g = np.random.default_rng(17)
+    tensors = []
+    for l in range(n_layers):
+        for nm, rows in (("attn_q", DIM), ("attn_k", KV_DIM), ("attn_v", KV_DIM),
+                         ("attn_output", DIM)):
+            raw = g.integers(0, 256, rows * Q4_ROW_BYTES, dtype=np.uint8).tobytes()
+            tensors.append((f"blk.{l}.{nm}.weight", GW.GGML_Q4_0, (DIM, rows), raw))
+    meta = [("llama.embedding_length", GW.U32, DIM), ("llama.block_count", GW.U32, n_layers)]
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "attn.gguf")
+        GW.write(path, meta, tensors)
+        del tensors
+        h = ctypes.c_void_p()
+        t0 = time.perf_counter()
+        check(lib.mia_gguf_open(path.encode(), ctypes.byref(h)), "gguf_open")
+        t_open = time.perf_counter() - t0
+        dev, nb = ctypes.c_void_p(), ctypes.c_size_t()
+        t0 = time.perf_counter()
+        check(lib.mia_gguf_upload(h, ctypes.byref(dev), ctypes.byref(nb)), "gguf_upload")
+        t_up = time.perf_counter() - t0
+        check(lib.mia_free(dev.value), "free")
+        lib.mia_gguf_close(h.value)
+    return {"workload": f"GGUF file of {n_layers} layers x (Wq, Wk, Wv, Wo) Q4_0 at 4096 width",
+            "bytes": nb.value, "open_ms": round(t_open * 1e3, 3),
+            "upload_ms": round(t_up * 1e3, 2),
+            "upload_gbs": round(nb.value / t_up / 1e9, 2), "unit": "GB/s",
+            "path": "mapped file -> hipMemcpy in 64 MiB pieces (host pages, PCIe), wall clock"}
+
+
 def cpu_other_configs():
     """Oracle timing (same thread count as the headline baseline) on bounded
     samples of configs 1, 2 and 5."""
@@ -651,6 +689,13 @@ def main() -> int:
         }
         del pf
 
+    gguf = None
+    if not args.skip_projections:
+        log("gguf: writing and uploading an 8-layer attention-weight file")
+        gguf = gguf_upload(lib)
+        log(f"gguf: open {gguf['open_ms']:.2f} ms, upload {gguf['upload_ms']:.1f} ms "
+            f"({gguf['upload_gbs']:.1f} GB/s)")
+
     configs = None
     if not args.skip_configs and not args.skip_decode:
         log("other configs: 1 (L 513), 2 (32 x L 4097), 5 (32 x verify S 8 on a wrapped ring)")
@@ -726,6 +771,7 @@ def main() -> int:
         "prefill": prefill,
         "configs": configs,
         "projections": projections,
+        "gguf": gguf,
     }
     print(json.dumps(line), flush=True)
     return 0
