@@ -79,6 +79,13 @@ class GGUFTensor(ctypes.Structure):
     ]
 
 
+class LayerWeights(ctypes.Structure):
+    """mia_layer_weights (include/miattn.h): device pointers of one layer."""
+
+    _fields_ = [(n, c_void_p) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "rms_att",
+                                         "rms_ffn")]
+
+
 _P = c_void_p
 _SIGS = {
     # runtime plumbing
@@ -132,6 +139,13 @@ _SIGS = {
     "mia_q4_0_matvec_qkv_f32": (
         c_int,
         [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, _P],
+    ),
+    "mia_rmsnorm_f32": (c_int, [_P, _P, _P, c_int, c_int, c_float, _P]),
+    "mia_q4_0_gemm_f32": (c_int, [_P, _P, _P, c_int, c_int, c_int, _P]),
+    "mia_prefill_layer": (
+        c_int,
+        [_P, POINTER(LayerWeights), _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,
+         c_int, c_int, _P],
     ),
     # GGUF weight files (include/mia_gguf.h); the config struct is MistralConfig's layout
     "mia_gguf_open": (c_int, [ctypes.c_char_p, POINTER(c_void_p)]),

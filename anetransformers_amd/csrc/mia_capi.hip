@@ -28,11 +28,14 @@ struct DevCtx {
   size_t scratch_bytes = 0;
   void *work = nullptr;  // fp16 draft staging for mia_attention_step
   size_t work_bytes = 0;
+  void *layer_work = nullptr;  // activations of mia_prefill_layer
+  size_t layer_work_bytes = 0;
   // Opt-in kernel timing: an event pair around the main kernel of each call
-  // (kind 0 = decode kernel, 1 = flash kernel, 2 = Q4_0 matvec kernel).
+  // (kind 0 = decode kernel, 1 = flash kernel, 2 = Q4_0 matvec kernel,
+  // 3 = Q4_0 GEMM kernel).
   bool prof_on = false;
-  std::vector<hipEvent_t> prof_ev[3];
-  size_t prof_n[3] = {0, 0, 0};
+  std::vector<hipEvent_t> prof_ev[4];
+  size_t prof_n[4] = {0, 0, 0, 0};
 };
 
 DevCtx g_ctx[kMaxDevices];
@@ -94,6 +97,18 @@ int ensure_work(DevCtx *c, size_t bytes) {
     c->work_bytes = 0;
     HIP_TRY(hipMalloc(&c->work, bytes));
     c->work_bytes = bytes;
+  }
+  return MIA_OK;
+}
+
+int ensure_layer_work(DevCtx *c, size_t bytes) {
+  if (bytes > c->layer_work_bytes) {
+    HIP_TRY(hipDeviceSynchronize());
+    if (c->layer_work) HIP_TRY(hipFree(c->layer_work));
+    c->layer_work = nullptr;
+    c->layer_work_bytes = 0;
+    HIP_TRY(hipMalloc(&c->layer_work, bytes));
+    c->layer_work_bytes = bytes;
   }
   return MIA_OK;
 }
@@ -271,6 +286,40 @@ int q4_impl(const void *Wq, const void *Wk, const void *Wv, const void *x_q8, co
 
 }  // namespace
 
+// Q4_0 GEMM over up to three stacked matrices (see GemmParams).
+int gemm_impl(DevCtx *c, const void *W0, const void *W1, const void *W2, int rows0, int rows1,
+              int rows2, const float *X, int K, int S, float *y0, float *y1, float *y2, int mode,
+              hipStream_t s) {
+  mia::GemmParams p{};
+  p.A = X;
+  p.lda = K;
+  p.w0 = reinterpret_cast<const uint8_t *>(W0);
+  p.w1 = reinterpret_cast<const uint8_t *>(W1);
+  p.w2 = reinterpret_cast<const uint8_t *>(W2);
+  p.rows0 = rows0;
+  p.rows01 = rows0 + rows1;
+  p.N = rows0 + rows1 + rows2;
+  p.K = K;
+  p.S = S;
+  p.y0 = y0;
+  p.y1 = y1;
+  p.y2 = y2;
+  hipEvent_t ev0, ev1;
+  if (int rc = prof_pair(c, 3, &ev0, &ev1)) return rc;
+  HIP_TRY(mia::launch_q4_gemm(p, mode, s, ev0, ev1));
+  return MIA_OK;
+}
+
+int check_gemm_dims(int out_dim, int in_dim, int S) {
+  if (out_dim <= 0 || in_dim <= 0 || S <= 0 || in_dim % 32)
+    return set_err(MIA_ERR_INVALID, "bad sizes (out_dim=%d in_dim=%d S=%d)", out_dim, in_dim, S);
+  if (in_dim % 64)
+    return set_err(MIA_ERR_UNSUPPORTED, "in_dim %d: the GEMM needs a multiple of 64", in_dim);
+  if ((long)S * in_dim > INT_MAX || (long)S * out_dim > INT_MAX)
+    return set_err(MIA_ERR_UNSUPPORTED, "S x dim above 2^31");
+  return MIA_OK;
+}
+
 // Error reporting for the library's C sources (not exported).
 extern "C" __attribute__((visibility("hidden"))) int mia_internal_set_error(int code,
                                                                             const char *msg) {
@@ -320,13 +369,13 @@ int mia_init(int device) {
 int mia_profile_begin(void) {
   DevCtx *c;
   if (int rc = current_ctx(&c)) return rc;
-  c->prof_n[0] = c->prof_n[1] = c->prof_n[2] = 0;
+  c->prof_n[0] = c->prof_n[1] = c->prof_n[2] = c->prof_n[3] = 0;
   c->prof_on = true;
   return MIA_OK;
 }
 
 int mia_profile_end(int kind, int *count, double *total_ms) {
-  if (kind < 0 || kind > 2 || !count || !total_ms) return set_err(MIA_ERR_INVALID, "bad profile query");
+  if (kind < 0 || kind > 3 || !count || !total_ms) return set_err(MIA_ERR_INVALID, "bad profile query");
   DevCtx *c;
   if (int rc = current_ctx(&c)) return rc;
   c->prof_on = false;
@@ -609,6 +658,87 @@ int mia_commit_staged(uint16_t *k_cache, uint16_t *v_cache, const uint16_t *k_st
                              max_seq, kv_dim, pick_stream(c, stream), n_layers,
                              (size_t)max_seq * kv_dim, (size_t)S_staged * kv_dim));
   return MIA_OK;
+}
+
+int mia_rmsnorm_f32(float *out, const float *in, const float *w, int dim, int S, float eps,
+                    void *stream) {
+  if (!out || !in || !w) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (dim <= 0 || dim % 4 || S <= 0) return set_err(MIA_ERR_INVALID, "bad sizes (dim=%d S=%d)", dim, S);
+  if (int rc = check_align16(out, in, w, nullptr)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  HIP_TRY(mia::launch_rmsnorm(out, in, w, dim, S, eps, pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_q4_0_gemm_f32(const void *W, const float *X, float *Y, int out_dim, int in_dim, int S,
+                      void *stream) {
+  if (!W || !X || !Y) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (int rc = check_gemm_dims(out_dim, in_dim, S)) return rc;
+  if ((uintptr_t)W & 3) return set_err(MIA_ERR_INVALID, "W must be 4-byte aligned");
+  if (int rc = check_align16(X, Y, nullptr, nullptr)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  return gemm_impl(c, W, nullptr, nullptr, out_dim, 0, 0, X, in_dim, S, Y, nullptr, nullptr,
+                   mia::kGemmStore, pick_stream(c, stream));
+}
+
+int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_inv,
+                      uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden, int n_heads,
+                      int n_kv_heads, float eps, int max_seq, int start_pos, int S,
+                      void *stream) {
+  if (!X || !lw || !theta_inv || !k_layer || !v_layer) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (!lw->wq || !lw->wk || !lw->wv || !lw->wo || !lw->w1 || !lw->w2 || !lw->w3 || !lw->rms_att ||
+      !lw->rms_ffn)
+    return set_err(MIA_ERR_INVALID, "NULL weight pointer");
+  if (n_heads <= 0 || dim != n_heads * kHD)
+    return set_err(MIA_ERR_UNSUPPORTED, "dim %d must be n_heads x 128", dim);
+  if (int rc = check_shape(n_heads, n_kv_heads, kHD, max_seq)) return rc;
+  if (int rc = check_pos(start_pos, S)) return rc;
+  if (int rc = check_gemm_dims(hidden, dim, S)) return rc;
+  if (int rc = check_gemm_dims(dim, hidden, S)) return rc;
+  const uintptr_t wb = (uintptr_t)lw->wq | (uintptr_t)lw->wk | (uintptr_t)lw->wv |
+                       (uintptr_t)lw->wo | (uintptr_t)lw->w1 | (uintptr_t)lw->w2 |
+                       (uintptr_t)lw->w3;
+  if (wb & 3) return set_err(MIA_ERR_INVALID, "weights must be 4-byte aligned");
+  if (int rc = check_align16(X, lw->rms_att, lw->rms_ffn, k_layer)) return rc;
+  if (int rc = check_align16(v_layer, nullptr, nullptr, nullptr)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  hipStream_t s = pick_stream(c, stream);
+  const int kv_dim = n_kv_heads * kHD;
+  // Xn [S][dim] | Q [S][dim] | K, V [S][kv_dim] | A [S][dim] | G [S][hidden]
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  const size_t bd = al((size_t)S * dim * 4), bk = al((size_t)S * kv_dim * 4),
+               bh = al((size_t)S * hidden * 4);
+  if (int rc = ensure_layer_work(c, 3 * bd + 2 * bk + bh)) return rc;
+  char *w = reinterpret_cast<char *>(c->layer_work);
+  float *Xn = reinterpret_cast<float *>(w);
+  float *Q = reinterpret_cast<float *>(w + bd);
+  float *K = reinterpret_cast<float *>(w + 2 * bd);
+  float *V = reinterpret_cast<float *>(w + 2 * bd + bk);
+  float *A = reinterpret_cast<float *>(w + 2 * bd + 2 * bk);
+  float *G = reinterpret_cast<float *>(w + 3 * bd + 2 * bk);
+  // mistral_ane_prefill.h:1092-1110
+  HIP_TRY(mia::launch_rmsnorm(Xn, X, lw->rms_att, dim, S, eps, s));
+  if (int rc = gemm_impl(c, lw->wq, lw->wk, lw->wv, dim, kv_dim, kv_dim, Xn, dim, S, Q, K, V,
+                         mia::kGemmStore, s))
+    return rc;
+  if (int rc = mia_attention_step(Q, K, V, theta_inv, k_layer, v_layer, A, n_heads, n_kv_heads,
+                                  kHD, max_seq, start_pos, S, s))
+    return rc;
+  if (int rc = gemm_impl(c, lw->wo, nullptr, nullptr, dim, 0, 0, A, dim, S, X, nullptr, nullptr,
+                         mia::kGemmAdd, s))
+    return rc;
+  HIP_TRY(mia::launch_rmsnorm(Xn, X, lw->rms_ffn, dim, S, eps, s));
+  if (int rc = gemm_impl(c, lw->w1, nullptr, nullptr, hidden, 0, 0, Xn, dim, S, G, nullptr,
+                         nullptr, mia::kGemmStore, s))
+    return rc;
+  if (int rc = gemm_impl(c, lw->w3, nullptr, nullptr, hidden, 0, 0, Xn, dim, S, G, nullptr,
+                         nullptr, mia::kGemmSiluMul, s))
+    return rc;
+  return gemm_impl(c, lw->w2, nullptr, nullptr, dim, 0, 0, G, hidden, S, X, nullptr, nullptr,
+                   mia::kGemmAdd, s);
 }
 
 int mia_quantize_q8_0(const float *x, void *out_q8, int n, void *stream) {

@@ -111,4 +111,24 @@ hipError_t launch_q4_matvec(const Q4MatvecParams &p, hipStream_t s, hipEvent_t e
 hipError_t launch_scale_rows(_Float16 *base, long n_rows, int row_elems, int every, int offset,
                              float factor, hipStream_t s);
 
+// Prefill layer pieces (mia_prefill.hip).  Y[S][N] = A[S][K] . W^T with W up
+// to three Q4_0 matrices stacked as virtual rows (as Q4MatvecParams); K a
+// multiple of 64; A 16-byte aligned with lda a multiple of 4.
+enum { kGemmStore = 0, kGemmAdd = 1, kGemmSiluMul = 2 };
+struct GemmParams {
+  const float *A;
+  int lda;
+  const uint8_t *w0, *w1, *w2;
+  int rows0, rows01, N;  // rows of w0, of w0 + w1, and in all
+  int K, S;
+  // kGemmStore: y0 [S][rows0], y1 [S][rows01 - rows0], y2 [S][N - rows01];
+  // kGemmAdd: y0 [S][N] += result; kGemmSiluMul: y0 [S][N] holds the gate and
+  // becomes gate * sigmoid(gate) * result.
+  float *y0, *y1, *y2;
+};
+hipError_t launch_q4_gemm(const GemmParams &p, int mode, hipStream_t s, hipEvent_t ev0,
+                          hipEvent_t ev1);
+hipError_t launch_rmsnorm(float *out, const float *in, const float *w, int dim, int S, float eps,
+                          hipStream_t s);
+
 }  // namespace mia

@@ -64,7 +64,8 @@ int mia_event_elapsed_ms(float *ms, void *start, void *stop);
  * stamps at its start and end (kind 0: the S=1 decode kernel of
  * mia_gqa_attention / mia_decode_step / mia_attention_step with S=1; kind 1:
  * the S>1 flash kernel; kind 2: the Q4_0 matvec kernel of mia_q4_0_matvec /
- * mia_q4_0_matvec_qkv); merge, quantize and RoPE kernels are not timed.
+ * mia_q4_0_matvec_qkv; kind 3: the Q4_0 GEMM kernel of mia_q4_0_gemm_f32 /
+ * mia_prefill_layer); merge, quantize, RMSNorm and RoPE kernels are not timed.
  * mia_profile_end stops recording, synchronises and returns the number of
  * timed launches of that kind and their summed duration. */
 int mia_profile_begin(void);
@@ -191,6 +192,44 @@ int mia_q4_0_matvec_f32(const void *W, const float *x, float *y, int out_dim, in
 int mia_q4_0_matvec_qkv_f32(const void *Wq, const void *Wk, const void *Wv, const float *x,
                             float *yq, float *yk, float *yv, int dim, int kv_dim, int in_dim,
                             void *stream);
+
+/* ---- the rest of the prefill layer ---------------------------------------- */
+
+/* rmsnorm_batch (mistral/mistral_ane_prefill.h:163-175): out[t] = in[t] *
+ * (1/sqrt(mean(in[t]^2) + eps)) * w for S rows of dim fp32 (dev, 16-byte
+ * aligned, dim a multiple of 4).  out may equal in. */
+int mia_rmsnorm_f32(float *out, const float *in, const float *w, int dim, int S, float eps,
+                    void *stream);
+
+/* tiled_q4_gemm for Q4_0 weights (mistral/mistral_ane_prefill.h:1018-1042,
+ * dequantise + cblas_sgemm): Y[S][out_dim] = X[S][in_dim] . W^T, fp32 X and Y
+ * (dev, 16-byte aligned), in_dim a multiple of 64.  fp16 MFMA on X split into
+ * hi + lo halves with the block scales applied in fp32: within fp32 rounding
+ * of the reference's sums, not bit-identical to them. */
+int mia_q4_0_gemm_f32(const void *W, const float *X, float *Y, int out_dim, int in_dim, int S,
+                      void *stream);
+
+/* One layer's Q4_0 weights on the device (GGUF layout) and RMSNorm weights. */
+typedef struct {
+    const void *wq, *wk, *wv, *wo; /* attention projections */
+    const void *w1, *w2, *w3;      /* gate, down, up */
+    const float *rms_att, *rms_ffn;
+} mia_layer_weights;
+
+/* blas_prefill_layer (mistral/mistral_ane_prefill.h:1081-1110) on the GPU:
+ * X [S][dim] fp32 dev is updated in place (X += attention(...) . Wo^T, then
+ * X += SwiGLU(...) . W2^T), the layer's ring gets the S rotated fp16 K/V at
+ * slots (start_pos + t) % max_seq.  dim = n_heads * 128, hidden and dim
+ * multiples of 64.  The attention step is mia_attention_step's, i.e. the
+ * sequential semantics: the same as the reference's write-all-then-attend
+ * whenever start_pos + S <= max_seq; when a chunk wraps the ring, earlier
+ * tokens do not see later tokens' K/V in recycled slots (the reference's
+ * attention_batch does).  Activations live in a per-device work area
+ * (58 MB at S = 512). */
+int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_inv,
+                      uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden, int n_heads,
+                      int n_kv_heads, float eps, int max_seq, int start_pos, int S,
+                      void *stream);
 
 #ifdef __cplusplus
 }

@@ -69,7 +69,21 @@ _SIGS = {
     "ora_q4_0_q8_0_matvec": (None, [_P, _P, _P, c_int, c_int]),
     "ora_q4_0_q8_0_matvec_qkv": (None, [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int]),
     "ora_q4_0_q8_0_matvec_parallel": (None, [_P, _P, _P, c_int, c_int, c_int]),
+    "ora_rmsnorm_batch": (None, [_P, _P, _P, c_int, c_int, c_float]),
+    "ora_dequant_q4_0_rows": (None, [_P, _P, c_int, c_int]),
+    "ora_q4_0_gemm": (None, [_P, c_int, c_int, _P, c_int, _P, c_int]),
+    "ora_silu_mul": (None, [_P, _P, c_int]),
+    "ora_prefill_layer": (
+        None,
+        [_P, POINTER(OraKV), _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P,
+         c_int],
+    ),
 }
+
+
+class OraLayerWeights(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "rms_att",
+                                         "rms_ffn")]
 
 _libs: dict = {}
 
@@ -289,3 +303,49 @@ def dequant_q4_0(W: np.ndarray, out_dim: int, in_dim: int) -> np.ndarray:
     hi = (q >> 4) - 8
     vals = np.concatenate([lo, hi], axis=2)          # weights 0..15, then 16..31
     return (vals * d[:, :, None]).reshape(out_dim, in_dim)
+
+
+# ---- prefill layer (oracle/prefill_oracle.c) --------------------------------
+
+def rmsnorm_batch(X, w, eps=1e-5):
+    X = np.ascontiguousarray(X, np.float32)
+    S, dim = X.shape
+    out = np.empty_like(X)
+    load().ora_rmsnorm_batch(_p(out), _p(X), _p(np.ascontiguousarray(w, np.float32)), dim, S, eps)
+    return out
+
+
+def dequant_q4_0_rows(W, rows, cols):
+    out = np.empty((rows, cols), np.float32)
+    load().ora_dequant_q4_0_rows(_p(np.ascontiguousarray(W, np.uint8)), _p(out), rows, cols)
+    return out
+
+
+def q4_0_gemm(W, out_dim, in_dim, X, threads=0):
+    X = np.ascontiguousarray(X, np.float32)
+    Y = np.empty((X.shape[0], out_dim), np.float32)
+    load().ora_q4_0_gemm(_p(np.ascontiguousarray(W, np.uint8)), out_dim, in_dim, _p(X),
+                         X.shape[0], _p(Y), threads)
+    return Y
+
+
+def silu_mul(gate, up):
+    g = np.array(gate, np.float32, copy=True)
+    load().ora_silu_mul(_p(g), _p(np.ascontiguousarray(up, np.float32)), g.size)
+    return g
+
+
+def prefill_layer(W, X, kc, vc, start_pos, S, dim, hidden, n_heads, n_kv, th, eps=1e-5,
+                  threads=0):
+    """One blas_prefill_layer on copies: returns X'; kc/vc (one layer) updated.
+    W: dict of wq wk wv wo w1 w2 w3 (uint8 Q4_0 rows) and rms_att rms_ffn."""
+    hd = dim // n_heads
+    kv = make_kv(kc, vc, n_kv, hd, kc.shape[0])
+    arrs = {k: np.ascontiguousarray(v) for k, v in W.items()}
+    lw = OraLayerWeights(*[_p(arrs[n]) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3",
+                                                  "rms_att", "rms_ffn")])
+    Xo = np.array(X, np.float32, copy=True)
+    load().ora_prefill_layer(ctypes.byref(lw), ctypes.byref(kv), _p(Xo), 0, start_pos, S, dim,
+                             hidden, n_heads, n_kv, eps, _p(np.ascontiguousarray(th, np.float32)),
+                             threads)
+    return Xo

@@ -136,6 +136,24 @@ def test_staged_verify_argument_errors_without_device_work():
         lib.mia_dropin_set_abort(1)
 
 
+def test_prefill_argument_errors_without_device_work():
+    lib = mia.load()
+    buf = np.zeros(64, np.float32)
+    p = buf.ctypes.data
+    assert lib.mia_q4_0_gemm_f32(p, p, p, 64, 96, 4, None) == mia.MIA_ERR_UNSUPPORTED
+    assert lib.mia_q4_0_gemm_f32(p, p, p, 64, 100, 4, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_q4_0_gemm_f32(p, p, p, 64, 128, 0, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_q4_0_gemm_f32(p + 2, p, p, 64, 128, 4, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_rmsnorm_f32(p, p, p, 6, 1, 1e-5, None) == mia.MIA_ERR_INVALID
+    lw = mia.LayerWeights(*([p] * 9))
+    # dim must be n_heads x 128
+    assert lib.mia_prefill_layer(p, ctypes.byref(lw), p, p, p, 500, 1024, 4, 1, 1e-5, 64, 0, 4,
+                                 None) == mia.MIA_ERR_UNSUPPORTED
+    lw.w2 = None
+    assert lib.mia_prefill_layer(p, ctypes.byref(lw), p, p, p, 512, 1024, 4, 1, 1e-5, 64, 0, 4,
+                                 None) == mia.MIA_ERR_INVALID
+
+
 def test_q4_argument_errors_without_device_work():
     lib = mia.load()
     buf = np.zeros(64, np.float32)

@@ -1,0 +1,147 @@
+"""GPU parity of the prefill layer (mistral/mistral_ane_prefill.h:1081-1110)
+against the oracle (oracle/prefill_oracle.c): RMSNorm, the Q4_0 GEMM on fp32
+activations, and the whole layer (RMSNorm, QKV GEMM, RoPE + ring write +
+attention, Wo GEMM + residual, RMSNorm, gate/up GEMMs + SwiGLU, down GEMM +
+residual).
+
+Bars: RMSNorm within (log2(dim) + 8) roundings of float64 and within the
+oracle's own error bound (its sum of squares is sequential);
+GEMM rows within 2 * K * 2^-24 * sum|x||w| of the oracle (the hi + lo split of
+x is exact to 2^-22, the sums are reassociated) plus the fp16 underflow of the
+lo halves of tiny inputs; the layer normwise within 2e-3 of the oracle (the
+attention's fp16 rounding carried through Wo and the FFN), and to fp32 level
+when Wo = 0; its ring writes within one fp16 ulp (plus 1e-5 of the row's scale
+for rotated keys near zero) of the oracle's."""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import _data as D
+import _gpu as G
+import _oracle as O
+import anetransformers_amd as mia
+from anetransformers_amd import DeviceBuffer as DB
+from anetransformers_amd import check
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_gemm(W, X, out_dim, in_dim):
+    L = G.lib()
+    S = X.shape[0]
+    dw, dx, dy = DB.from_array(W), DB.from_array(np.ascontiguousarray(X, np.float32)), DB(
+        S * out_dim * 4)
+    check(L.mia_q4_0_gemm_f32(dw.ptr, dx.ptr, dy.ptr, out_dim, in_dim, S, None), "gemm")
+    check(L.mia_stream_sync(None), "sync")
+    return dy.download((S, out_dim), np.float32)
+
+
+@pytest.mark.parametrize("S,dim", [(1, 64), (7, 4096), (33, 14336)])
+def test_rmsnorm(S, dim):
+    G.say(f"prefill: rmsnorm S={S} dim={dim}")
+    L = G.lib()
+    g = np.random.default_rng(S + dim)
+    X = (g.standard_normal((S, dim)) * 2).astype(np.float32)
+    w = g.standard_normal(dim).astype(np.float32)
+    dx, dw, do = DB.from_array(X), DB.from_array(w), DB(X.nbytes)
+    check(L.mia_rmsnorm_f32(do.ptr, dx.ptr, dw.ptr, dim, S, 1e-5, None), "rmsnorm")
+    check(L.mia_stream_sync(None), "sync")
+    got = do.download(X.shape, np.float32).astype(np.float64)
+    # against float64: the GPU's tree-reduced sum of squares is good to about
+    # log2(dim) roundings, then a divide, a sqrt and two products
+    x = X.astype(np.float64)
+    exact = x / np.sqrt((x * x).mean(axis=1, keepdims=True) + 1e-5) * w
+    tight = (np.log2(dim) + 8) * 2.0 ** -24 * np.abs(exact) + 1e-30
+    assert np.all(np.abs(got - exact) <= tight)
+    # against the oracle, whose sequential fp32 sum is good to dim roundings
+    ref = O.rmsnorm_batch(X, w, 1e-5)
+    assert np.all(np.abs(got - ref) <= (dim + 8) * 2.0 ** -24 * np.abs(ref) + 1e-30)
+
+
+@pytest.mark.parametrize("S,out_dim,in_dim", [(1, 64, 64), (37, 100, 256), (128, 128, 4096),
+                                              (200, 384, 4096), (130, 64, 14336)])
+def test_gemm_matches_oracle(S, out_dim, in_dim):
+    G.say(f"prefill: q4 gemm S={S} N={out_dim} K={in_dim}")
+    g = np.random.default_rng(S * 3 + out_dim)
+    W = O.make_q4_0(g, out_dim, in_dim)
+    X = g.standard_normal((S, in_dim)).astype(np.float32)
+    X[0, :64] *= 1e-6                       # tiny values: lo halves underflow in fp16
+    got = gpu_gemm(W, X, out_dim, in_dim)
+    ref = O.q4_0_gemm(W, out_dim, in_dim, X)
+    Wd = O.dequant_q4_0(W, out_dim, in_dim)
+    mag = np.abs(X.astype(np.float64)) @ np.abs(Wd).T
+    bound = 2 * in_dim * 2.0 ** -24 * mag + in_dim * 6e-8 * np.abs(Wd).max()
+    err = np.abs(got.astype(np.float64) - ref)
+    assert np.all(err <= bound), float((err / bound).max())
+    D.check_close(got, ref, what=f"gemm {S}x{out_dim}x{in_dim}")
+
+
+def _layer(g, dim, hidden, nh, nkv):
+    kvd = dim // nh * nkv
+    return {"wq": O.make_q4_0(g, dim, dim), "wk": O.make_q4_0(g, kvd, dim),
+            "wv": O.make_q4_0(g, kvd, dim), "wo": O.make_q4_0(g, dim, dim),
+            "w1": O.make_q4_0(g, hidden, dim), "w3": O.make_q4_0(g, hidden, dim),
+            "w2": O.make_q4_0(g, dim, hidden),
+            "rms_att": (1.0 + 0.1 * g.standard_normal(dim)).astype(np.float32),
+            "rms_ffn": (1.0 + 0.1 * g.standard_normal(dim)).astype(np.float32)}
+
+
+def _zero_scales(Wq):
+    B = Wq.reshape(Wq.shape[0], -1, 18).copy()
+    B[:, :, 0:2] = 0                          # d = 0: every weight of the matrix is 0
+    return B.reshape(Wq.shape)
+
+
+@pytest.mark.parametrize("dim,hidden,nh,nkv,M,start,S,wo_zero", [
+    (512, 1024, 4, 1, 64, 10, 20, False),
+    (512, 1024, 4, 1, 64, 10, 20, True),
+    (512, 1024, 4, 1, 256, 0, 130, False),
+    (4096, 14336, 32, 8, 4096, 100, 64, False),
+    (4096, 14336, 32, 8, 4096, 100, 64, True),
+])
+def test_prefill_layer_matches_oracle(dim, hidden, nh, nkv, M, start, S, wo_zero):
+    # The attention inside the layer computes on fp16 operands and meets the
+    # attention tolerance (2e-3 / 1e-2) on its own output (tests of
+    # mia_attention_step); Wo and the FFN then carry that error into the
+    # residual stream, whose values here reach ~60.  So the whole layer is
+    # held to a normwise bar, max |gpu - oracle| <= 2e-3 * max |oracle|, and
+    # with Wo = 0 (the attention still runs and writes the ring, its output
+    # no longer reaches X) everything else must agree to fp32 level.
+    G.say(f"prefill: layer dim={dim} hidden={hidden} M={M} start={start} S={S} wo0={wo_zero}")
+    L = G.lib()
+    g = np.random.default_rng(dim + S)
+    W = _layer(g, dim, hidden, nh, nkv)
+    if wo_zero:
+        W["wo"] = _zero_scales(W["wo"])
+    kvd = dim // nh * nkv
+    kc, vc = D.ring(g, M, kv_dim=kvd, filled=start)
+    X = g.standard_normal((S, dim)).astype(np.float32)
+    th = O.theta_inv(D.THETA, 128)
+    dev = {k: DB.from_array(v) for k, v in W.items()}
+    lw = mia.LayerWeights(*[dev[n].ptr for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3",
+                                                  "rms_att", "rms_ffn")])
+    dX, dth, dkc, dvc = DB.from_array(X), DB.from_array(th), DB.from_array(kc), DB.from_array(vc)
+    check(L.mia_prefill_layer(dX.ptr, ctypes.byref(lw), dth.ptr, dkc.ptr, dvc.ptr, dim, hidden,
+                              nh, nkv, 1e-5, M, start, S, None), "prefill_layer")
+    check(L.mia_stream_sync(None), "sync")
+    got = dX.download(X.shape, np.float32)
+    kc_o, vc_o = kc.copy(), vc.copy()
+    ref = O.prefill_layer(W, X, kc_o, vc_o, start, S, dim, hidden, nh, nkv, th)
+    err = float(np.abs(got - ref).max())
+    scale = float(np.abs(ref).max())
+    assert err <= (2e-5 if wo_zero else 2e-3) * scale, (err, scale)
+    kc_g, vc_g = dkc.download(kc.shape, np.uint16), dvc.download(vc.shape, np.uint16)
+    slots = np.arange(start, start + S) % M
+    untouched = np.setdiff1d(np.arange(M), slots)
+    assert np.array_equal(kc_g[untouched], kc[untouched])
+    assert np.array_equal(vc_g[untouched], vc[untouched])
+    # new rows: one fp16 ulp, plus 1e-5 of the row's scale for the keys near
+    # zero after rotation (K and V come from the GEMM, whose fp32 sums differ
+    # from the oracle's by reassociation; RoPE's sin/cos by ulps)
+    for a, b in ((kc_g, kc_o), (vc_g, vc_o)):
+        fa, fb = D.f16_bits_to_f32(a[slots]), D.f16_bits_to_f32(b[slots])
+        ulp = np.spacing(np.maximum(np.abs(fa), np.abs(fb)).astype(np.float16)).astype(np.float32)
+        row = np.abs(fb).max(axis=1, keepdims=True)
+        assert np.all(np.abs(fa - fb) <= ulp + 1e-5 * row)
