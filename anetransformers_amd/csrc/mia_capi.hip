@@ -306,7 +306,7 @@ int gemm_impl(DevCtx *c, const void *W0, const void *W1, const void *W2, int row
   p.y2 = y2;
   hipEvent_t ev0, ev1;
   if (int rc = prof_pair(c, 3, &ev0, &ev1)) return rc;
-  HIP_TRY(mia::launch_q4_gemm(p, mode, s, ev0, ev1));
+  HIP_TRY(mia::launch_q4_gemm(p, mode, c->num_cus, s, ev0, ev1));
   return MIA_OK;
 }
 

@@ -126,8 +126,8 @@ struct GemmParams {
   // becomes gate * sigmoid(gate) * result.
   float *y0, *y1, *y2;
 };
-hipError_t launch_q4_gemm(const GemmParams &p, int mode, hipStream_t s, hipEvent_t ev0,
-                          hipEvent_t ev1);
+hipError_t launch_q4_gemm(const GemmParams &p, int mode, int num_cus, hipStream_t s,
+                          hipEvent_t ev0, hipEvent_t ev1);
 hipError_t launch_rmsnorm(float *out, const float *in, const float *w, int dim, int S, float eps,
                           hipStream_t s);
 

@@ -11,10 +11,11 @@
 //   - W's 4-bit values q - 8 are exact in fp16; the fp16 block scale d is
 //     applied in fp32 once per 32-value block: acc += d * (X . q) for the
 //     block's partial product, which is what dequantising to fp32 computes.
-// Workgroup: 256 threads, 128 tokens x 64 weight rows, 4 waves of 64 x 32;
-// each iteration stages 64 K values (two Q4_0 blocks, 36 bytes of each row,
-// 4-byte aligned because the blocks per row are even) through one LDS buffer,
-// with the next iteration's global loads in registers during the MFMAs.
+// Workgroup: 256 threads, 64 tokens x 128 weight rows, 4 waves of 32 x 64
+// (the kernel also builds for 128-token tiles); each iteration stages 64
+// K values (two Q4_0 blocks, 36 bytes of each row, 4-byte aligned because the
+// blocks per row are even) into one of two LDS stages, the global loads of
+// the next iteration in flight during the MFMAs of this one.
 #include "mia_device.h"
 #include "mia_kernels.h"
 
@@ -22,14 +23,15 @@ namespace mia {
 namespace {
 
 constexpr int kGThreads = 256;
-constexpr int kBM = 128;          // tokens per workgroup
-constexpr int kBN = 64;           // weight rows per workgroup
+constexpr int kBN = 128;          // weight rows per workgroup
 constexpr int kBK = 64;           // K values per iteration (two Q4_0 blocks)
 constexpr int kKP = kBK + 8;      // LDS row stride in halves (144 B: conflict-free b128 reads)
 
+// One LDS stage for BM tokens; the kernel keeps two.
+template <int BM>
 struct GemmLds {
-  _Float16 ahi[kBM][kKP];
-  _Float16 alo[kBM][kKP];
+  _Float16 ahi[BM][kKP];
+  _Float16 alo[BM][kKP];
   _Float16 bq[kBN][kKP];
   float bd[kBN][2];
 };
@@ -47,21 +49,26 @@ __device__ __forceinline__ unsigned nib2_to_h2(unsigned v) {
   return __builtin_bit_cast(unsigned, r);
 }
 
-template <int MODE>
+// BM = 128 or 64 tokens per workgroup; waves 2 x 2, each BM/2 tokens x 64
+// weight rows (TM x 2 MFMA tiles of 32 x 32).
+template <int MODE, int BM>
 __global__ __launch_bounds__(kGThreads) void q4_gemm_kernel(GemmParams p) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) GemmLds sm;
+  constexpr int TM = BM / 64;           // MFMA tiles per wave along the tokens
+  constexpr int ATPR = kGThreads / BM;  // threads per staged token row
+  constexpr int AF4 = kBK / ATPR / 4;   // float4 loads per thread and iteration
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  GemmLds<BM> *const sm = reinterpret_cast<GemmLds<BM> *>(smem);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kBM;
+  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * BM;
 
-  // A staging: thread -> token row ar, 32 values at column ac of the iteration
-  const int ar = tid >> 1, ac = 32 * (tid & 1);
+  // A staging: thread -> token row ar, 4 * AF4 values at column ac
+  const int ar = tid / ATPR, ac = (tid % ATPR) * 4 * AF4;
   const float *aptr = p.A + (size_t)min(m0 + ar, p.S - 1) * p.lda + ac;
   // B staging: thread -> weight row br, block bb (0, 1) of the iteration's pair
-  const int br = tid & (kBN - 1), bb = (tid >> 6) & 1;
-  const bool bload = tid < 2 * kBN;
+  const int br = tid & (kBN - 1), bb = tid / kBN;
   const uint8_t *bptr;
   {
     const int g = min(n0 + br, p.N - 1);
@@ -70,21 +77,19 @@ __global__ __launch_bounds__(kGThreads) void q4_gemm_kernel(GemmParams p) {
     bptr = base + (size_t)lr * (size_t)(p.K / 32) * 18 + 16 * bb;
   }
 
-  f4 areg[8];
+  f4 areg[AF4];
   unsigned breg[5];
   auto load = [&](int it) {
     const float *a = aptr + (size_t)it * kBK;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) areg[j] = *reinterpret_cast<const f4 *>(a + 4 * j);
-    if (bload) {
-      const uint8_t *b = bptr + (size_t)it * 36;
+    for (int j = 0; j < AF4; ++j) areg[j] = *reinterpret_cast<const f4 *>(a + 4 * j);
+    const uint8_t *b = bptr + (size_t)it * 36;
 #pragma unroll
-      for (int j = 0; j < 5; ++j) breg[j] = *reinterpret_cast<const unsigned *>(b + 4 * j);
-    }
+    for (int j = 0; j < 5; ++j) breg[j] = *reinterpret_cast<const unsigned *>(b + 4 * j);
   };
-  auto store = [&]() {
+  auto store = [&](GemmLds<BM> &st) {
 #pragma unroll
-    for (int j = 0; j < 8; j += 2) {
+    for (int j = 0; j < AF4; j += 2) {
       h8 hi, lo;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -93,109 +98,132 @@ __global__ __launch_bounds__(kGThreads) void q4_gemm_kernel(GemmParams p) {
         hi[e] = h;
         lo[e] = (_Float16)(x - (float)h);
       }
-      *reinterpret_cast<h8 *>(&sm.ahi[ar][ac + 4 * j]) = hi;
-      *reinterpret_cast<h8 *>(&sm.alo[ar][ac + 4 * j]) = lo;
+      *reinterpret_cast<h8 *>(&st.ahi[ar][ac + 4 * j]) = hi;
+      *reinterpret_cast<h8 *>(&st.alo[ar][ac + 4 * j]) = lo;
     }
-    if (bload) {
-      // bb 0: bytes 0-19 of the pair (scale 0-1, nibbles 2-17);
-      // bb 1: bytes 16-35 (scale 18-19, nibbles 20-35)
-      unsigned q[4];
-      float d;
-      if (bb == 0) {
-        d = f16_bits_f32(breg[0]);
+    // bb 0: bytes 0-19 of the pair (scale 0-1, nibbles 2-17);
+    // bb 1: bytes 16-35 (scale 18-19, nibbles 20-35)
+    unsigned q[4];
+    float d;
+    if (bb == 0) {
+      d = f16_bits_f32(breg[0]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) q[i] = __builtin_amdgcn_alignbyte(breg[i + 1], breg[i], 2);
-      } else {
-        d = f16_bits_f32(breg[0] >> 16);
+      for (int i = 0; i < 4; ++i) q[i] = __builtin_amdgcn_alignbyte(breg[i + 1], breg[i], 2);
+    } else {
+      d = f16_bits_f32(breg[0] >> 16);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) q[i] = breg[i + 1];
-      }
-      // byte j: low nibble = value j, high nibble = value j + 16
-      unsigned lo8[8], hi8[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const unsigned v = q[i], h = q[i] >> 4;
-        lo8[2 * i] = nib2_to_h2((v & 0xFu) | ((v << 8) & 0xF0000u));
-        lo8[2 * i + 1] = nib2_to_h2(((v >> 16) & 0xFu) | ((v >> 8) & 0xF0000u));
-        hi8[2 * i] = nib2_to_h2((h & 0xFu) | ((h << 8) & 0xF0000u));
-        hi8[2 * i + 1] = nib2_to_h2(((h >> 16) & 0xFu) | ((h >> 8) & 0xF0000u));
-      }
-      _Float16 *dst = &sm.bq[br][32 * bb];
-      *reinterpret_cast<u4 *>(dst) = (u4){lo8[0], lo8[1], lo8[2], lo8[3]};
-      *reinterpret_cast<u4 *>(dst + 8) = (u4){lo8[4], lo8[5], lo8[6], lo8[7]};
-      *reinterpret_cast<u4 *>(dst + 16) = (u4){hi8[0], hi8[1], hi8[2], hi8[3]};
-      *reinterpret_cast<u4 *>(dst + 24) = (u4){hi8[4], hi8[5], hi8[6], hi8[7]};
-      sm.bd[br][bb] = d;
+      for (int i = 0; i < 4; ++i) q[i] = breg[i + 1];
     }
+    // byte j: low nibble = value j, high nibble = value j + 16
+    unsigned lo8[8], hi8[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const unsigned v = q[i], h = q[i] >> 4;
+      lo8[2 * i] = nib2_to_h2((v & 0xFu) | ((v << 8) & 0xF0000u));
+      lo8[2 * i + 1] = nib2_to_h2(((v >> 16) & 0xFu) | ((v >> 8) & 0xF0000u));
+      hi8[2 * i] = nib2_to_h2((h & 0xFu) | ((h << 8) & 0xF0000u));
+      hi8[2 * i + 1] = nib2_to_h2(((h >> 16) & 0xFu) | ((h >> 8) & 0xF0000u));
+    }
+    _Float16 *dst = &st.bq[br][32 * bb];
+    *reinterpret_cast<u4 *>(dst) = (u4){lo8[0], lo8[1], lo8[2], lo8[3]};
+    *reinterpret_cast<u4 *>(dst + 8) = (u4){lo8[4], lo8[5], lo8[6], lo8[7]};
+    *reinterpret_cast<u4 *>(dst + 16) = (u4){hi8[0], hi8[1], hi8[2], hi8[3]};
+    *reinterpret_cast<u4 *>(dst + 24) = (u4){hi8[4], hi8[5], hi8[6], hi8[7]};
+    st.bd[br][bb] = d;
   };
 
-  f16v acc[2];
+  f16v acc[TM][2];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+    for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[tm][tn][i] = 0.0f;
 
-  const int n_it = p.K / kBK;
   const int col = lane & 31, half = lane >> 5;
-  load(0);
-  for (int it = 0; it < n_it; ++it) {
-    __syncthreads();  // the previous iteration's operand reads are done
-    store();
-    __syncthreads();
-    if (it + 1 < n_it) load(it + 1);
+  auto compute = [&](const GemmLds<BM> &st) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      f16v blk[2];
+      f16v blk[TM][2];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int k = 32 * kb + 16 * ks + 8 * half;
-        const h8 b = *reinterpret_cast<const h8 *>(&sm.bq[32 * wn + col][k]);
+        h8 b[2], ah[TM], al[TM];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int r = 64 * wm + 32 * t + col;
-          const h8 ah = *reinterpret_cast<const h8 *>(&sm.ahi[r][k]);
-          const h8 al = *reinterpret_cast<const h8 *>(&sm.alo[r][k]);
-          if (ks == 0) {
+        for (int tn = 0; tn < 2; ++tn)
+          b[tn] = *reinterpret_cast<const h8 *>(&st.bq[64 * wn + 32 * tn + col][k]);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) blk[t][i] = 0.0f;
-          }
-          blk[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, blk[t], 0, 0, 0);
-          blk[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, blk[t], 0, 0, 0);
+        for (int tm = 0; tm < TM; ++tm) {
+          ah[tm] = *reinterpret_cast<const h8 *>(&st.ahi[(BM / 2) * wm + 32 * tm + col][k]);
+          al[tm] = *reinterpret_cast<const h8 *>(&st.alo[(BM / 2) * wm + 32 * tm + col][k]);
         }
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int tn = 0; tn < 2; ++tn) {
+            if (ks == 0) {
+#pragma unroll
+              for (int i = 0; i < 16; ++i) blk[tm][tn][i] = 0.0f;
+            }
+            blk[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[tm], b[tn], blk[tm][tn], 0, 0, 0);
+            blk[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[tm], b[tn], blk[tm][tn], 0, 0, 0);
+          }
       }
-      const float d = sm.bd[32 * wn + col][kb];
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int tn = 0; tn < 2; ++tn) {
+        const float d = st.bd[64 * wn + 32 * tn + col][kb];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[t][i] = __builtin_fmaf(d, blk[t][i], acc[t][i]);
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            acc[tm][tn][i] = __builtin_fmaf(d, blk[tm][tn][i], acc[tm][tn][i]);
+      }
     }
+  };
+
+  // Two LDS stages: the next iteration's rows are loaded before the MFMAs of
+  // this one and stored into the other stage after them; one barrier per
+  // iteration orders both against the other waves.
+  const int n_it = p.K / kBK;
+  load(0);
+  store(sm[0]);
+  __syncthreads();
+  for (int it = 0; it < n_it; ++it) {
+    const bool more = it + 1 < n_it;
+    if (more) load(it + 1);
+    compute(sm[it & 1]);
+    if (more) store(sm[(it + 1) & 1]);
+    __syncthreads();
   }
 
   // D layout: lane holds column n = col; value i is row 8*(i/4) + 4*half + i%4.
-  const int n = n0 + 32 * wn + col;
-  if (n >= p.N) return;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int tn = 0; tn < 2; ++tn) {
+    const int n = n0 + 64 * wn + 32 * tn + col;
+    if (n >= p.N) continue;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int m = m0 + 64 * wm + 32 * t + 8 * (i >> 2) + 4 * half + (i & 3);
-      if (m >= p.S) continue;
-      const float v = acc[t][i];
-      if (MODE == kGemmStore) {
-        if (n < p.rows0)
-          p.y0[(size_t)m * p.rows0 + n] = v;
-        else if (n < p.rows01)
-          p.y1[(size_t)m * (p.rows01 - p.rows0) + (n - p.rows0)] = v;
-        else
-          p.y2[(size_t)m * (p.N - p.rows01) + (n - p.rows01)] = v;
-      } else if (MODE == kGemmAdd) {
-        float *y = p.y0 + (size_t)m * p.N + n;
-        *y = *y + v;
-      } else {  // kGemmSiluMul: y0 holds the gate; gate * sigmoid(gate) * up
-        float *y = p.y0 + (size_t)m * p.N + n;
-        const float g = *y;
-        const float sig = 1.0f / (1.0f + expf(-g));
-        *y = (g * sig) * v;
+    for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int m = m0 + (BM / 2) * wm + 32 * tm + 8 * (i >> 2) + 4 * half + (i & 3);
+        if (m >= p.S) continue;
+        const float v = acc[tm][tn][i];
+        if (MODE == kGemmStore) {
+          if (n < p.rows0)
+            p.y0[(size_t)m * p.rows0 + n] = v;
+          else if (n < p.rows01)
+            p.y1[(size_t)m * (p.rows01 - p.rows0) + (n - p.rows0)] = v;
+          else
+            p.y2[(size_t)m * (p.N - p.rows01) + (n - p.rows01)] = v;
+        } else if (MODE == kGemmAdd) {
+          float *y = p.y0 + (size_t)m * p.N + n;
+          *y = *y + v;
+        } else {  // kGemmSiluMul: y0 holds the gate; gate * sigmoid(gate) * up
+          float *y = p.y0 + (size_t)m * p.N + n;
+          const float g = *y;
+          const float sig = 1.0f / (1.0f + expf(-g));
+          *y = (g * sig) * v;
+        }
       }
     }
   }
@@ -229,19 +257,38 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *out, const float *i
   }
 }
 
+template <int MODE, int BM>
+hipError_t launch_gemm_variant(const GemmParams &p, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
+  constexpr size_t kLds = 2 * sizeof(GemmLds<BM>);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void *)q4_gemm_kernel<MODE, BM>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const dim3 grid((p.N + kBN - 1) / kBN, (p.S + BM - 1) / BM);
+  hipExtLaunchKernelGGL((q4_gemm_kernel<MODE, BM>), grid, dim3(kGThreads), kLds, s, ev0, ev1, 0, p);
+  return hipGetLastError();
+}
+
+// 64-token tiles: two workgroups per CU (164 VGPRs, 74 KB of LDS) measured
+// faster than 128-token tiles (272 VGPRs, one per CU) at every Mistral-7B
+// shape with S = 512 (W1 14336 x 4096: 219 against 303 us).
+template <int MODE>
+hipError_t launch_gemm_mode(const GemmParams &p, int num_cus, hipStream_t s, hipEvent_t ev0,
+                            hipEvent_t ev1) {
+  (void)num_cus;
+  return launch_gemm_variant<MODE, 64>(p, s, ev0, ev1);
+}
+
 }  // namespace
 
-hipError_t launch_q4_gemm(const GemmParams &p, int mode, hipStream_t s, hipEvent_t ev0,
-                          hipEvent_t ev1) {
-  const dim3 grid((p.N + kBN - 1) / kBN, (p.S + kBM - 1) / kBM);
-  if (mode == kGemmStore)
-    hipExtLaunchKernelGGL(q4_gemm_kernel<kGemmStore>, grid, dim3(kGThreads), 0, s, ev0, ev1, 0, p);
-  else if (mode == kGemmAdd)
-    hipExtLaunchKernelGGL(q4_gemm_kernel<kGemmAdd>, grid, dim3(kGThreads), 0, s, ev0, ev1, 0, p);
-  else
-    hipExtLaunchKernelGGL(q4_gemm_kernel<kGemmSiluMul>, grid, dim3(kGThreads), 0, s, ev0, ev1, 0,
-                          p);
-  return hipGetLastError();
+hipError_t launch_q4_gemm(const GemmParams &p, int mode, int num_cus, hipStream_t s,
+                          hipEvent_t ev0, hipEvent_t ev1) {
+  if (mode == kGemmStore) return launch_gemm_mode<kGemmStore>(p, num_cus, s, ev0, ev1);
+  if (mode == kGemmAdd) return launch_gemm_mode<kGemmAdd>(p, num_cus, s, ev0, ev1);
+  return launch_gemm_mode<kGemmSiluMul>(p, num_cus, s, ev0, ev1);
 }
 
 hipError_t launch_rmsnorm(float *out, const float *in, const float *w, int dim, int S, float eps,

@@ -491,6 +491,97 @@ def cpu_baseline_projections(n_layers: int = 4, reps: int = 3):
                       f"rows"}
 
 
+HIDDEN = 14336
+LAYER_GEMMS = ((QKV_ROWS, DIM), (DIM, DIM), (HIDDEN, DIM), (HIDDEN, DIM), (DIM, HIDDEN))
+LAYER_GEMM_FLOP = sum(2 * PF_S * n * k for n, k in LAYER_GEMMS)      # per layer, S = 512
+
+
+def q4_bytes(rows: int, cols: int) -> int:
+    return rows * (cols // 32) * 18
+
+
+class PrefillLayers:
+    """The whole prefill layer on the GPU (mia_prefill_layer), 32 layers with
+    their own Q4_0 weights (3.9 GB), S = 512 new tokens after 1536 cached
+    positions, the residual stream X carried from layer to layer."""
+
+    def __init__(self, lib, seed: int = 51):
+        self.lib = lib
+        g = np.random.default_rng(seed)
+        self.sizes = [("wq", DIM, DIM), ("wk", KV_DIM, DIM), ("wv", KV_DIM, DIM), ("wo", DIM, DIM),
+                      ("w1", HIDDEN, DIM), ("w2", DIM, HIDDEN), ("w3", HIDDEN, DIM)]
+        self.lw_bytes = sum(q4_bytes(r, c) for _, r, c in self.sizes)
+        self.w = DeviceBuffer(N_LAYERS * self.lw_bytes)
+        check(lib.mia_fill_normal_f16(self.w.ptr, N_LAYERS * self.lw_bytes // 2, seed, None))
+        # x 2^-12 keeps the block scales near 2.4e-4: the residual stream stays O(1)
+        check(lib.mia_scale_rows_f16(self.w.ptr, N_LAYERS * self.lw_bytes // 2048, 1024, 1, 0,
+                                     1.0 / 4096, None))
+        self.norms = DeviceBuffer.from_array(
+            (1.0 + 0.1 * g.standard_normal((N_LAYERS, 2, DIM))).astype(np.float32))
+        lay = PF_M * KV_DIM
+        self.kc = DeviceBuffer(N_LAYERS * lay * 2)
+        self.vc = DeviceBuffer(N_LAYERS * lay * 2)
+        self.kc.zero()
+        self.vc.zero()
+        for l in range(N_LAYERS):
+            check(lib.mia_fill_normal_f16(self.kc.ptr + l * lay * 2, PF_START * KV_DIM, 2000 + l, None))
+            check(lib.mia_fill_normal_f16(self.vc.ptr + l * lay * 2, PF_START * KV_DIM, 3000 + l, None))
+        self.X = DeviceBuffer.from_array(g.standard_normal((PF_S, DIM)).astype(np.float32))
+        self.th = DeviceBuffer.from_array(theta_inv())
+        self.lws = []
+        for l in range(N_LAYERS):
+            ptrs, off = {}, self.w.ptr + l * self.lw_bytes
+            for name, r, c in self.sizes:
+                ptrs[name] = off
+                off += q4_bytes(r, c)
+            nb = self.norms.ptr + l * 2 * DIM * 4
+            self.lws.append(mia.LayerWeights(ptrs["wq"], ptrs["wk"], ptrs["wv"], ptrs["wo"],
+                                             ptrs["w1"], ptrs["w2"], ptrs["w3"], nb, nb + DIM * 4))
+        check(lib.mia_device_sync())
+
+    def step(self) -> None:
+        lay = PF_M * KV_DIM * 2
+        for l in range(N_LAYERS):
+            check(self.lib.mia_prefill_layer(self.X.ptr, ctypes.byref(self.lws[l]), self.th.ptr,
+                                             self.kc.ptr + l * lay, self.vc.ptr + l * lay, DIM,
+                                             HIDDEN, N_HEADS, N_KV, 1e-5, PF_M, PF_START, PF_S,
+                                             None), "prefill_layer")
+
+
+def cpu_baseline_prefill_layer():
+    """The oracle's prefill layer (timing build, OpenMP) on 1 of the 32 layers."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import _oracle as O
+
+    g = np.random.default_rng(15)
+    W = {"wq": O.make_q4_0(g, DIM, DIM), "wk": O.make_q4_0(g, KV_DIM, DIM),
+         "wv": O.make_q4_0(g, KV_DIM, DIM), "wo": O.make_q4_0(g, DIM, DIM),
+         "w1": O.make_q4_0(g, HIDDEN, DIM), "w3": O.make_q4_0(g, HIDDEN, DIM),
+         "w2": O.make_q4_0(g, DIM, HIDDEN),
+         "rms_att": np.ones(DIM, np.float32), "rms_ffn": np.ones(DIM, np.float32)}
+    kc = np.zeros((PF_M, KV_DIM), np.uint16)
+    vc = np.zeros((PF_M, KV_DIM), np.uint16)
+    kc[:PF_START] = g.standard_normal((PF_START, KV_DIM), np.float32).astype(np.float16).view(np.uint16)
+    vc[:PF_START] = g.standard_normal((PF_START, KV_DIM), np.float32).astype(np.float16).view(np.uint16)
+    X = g.standard_normal((PF_S, DIM)).astype(np.float32)
+    threads = O.num_threads(fast=True)
+    lib = O.load(True)
+    hd = HD
+    kv = O.make_kv(kc, vc, N_KV, hd, PF_M)
+    arrs = {k: np.ascontiguousarray(v) for k, v in W.items()}
+    lw = O.OraLayerWeights(*[arrs[n].ctypes.data for n in ("wq", "wk", "wv", "wo", "w1", "w2",
+                                                              "w3", "rms_att", "rms_ffn")])
+    th = theta_inv()
+    t0 = time.perf_counter()
+    lib.ora_prefill_layer(ctypes.byref(lw), ctypes.byref(kv), X.ctypes.data, 0, PF_START, PF_S,
+                          DIM, HIDDEN, N_HEADS, N_KV, 1e-5, th.ctypes.data, threads)
+    dt = time.perf_counter() - t0
+    return {"value": round((LAYER_GEMM_FLOP + PF_FLOP_PER_LAYER) / dt / 1e12, 4),
+            "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": "1 of 32 layers (S 512 after 1536), oracle timing build: dequantised fp32 "
+                      "GEMMs and attention, OpenMP over tokens / heads"}
+
+
 def gguf_upload(lib, n_layers: int = 8):
     """A GGUF file holding n_layers layers of Mistral-7B attention weights
     (Q4_0, written to a temp dir from the format): time to open (map + parse)
@@ -591,6 +682,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-decode", action="store_true", help="prefill only (profiling)")
+    ap.add_argument("--skip-layer", action="store_true",
+                    help="skip the whole-prefill-layer line (profiling)")
     ap.add_argument("--skip-projections", action="store_true",
                     help="skip the W4A8 projection line (profiling)")
     ap.add_argument("--skip-configs", action="store_true",
@@ -696,6 +789,34 @@ def main() -> int:
         log(f"gguf: open {gguf['open_ms']:.2f} ms, upload {gguf['upload_ms']:.1f} ms "
             f"({gguf['upload_gbs']:.1f} GB/s)")
 
+    layer = None
+    if not args.skip_prefill and not args.skip_layer:
+        log("prefill layer: 32 layers x (RMSNorm, QKV, attention, Wo, RMSNorm, SwiGLU FFN), S 512")
+        pl = PrefillLayers(lib)
+        pl_steps = max(args.steps // 4, 2)
+        pl_ms = timed(lib, pl.step, pl_steps, 1)
+        g_n, g_ms = kernel_stats(lib, pl.step, pl_steps, 3)
+        gemm_tfs = (LAYER_GEMM_FLOP / 5) / (g_ms * 1e-3) / 1e12
+        layer_flop = LAYER_GEMM_FLOP + PF_FLOP_PER_LAYER
+        log(f"prefill layer: {pl_ms:.2f} ms/step ({N_LAYERS * layer_flop / (pl_ms * 1e-3) / 1e12:.1f} "
+            f"TFLOP/s), GEMM kernel {g_ms * 1e3:.1f} us avg ({gemm_tfs:.1f} TFLOP/s)")
+        layer = {
+            "workload": "prefill layer x 32 (mia_prefill_layer): RMSNorm, fused QKV GEMM, RoPE + "
+                        "ring write + flash attention, Wo GEMM + residual, RMSNorm, gate / up "
+                        "GEMMs + SwiGLU, down GEMM + residual; S 512 after 1536 cached, Q4_0 "
+                        "weights per layer (3.9 GB)",
+            "value": round(N_LAYERS * layer_flop / (pl_ms * 1e-3) / 1e12, 3),
+            "unit": "TFLOP/s", "ms_per_step": round(pl_ms, 3),
+            "flop_per_layer": layer_flop, "gemm_flop_per_layer": LAYER_GEMM_FLOP,
+            "gemm_kernel_us": round(g_ms * 1e3, 2), "gemm_launches": g_n,
+            "roofline": {"bound": "mfma", "achieved": round(gemm_tfs, 3),
+                         "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
+                         "frac": round(gemm_tfs / MFMA_F16_PEAK_TFS, 4), "traffic": None,
+                         "note": "algorithmic FLOPs of the fp32 GEMM; the kernel issues twice "
+                                 "as many fp16 MFMA FLOPs (activations split hi + lo)"},
+        }
+        del pl
+
     configs = None
     if not args.skip_configs and not args.skip_decode:
         log("other configs: 1 (L 513), 2 (32 x L 4097), 5 (32 x verify S 8 on a wrapped ring)")
@@ -733,6 +854,9 @@ def main() -> int:
         if prefill is not None:
             log("cpu baseline: prefill sample")
             prefill["cpu_baseline"] = cpu_baseline_prefill()
+        if layer is not None:
+            log("cpu baseline: prefill layer sample")
+            layer["cpu_baseline"] = cpu_baseline_prefill_layer()
         if projections is not None:
             log("cpu baseline: projections sample")
             projections["cpu_baseline"] = cpu_baseline_projections()
@@ -772,6 +896,7 @@ def main() -> int:
         "configs": configs,
         "projections": projections,
         "gguf": gguf,
+        "prefill_layer": layer,
     }
     print(json.dumps(line), flush=True)
     return 0
