@@ -14,8 +14,10 @@
 // Workgroup: 256 threads, 64 tokens x 128 weight rows, 4 waves of 32 x 64
 // (the kernel also builds for 128-token tiles); each iteration stages 64
 // K values (two Q4_0 blocks, 36 bytes of each row, 4-byte aligned because the
-// blocks per row are even) into one of two LDS stages, the global loads of
-// the next iteration in flight during the MFMAs of this one.
+// blocks per row are even) into one of two LDS stages, with the global loads
+// issued two iterations ahead of their store.
+#include <type_traits>
+
 #include "mia_device.h"
 #include "mia_kernels.h"
 
@@ -51,7 +53,11 @@ __device__ __forceinline__ unsigned nib2_to_h2(unsigned v) {
 
 // BM = 128 or 64 tokens per workgroup; waves 2 x 2, each BM/2 tokens x 64
 // weight rows (TM x 2 MFMA tiles of 32 x 32).
-template <int MODE, int BM>
+// PF: register slots of staged loads.  PF = 1 loads the next iteration just
+// before this one's MFMAs (at most 256 VGPRs: two workgroups per CU); PF = 3
+// loads two iterations further ahead (about 400 VGPRs: one workgroup per
+// CU, for grids that have no more workgroups than CUs anyway).
+template <int MODE, int BM, int PF>
 __global__ __launch_bounds__(kGThreads) void q4_gemm_kernel(GemmParams p) {
 #pragma clang fp contract(off)
   constexpr int TM = BM / 64;           // MFMA tiles per wave along the tokens
@@ -77,17 +83,24 @@ __global__ __launch_bounds__(kGThreads) void q4_gemm_kernel(GemmParams p) {
     bptr = base + (size_t)lr * (size_t)(p.K / 32) * 18 + 16 * bb;
   }
 
-  f4 areg[AF4];
-  unsigned breg[5];
-  auto load = [&](int it) {
+  // Iteration j's rows live in register slot j % PF from their load to their
+  // LDS store.
+  constexpr int kSlots = PF;
+  f4 areg_s[kSlots][AF4];
+  unsigned breg_s[kSlots][5];
+  auto load = [&](auto slot, int it) {
+    constexpr int SL = decltype(slot)::value;
     const float *a = aptr + (size_t)it * kBK;
 #pragma unroll
-    for (int j = 0; j < AF4; ++j) areg[j] = *reinterpret_cast<const f4 *>(a + 4 * j);
+    for (int j = 0; j < AF4; ++j) areg_s[SL][j] = *reinterpret_cast<const f4 *>(a + 4 * j);
     const uint8_t *b = bptr + (size_t)it * 36;
 #pragma unroll
-    for (int j = 0; j < 5; ++j) breg[j] = *reinterpret_cast<const unsigned *>(b + 4 * j);
+    for (int j = 0; j < 5; ++j) breg_s[SL][j] = *reinterpret_cast<const unsigned *>(b + 4 * j);
   };
-  auto store = [&](GemmLds<BM> &st) {
+  auto store = [&](auto slot, GemmLds<BM> &st) {
+    constexpr int SL = decltype(slot)::value;
+    const f4 *areg = areg_s[SL];
+    const unsigned *breg = breg_s[SL];
 #pragma unroll
     for (int j = 0; j < AF4; j += 2) {
       h8 hi, lo;
@@ -181,19 +194,50 @@ __global__ __launch_bounds__(kGThreads) void q4_gemm_kernel(GemmParams p) {
     }
   };
 
-  // Two LDS stages: the next iteration's rows are loaded before the MFMAs of
-  // this one and stored into the other stage after them; one barrier per
-  // iteration orders both against the other waves.
+  // Two LDS stages: iteration it computes from stage it & 1 and stores the
+  // next iteration's rows into the other stage; one barrier per iteration
+  // orders the stores and reads against the other waves.
+  using S0 = std::integral_constant<int, 0>;
   const int n_it = p.K / kBK;
-  load(0);
-  store(sm[0]);
-  __syncthreads();
-  for (int it = 0; it < n_it; ++it) {
-    const bool more = it + 1 < n_it;
-    if (more) load(it + 1);
-    compute(sm[it & 1]);
-    if (more) store(sm[(it + 1) & 1]);
+  const int last = n_it - 1;
+  if constexpr (PF == 1) {
+    load(S0{}, 0);
+    store(S0{}, sm[0]);
     __syncthreads();
+    for (int it = 0; it < n_it; ++it) {
+      const bool more = it + 1 < n_it;
+      if (more) load(S0{}, it + 1);
+      compute(sm[it & 1]);
+      if (more) store(S0{}, sm[(it + 1) & 1]);
+      __syncthreads();
+    }
+  } else {
+    // The loads of iteration it + 3 go out after the store of it + 1; loads
+    // past the end repeat the last iteration (in bounds, stored into a stage
+    // nobody reads).  Unrolled by the slot count so that the slots are
+    // registers and the waits exact.
+    static_assert(PF == 3, "three slots");
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    load(S0{}, 0);
+    load(S1{}, min(1, last));
+    load(S2{}, min(2, last));
+    store(S0{}, sm[0]);
+    __syncthreads();
+    auto step = [&](auto slot, auto next, int it) {
+      compute(sm[it & 1]);
+      store(next, sm[(it + 1) & 1]);
+      load(slot, min(it + kSlots, last));
+      __syncthreads();
+    };
+    int it = 0;
+    for (; it + kSlots <= n_it; it += kSlots) {
+      step(S0{}, S1{}, it);
+      step(S1{}, S2{}, it + 1);
+      step(S2{}, S0{}, it + 2);
+    }
+    if (it < n_it) step(S0{}, S1{}, it);
+    if (it + 1 < n_it) step(S1{}, S2{}, it + 1);
   }
 
   // D layout: lane holds column n = col; value i is row 8*(i/4) + 4*half + i%4.
@@ -257,29 +301,33 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *out, const float *i
   }
 }
 
-template <int MODE, int BM>
+template <int MODE, int BM, int PF>
 hipError_t launch_gemm_variant(const GemmParams &p, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   constexpr size_t kLds = 2 * sizeof(GemmLds<BM>);
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void *)q4_gemm_kernel<MODE, BM>,
+    hipError_t e = hipFuncSetAttribute((const void *)q4_gemm_kernel<MODE, BM, PF>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   const dim3 grid((p.N + kBN - 1) / kBN, (p.S + BM - 1) / BM);
-  hipExtLaunchKernelGGL((q4_gemm_kernel<MODE, BM>), grid, dim3(kGThreads), kLds, s, ev0, ev1, 0, p);
+  hipExtLaunchKernelGGL((q4_gemm_kernel<MODE, BM, PF>), grid, dim3(kGThreads), kLds, s, ev0, ev1,
+                        0, p);
   return hipGetLastError();
 }
 
-// 64-token tiles: two workgroups per CU (164 VGPRs, 74 KB of LDS) measured
-// faster than 128-token tiles (272 VGPRs, one per CU) at every Mistral-7B
-// shape with S = 512 (W1 14336 x 4096: 219 against 303 us).
+// 64-token tiles (74 KB of LDS per workgroup).  Grids with more workgroups
+// than CUs keep two per CU with PF = 1; grids of at most one per CU use the
+// deeper prefetch.  Measured at S = 512 (PF 1 / PF 3): W1 14336 x 4096 222 /
+// 221 us, QKV 6144 x 4096 106 / 137, Wo 4096 x 4096 88 / 72, W2 4096 x 14336
+// 312 / 245.
 template <int MODE>
 hipError_t launch_gemm_mode(const GemmParams &p, int num_cus, hipStream_t s, hipEvent_t ev0,
                             hipEvent_t ev1) {
-  (void)num_cus;
-  return launch_gemm_variant<MODE, 64>(p, s, ev0, ev1);
+  const long wgs = (long)((p.N + kBN - 1) / kBN) * ((p.S + 63) / 64);
+  if (wgs > num_cus) return launch_gemm_variant<MODE, 64, 1>(p, s, ev0, ev1);
+  return launch_gemm_variant<MODE, 64, 3>(p, s, ev0, ev1);
 }
 
 }  // namespace
