@@ -361,6 +361,8 @@ int mia_init(int device) {
     return set_err(MIA_ERR_UNSUPPORTED, "device %d is %s; libmiattn is built for gfx950", device,
                    prop.gcnArchName);
   c.num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+  HIP_TRY(mia::prepare_flash());
+  HIP_TRY(mia::prepare_gemm());
   HIP_TRY(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
   c.ready = true;
   return MIA_OK;

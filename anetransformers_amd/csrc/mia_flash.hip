@@ -931,15 +931,14 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(FlashParams p, int rt)
 }
 
 template <int NB>
+hipError_t set_lds_limit() {
+  return hipFuncSetAttribute((const void *)flash_kernel<NB>,
+                             hipFuncAttributeMaxDynamicSharedMemorySize, Lay<NB>::kBytes);
+}
+
+template <int NB>
 hipError_t launch_variant(const FlashParams &p, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   using L = Lay<NB>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void *)flash_kernel<NB>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
   dim3 grid(p.n_kv * p.n_rtiles * p.nsplit);
   hipExtLaunchKernelGGL((flash_kernel<NB>), grid, dim3(256), L::kBytes, s, ev0, ev1, 0, p);
   return hipGetLastError();
@@ -948,6 +947,11 @@ hipError_t launch_variant(const FlashParams &p, hipStream_t s, hipEvent_t ev0, h
 int rows_per_tile(int S) { return S * 4 <= 32 ? 32 : 64; }
 
 }  // namespace
+
+hipError_t prepare_flash() {
+  hipError_t e = set_lds_limit<1>();
+  return e != hipSuccess ? e : set_lds_limit<2>();
+}
 
 size_t flash_scratch_bytes(int n_kv, int n_rtiles, int nsplit, int rows_per_tile) {
   return (size_t)n_kv * n_rtiles * nsplit * rows_per_tile * (HD + 2) * sizeof(float);

@@ -8,6 +8,11 @@
 
 namespace mia {
 
+// Per-device set-up, called by mia_init with the device current: raises the
+// dynamic LDS limit of the kernels that use more than 64 KB.
+hipError_t prepare_flash();
+hipError_t prepare_gemm();
+
 // S=1 split-K flash-decode over the fp16 sequence-major ring of one layer.
 struct DecodeParams {
   const float *q;          // [n_kv*G][128] fp32: raw (fused) or already rotated

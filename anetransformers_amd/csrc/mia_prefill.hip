@@ -302,15 +302,15 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *out, const float *i
 }
 
 template <int MODE, int BM, int PF>
+hipError_t set_lds_limit() {
+  return hipFuncSetAttribute((const void *)q4_gemm_kernel<MODE, BM, PF>,
+                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)(2 * sizeof(GemmLds<BM>)));
+}
+
+template <int MODE, int BM, int PF>
 hipError_t launch_gemm_variant(const GemmParams &p, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   constexpr size_t kLds = 2 * sizeof(GemmLds<BM>);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void *)q4_gemm_kernel<MODE, BM, PF>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
   const dim3 grid((p.N + kBN - 1) / kBN, (p.S + BM - 1) / BM);
   hipExtLaunchKernelGGL((q4_gemm_kernel<MODE, BM, PF>), grid, dim3(kGThreads), kLds, s, ev0, ev1,
                         0, p);
@@ -331,6 +331,16 @@ hipError_t launch_gemm_mode(const GemmParams &p, int num_cus, hipStream_t s, hip
 }
 
 }  // namespace
+
+hipError_t prepare_gemm() {
+  const hipError_t e[] = {
+      set_lds_limit<kGemmStore, 64, 1>(),   set_lds_limit<kGemmStore, 64, 3>(),
+      set_lds_limit<kGemmAdd, 64, 1>(),     set_lds_limit<kGemmAdd, 64, 3>(),
+      set_lds_limit<kGemmSiluMul, 64, 1>(), set_lds_limit<kGemmSiluMul, 64, 3>()};
+  for (hipError_t x : e)
+    if (x != hipSuccess) return x;
+  return hipSuccess;
+}
 
 hipError_t launch_q4_gemm(const GemmParams &p, int mode, int num_cus, hipStream_t s,
                           hipEvent_t ev0, hipEvent_t ev1) {
