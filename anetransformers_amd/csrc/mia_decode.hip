@@ -345,29 +345,35 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
     *reinterpret_cast<float2 *>(p.part_ml + row * 2) = make_float2(m_lane, l_part);
 }
 
-// Cross-chunk log-sum-exp merge.  Workgroup = (kv head, q head, 32-dim
-// block); thread = (chunk group cg of 8, dim d).  Every load (the chunk
+// Cross-chunk log-sum-exp merge.  Workgroup = (kv head, q head, block of
+// kMergeDims dims); thread = (chunk group cg, dim d).  Every load (the chunk
 // maxima and sums, and the thread's partial outputs) is issued before the
 // first reduction, so the merge costs one memory round trip.  A separate
 // launch: the kernel boundary orders the partial writes before these reads.
+// 16 dims per workgroup (256 workgroups for 8 kv heads) measured 1.6 %
+// faster per decode step than 32 (128 workgroups) and than 8 (512).
+constexpr int kMergeDims = 16;
+
 __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
-  constexpr int kPer = kMaxChunks / 8;  // chunks per thread at most
+  constexpr int kDW = kMergeDims;      // dims of one workgroup
+  constexpr int kCG = 256 / kDW;       // chunk groups (threads per dim)
+  constexpr int kPer = kMaxChunks / kCG;  // chunks per thread at most
   __shared__ float mx[8];
-  __shared__ float red[8][32];
+  __shared__ float red[kCG][kDW];
   __shared__ float wt[kMaxChunks];
   __shared__ float lsum[8];
-  const int db = blockIdx.x % 4;
-  const int hg = blockIdx.x / 4;  // kvh * G + g
+  const int db = blockIdx.x % (HD / kDW);
+  const int hg = blockIdx.x / (HD / kDW);  // kvh * G + g
   const int kvh = hg / G, g = hg % G;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int cg = tid >> 5, d = 32 * db + (tid & 31);
+  const int cg = tid / kDW, d = kDW * db + (tid % kDW);
   const size_t hb = (size_t)kvh * p.nchunk * G;
   float2 ml = make_float2(-INFINITY, 0.f);
   if (tid < p.nchunk) ml = *reinterpret_cast<const float2 *>(p.part_ml + (hb + (size_t)tid * G + g) * 2);
   float ov[kPer];
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
-    const int c = cg + 8 * k;
+    const int c = cg + kCG * k;
     ov[k] = c < p.nchunk ? p.part_o[(hb + (size_t)c * G + g) * HD + d] : 0.f;
   }
   // max over chunks
@@ -386,15 +392,15 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
   float O = 0.f;
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
-    const int c = cg + 8 * k;
+    const int c = cg + kCG * k;
     if (c < p.nchunk) O = __builtin_fmaf(wt[c], ov[k], O);
   }
-  red[cg][tid & 31] = O;
+  red[cg][tid % kDW] = O;
   __syncthreads();
-  if (tid < 32) {
+  if (tid < kDW) {
     float t = 0.f;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) t += red[k][tid];
+    for (int k = 0; k < kCG; ++k) t += red[k][tid];
     const float Ls = lsum[0] + lsum[1] + lsum[2] + lsum[3];
     p.out[(size_t)hg * HD + d] = t / Ls;
   }
@@ -430,7 +436,7 @@ hipError_t launch_decode(const DecodeParams &p, int g, bool fused, hipStream_t s
 }
 
 hipError_t launch_decode_merge(const DecodeParams &p, hipStream_t s) {
-  if (p.nchunk > 1) hipLaunchKernelGGL(decode_merge_kernel, dim3(p.n_kv * G * 4), dim3(256), 0, s, p);
+  if (p.nchunk > 1) hipLaunchKernelGGL(decode_merge_kernel, dim3(p.n_kv * G * (HD / kMergeDims)), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
