@@ -12,6 +12,8 @@
 
 #include "../../include/mia_dropin.h"
 
+int mia_internal_set_error(int code, const char *msg); /* mia_capi.hip, not exported */
+
 static int g_abort = 1;
 static __thread int g_status = 0;
 static char *g_dbuf = NULL;
@@ -219,7 +221,7 @@ static int stage_for(KVCache *kv, int start_pos, int S) {
             g_stage_bytes = need;
         }
         unsigned char *done = (unsigned char *)realloc(g_stage_done, (size_t)kv->n_layers);
-        if (!done) return MIA_ERR_INVALID;
+        if (!done) return mia_internal_set_error(MIA_ERR_INVALID, "out of host memory");
         g_stage_done = done;
         memset(g_stage_done, 0, (size_t)kv->n_layers);
         g_stage_start = start_pos;
