@@ -53,13 +53,14 @@ __device__ __forceinline__ unsigned nib2_to_h2(unsigned v) {
 
 // BM = 128 or 64 tokens per workgroup; waves 2 x 2, each BM/2 tokens x 64
 // weight rows (TM x 2 MFMA tiles of 32 x 32).
-// PF: register slots of staged loads.  PF = 1 loads the next iteration just
-// before this one's MFMAs (at most 256 VGPRs: two workgroups per CU); PF = 3
-// loads two iterations further ahead (about 400 VGPRs: one workgroup per
-// CU, for grids that have no more workgroups than CUs anyway).
+// PF: register slots of staged loads, loaded PF - 1 iterations before they
+// are stored.  PF = 2 fits 256 VGPRs (two workgroups per CU); PF = 3 takes
+// about 400 (one workgroup per CU, for grids that have no more workgroups
+// than CUs anyway).
 template <int MODE, int BM, int PF>
-__global__ __launch_bounds__(kGThreads) void q4_gemm_kernel(GemmParams p) {
+__global__ __launch_bounds__(kGThreads, PF == 3 ? 1 : 2) void q4_gemm_kernel(GemmParams p) {
 #pragma clang fp contract(off)
+  static_assert(PF == 2 || PF == 3, "two or three register slots");
   constexpr int TM = BM / 64;           // MFMA tiles per wave along the tokens
   constexpr int ATPR = kGThreads / BM;  // threads per staged token row
   constexpr int AF4 = kBK / ATPR / 4;   // float4 loads per thread and iteration
@@ -200,37 +201,28 @@ __global__ __launch_bounds__(kGThreads) void q4_gemm_kernel(GemmParams p) {
   using S0 = std::integral_constant<int, 0>;
   const int n_it = p.K / kBK;
   const int last = n_it - 1;
-  if constexpr (PF == 1) {
-    load(S0{}, 0);
-    store(S0{}, sm[0]);
+  // The loads of iteration it + PF go out after the store of it + 1; loads
+  // past the end repeat the last iteration (in bounds, stored into a stage
+  // nobody reads).  Unrolled by the slot count so that the slots are
+  // registers and the waits exact; the scheduling fence after each step
+  // keeps the steps from being interleaved (which would need more VGPRs
+  // than two workgroups per CU leave).
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, PF == 3 ? 2 : 0>;
+  load(S0{}, 0);
+  load(S1{}, min(1, last));
+  if constexpr (PF == 3) load(S2{}, min(2, last));
+  store(S0{}, sm[0]);
+  __syncthreads();
+  auto step = [&](auto slot, auto next, int it) {
+    compute(sm[it & 1]);
+    store(next, sm[(it + 1) & 1]);
+    load(slot, min(it + kSlots, last));
     __syncthreads();
-    for (int it = 0; it < n_it; ++it) {
-      const bool more = it + 1 < n_it;
-      if (more) load(S0{}, it + 1);
-      compute(sm[it & 1]);
-      if (more) store(S0{}, sm[(it + 1) & 1]);
-      __syncthreads();
-    }
-  } else {
-    // The loads of iteration it + 3 go out after the store of it + 1; loads
-    // past the end repeat the last iteration (in bounds, stored into a stage
-    // nobody reads).  Unrolled by the slot count so that the slots are
-    // registers and the waits exact.
-    static_assert(PF == 3, "three slots");
-    using S1 = std::integral_constant<int, 1>;
-    using S2 = std::integral_constant<int, 2>;
-    load(S0{}, 0);
-    load(S1{}, min(1, last));
-    load(S2{}, min(2, last));
-    store(S0{}, sm[0]);
-    __syncthreads();
-    auto step = [&](auto slot, auto next, int it) {
-      compute(sm[it & 1]);
-      store(next, sm[(it + 1) & 1]);
-      load(slot, min(it + kSlots, last));
-      __syncthreads();
-    };
-    int it = 0;
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int it = 0;
+  if constexpr (PF == 3) {
     for (; it + kSlots <= n_it; it += kSlots) {
       step(S0{}, S1{}, it);
       step(S1{}, S2{}, it + 1);
@@ -238,6 +230,12 @@ __global__ __launch_bounds__(kGThreads) void q4_gemm_kernel(GemmParams p) {
     }
     if (it < n_it) step(S0{}, S1{}, it);
     if (it + 1 < n_it) step(S1{}, S2{}, it + 1);
+  } else {
+    for (; it + kSlots <= n_it; it += kSlots) {
+      step(S0{}, S1{}, it);
+      step(S1{}, S0{}, it + 1);
+    }
+    if (it < n_it) step(S0{}, S1{}, it);
   }
 
   // D layout: lane holds column n = col; value i is row 8*(i/4) + 4*half + i%4.
@@ -318,15 +316,15 @@ hipError_t launch_gemm_variant(const GemmParams &p, hipStream_t s, hipEvent_t ev
 }
 
 // 64-token tiles (74 KB of LDS per workgroup).  Grids with more workgroups
-// than CUs keep two per CU with PF = 1; grids of at most one per CU use the
-// deeper prefetch.  Measured at S = 512 (PF 1 / PF 3): W1 14336 x 4096 222 /
-// 221 us, QKV 6144 x 4096 106 / 137, Wo 4096 x 4096 88 / 72, W2 4096 x 14336
-// 312 / 245.
+// than CUs keep two per CU with PF = 2; grids of at most one per CU use
+// PF = 3.  Measured at S = 512 (PF 1 / 2 / 3): W1 14336 x 4096 222 / 189 /
+// 286 us, QKV 6144 x 4096 106 / 92 / 137, Wo 4096 x 4096 88 / - / 72,
+// W2 4096 x 14336 312 / - / 242.
 template <int MODE>
 hipError_t launch_gemm_mode(const GemmParams &p, int num_cus, hipStream_t s, hipEvent_t ev0,
                             hipEvent_t ev1) {
   const long wgs = (long)((p.N + kBN - 1) / kBN) * ((p.S + 63) / 64);
-  if (wgs > num_cus) return launch_gemm_variant<MODE, 64, 1>(p, s, ev0, ev1);
+  if (wgs > num_cus) return launch_gemm_variant<MODE, 64, 2>(p, s, ev0, ev1);
   return launch_gemm_variant<MODE, 64, 3>(p, s, ev0, ev1);
 }
 
@@ -334,9 +332,9 @@ hipError_t launch_gemm_mode(const GemmParams &p, int num_cus, hipStream_t s, hip
 
 hipError_t prepare_gemm() {
   const hipError_t e[] = {
-      set_lds_limit<kGemmStore, 64, 1>(),   set_lds_limit<kGemmStore, 64, 3>(),
-      set_lds_limit<kGemmAdd, 64, 1>(),     set_lds_limit<kGemmAdd, 64, 3>(),
-      set_lds_limit<kGemmSiluMul, 64, 1>(), set_lds_limit<kGemmSiluMul, 64, 3>()};
+      set_lds_limit<kGemmStore, 64, 2>(),   set_lds_limit<kGemmStore, 64, 3>(),
+      set_lds_limit<kGemmAdd, 64, 2>(),     set_lds_limit<kGemmAdd, 64, 3>(),
+      set_lds_limit<kGemmSiluMul, 64, 2>(), set_lds_limit<kGemmSiluMul, 64, 3>()};
   for (hipError_t x : e)
     if (x != hipSuccess) return x;
   return hipSuccess;
