@@ -30,6 +30,8 @@ struct DevCtx {
   size_t work_bytes = 0;
   void *layer_work = nullptr;  // activations of mia_prefill_layer
   size_t layer_work_bytes = 0;
+  void *gemm_work = nullptr;  // split-K partial products of the Q4_0 GEMM
+  size_t gemm_work_bytes = 0;
   // Opt-in kernel timing: an event pair around the main kernel of each call
   // (kind 0 = decode kernel, 1 = flash kernel, 2 = Q4_0 matvec kernel,
   // 3 = Q4_0 GEMM kernel).
@@ -109,6 +111,18 @@ int ensure_layer_work(DevCtx *c, size_t bytes) {
     c->layer_work_bytes = 0;
     HIP_TRY(hipMalloc(&c->layer_work, bytes));
     c->layer_work_bytes = bytes;
+  }
+  return MIA_OK;
+}
+
+int ensure_gemm_work(DevCtx *c, size_t bytes) {
+  if (bytes > c->gemm_work_bytes) {
+    HIP_TRY(hipDeviceSynchronize());
+    if (c->gemm_work) HIP_TRY(hipFree(c->gemm_work));
+    c->gemm_work = nullptr;
+    c->gemm_work_bytes = 0;
+    HIP_TRY(hipMalloc(&c->gemm_work, bytes));
+    c->gemm_work_bytes = bytes;
   }
   return MIA_OK;
 }
@@ -304,6 +318,11 @@ int gemm_impl(DevCtx *c, const void *W0, const void *W1, const void *W2, int row
   p.y0 = y0;
   p.y1 = y1;
   p.y2 = y2;
+  p.ksplit = mia::gemm_pick_ksplit(p.N, K, S, c->num_cus);
+  if (p.ksplit > 1) {
+    if (int rc = ensure_gemm_work(c, (size_t)p.ksplit * S * p.N * sizeof(float))) return rc;
+    p.part = reinterpret_cast<float *>(c->gemm_work);
+  }
   hipEvent_t ev0, ev1;
   if (int rc = prof_pair(c, 3, &ev0, &ev1)) return rc;
   HIP_TRY(mia::launch_q4_gemm(p, mode, c->num_cus, s, ev0, ev1));

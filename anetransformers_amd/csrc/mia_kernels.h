@@ -130,7 +130,14 @@ struct GemmParams {
   // kGemmAdd: y0 [S][N] += result; kGemmSiluMul: y0 [S][N] holds the gate and
   // becomes gate * sigmoid(gate) * result.
   float *y0, *y1, *y2;
+  // K split over blockIdx.z (1: none).  With ksplit > 1 the partial products
+  // go to part [ksplit][S][N] and a second kernel sums them in split order
+  // and applies the epilogue.
+  int ksplit;
+  float *part;
 };
+long gemm_tiles(int N, int S);
+int gemm_pick_ksplit(int N, int K, int S, int num_cus);
 hipError_t launch_q4_gemm(const GemmParams &p, int mode, int num_cus, hipStream_t s,
                           hipEvent_t ev0, hipEvent_t ev1);
 hipError_t launch_rmsnorm(float *out, const float *in, const float *w, int dim, int S, float eps,

@@ -51,6 +51,27 @@ __device__ __forceinline__ unsigned nib2_to_h2(unsigned v) {
   return __builtin_bit_cast(unsigned, r);
 }
 
+// The epilogue of element (m, n) of the product, v.
+template <int MODE>
+__device__ __forceinline__ void gemm_epilogue(const GemmParams &p, int m, int n, float v) {
+  if (MODE == kGemmStore) {
+    if (n < p.rows0)
+      p.y0[(size_t)m * p.rows0 + n] = v;
+    else if (n < p.rows01)
+      p.y1[(size_t)m * (p.rows01 - p.rows0) + (n - p.rows0)] = v;
+    else
+      p.y2[(size_t)m * (p.N - p.rows01) + (n - p.rows01)] = v;
+  } else if (MODE == kGemmAdd) {
+    float *y = p.y0 + (size_t)m * p.N + n;
+    *y = *y + v;
+  } else {  // kGemmSiluMul: y0 holds the gate; gate * sigmoid(gate) * up
+    float *y = p.y0 + (size_t)m * p.N + n;
+    const float g = *y;
+    const float sig = 1.0f / (1.0f + expf(-g));
+    *y = (g * sig) * v;
+  }
+}
+
 // BM = 128 or 64 tokens per workgroup; waves 2 x 2, each BM/2 tokens x 64
 // weight rows (TM x 2 MFMA tiles of 32 x 32).
 // PF: register slots of staged loads, loaded PF - 1 iterations before they
@@ -199,8 +220,12 @@ __global__ __launch_bounds__(kGThreads, PF == 3 ? 1 : 2) void q4_gemm_kernel(Gem
   // next iteration's rows into the other stage; one barrier per iteration
   // orders the stores and reads against the other waves.
   using S0 = std::integral_constant<int, 0>;
-  const int n_it = p.K / kBK;
-  const int last = n_it - 1;
+  // K range of this workgroup: all of it, or split blockIdx.z of p.ksplit
+  // (the partial products then go to p.part and gemm_reduce_kernel sums them)
+  const int n_all = p.K / kBK;
+  const int it0 = (int)((long)n_all * blockIdx.z / p.ksplit);
+  const int n_it = (int)((long)n_all * (blockIdx.z + 1) / p.ksplit) - it0;
+  const int last = it0 + n_it - 1;
   // The loads of iteration it + PF go out after the store of it + 1; loads
   // past the end repeat the last iteration (in bounds, stored into a stage
   // nobody reads).  Unrolled by the slot count so that the slots are
@@ -209,15 +234,17 @@ __global__ __launch_bounds__(kGThreads, PF == 3 ? 1 : 2) void q4_gemm_kernel(Gem
   // than two workgroups per CU leave).
   using S1 = std::integral_constant<int, 1>;
   using S2 = std::integral_constant<int, PF == 3 ? 2 : 0>;
-  load(S0{}, 0);
-  load(S1{}, min(1, last));
-  if constexpr (PF == 3) load(S2{}, min(2, last));
+  load(S0{}, it0);
+  load(S1{}, min(it0 + 1, last));
+  if constexpr (PF == 3) load(S2{}, min(it0 + 2, last));
   store(S0{}, sm[0]);
   __syncthreads();
+  // it counts from 0 within the range (stage parity and slot), it0 + it is
+  // the absolute iteration
   auto step = [&](auto slot, auto next, int it) {
     compute(sm[it & 1]);
     store(next, sm[(it + 1) & 1]);
-    load(slot, min(it + kSlots, last));
+    load(slot, min(it0 + it + kSlots, last));
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -249,25 +276,23 @@ __global__ __launch_bounds__(kGThreads, PF == 3 ? 1 : 2) void q4_gemm_kernel(Gem
       for (int i = 0; i < 16; ++i) {
         const int m = m0 + (BM / 2) * wm + 32 * tm + 8 * (i >> 2) + 4 * half + (i & 3);
         if (m >= p.S) continue;
-        const float v = acc[tm][tn][i];
-        if (MODE == kGemmStore) {
-          if (n < p.rows0)
-            p.y0[(size_t)m * p.rows0 + n] = v;
-          else if (n < p.rows01)
-            p.y1[(size_t)m * (p.rows01 - p.rows0) + (n - p.rows0)] = v;
-          else
-            p.y2[(size_t)m * (p.N - p.rows01) + (n - p.rows01)] = v;
-        } else if (MODE == kGemmAdd) {
-          float *y = p.y0 + (size_t)m * p.N + n;
-          *y = *y + v;
-        } else {  // kGemmSiluMul: y0 holds the gate; gate * sigmoid(gate) * up
-          float *y = p.y0 + (size_t)m * p.N + n;
-          const float g = *y;
-          const float sig = 1.0f / (1.0f + expf(-g));
-          *y = (g * sig) * v;
-        }
+        if (p.ksplit > 1)
+          p.part[((size_t)blockIdx.z * p.S + m) * p.N + n] = acc[tm][tn][i];
+        else
+          gemm_epilogue<MODE>(p, m, n, acc[tm][tn][i]);
       }
     }
+  }
+}
+
+// Sum of the split partial products in split order, then the epilogue.
+template <int MODE>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
+  const size_t total = (size_t)p.S * p.N;
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (size_t)gridDim.x * 256) {
+    float v = p.part[e];
+    for (int z = 1; z < p.ksplit; ++z) v += p.part[(size_t)z * total + e];
+    gemm_epilogue<MODE>(p, (int)(e / p.N), (int)(e % p.N), v);
   }
 }
 
@@ -309,9 +334,14 @@ hipError_t set_lds_limit() {
 template <int MODE, int BM, int PF>
 hipError_t launch_gemm_variant(const GemmParams &p, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   constexpr size_t kLds = 2 * sizeof(GemmLds<BM>);
-  const dim3 grid((p.N + kBN - 1) / kBN, (p.S + BM - 1) / BM);
+  const dim3 grid((p.N + kBN - 1) / kBN, (p.S + BM - 1) / BM, p.ksplit);
   hipExtLaunchKernelGGL((q4_gemm_kernel<MODE, BM, PF>), grid, dim3(kGThreads), kLds, s, ev0, ev1,
                         0, p);
+  if (p.ksplit > 1) {
+    const size_t total = (size_t)p.S * p.N;
+    const unsigned blocks = (unsigned)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+    hipLaunchKernelGGL(gemm_reduce_kernel<MODE>, dim3(blocks), dim3(256), 0, s, p);
+  }
   return hipGetLastError();
 }
 
@@ -323,12 +353,20 @@ hipError_t launch_gemm_variant(const GemmParams &p, hipStream_t s, hipEvent_t ev
 template <int MODE>
 hipError_t launch_gemm_mode(const GemmParams &p, int num_cus, hipStream_t s, hipEvent_t ev0,
                             hipEvent_t ev1) {
-  const long wgs = (long)((p.N + kBN - 1) / kBN) * ((p.S + 63) / 64);
-  if (wgs > num_cus) return launch_gemm_variant<MODE, 64, 2>(p, s, ev0, ev1);
+  if (p.ksplit > 1 || gemm_tiles(p.N, p.S) > num_cus)
+    return launch_gemm_variant<MODE, 64, 2>(p, s, ev0, ev1);
   return launch_gemm_variant<MODE, 64, 3>(p, s, ev0, ev1);
 }
 
 }  // namespace
+
+long gemm_tiles(int N, int S) { return (long)((N + kBN - 1) / kBN) * ((S + 63) / 64); }
+
+int gemm_pick_ksplit(int N, int K, int S, int num_cus) {
+  // Grids of at most one workgroup per CU with a long K: two K halves give
+  // two workgroups per CU (the narrow Wo and W2 shapes of a prefill chunk).
+  return gemm_tiles(N, S) <= num_cus && K / kBK >= 16 ? 2 : 1;
+}
 
 hipError_t prepare_gemm() {
   const hipError_t e[] = {

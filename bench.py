@@ -813,7 +813,9 @@ def main() -> int:
                          "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
                          "frac": round(gemm_tfs / MFMA_F16_PEAK_TFS, 4), "traffic": None,
                          "note": "algorithmic FLOPs of the fp32 GEMM; the kernel issues twice "
-                                 "as many fp16 MFMA FLOPs (activations split hi + lo)"},
+                                 "as many fp16 MFMA FLOPs (activations split hi + lo); the "
+                                 "split-K sum kernel of Wo and W2 is in ms_per_step, not in "
+                                 "the GEMM kernel average"},
         }
         del pl
 
