@@ -693,8 +693,9 @@ def main() -> int:
                          "size, to scale HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only: the attention path has no "
-                          "multi-GPU mode (see DESIGN.md for how it would shard)",
+        print(json.dumps({"error": "one GPU only: the attention path has no multi-GPU mode "
+                          "(it would shard by kv head, each GPU running these kernels on "
+                          "its heads' slice of the ring)",
                           "n_gpus": args.gpus}))
         return 2
 
