@@ -812,7 +812,8 @@ def main() -> int:
             "gemm_kernel_us": round(g_ms * 1e3, 2), "gemm_launches": g_n,
             "roofline": {"bound": "mfma", "achieved": round(gemm_tfs, 3),
                          "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
-                         "frac": round(gemm_tfs / MFMA_F16_PEAK_TFS, 4), "traffic": None,
+                         "frac": round(gemm_tfs / MFMA_F16_PEAK_TFS, 4),
+                         "traffic": load_traffic("q4_gemm_prefill"),
                          "note": "algorithmic FLOPs of the fp32 GEMM; the kernel issues twice "
                                  "as many fp16 MFMA FLOPs (activations split hi + lo); the "
                                  "split-K sum kernel of Wo and W2 is in ms_per_step, not in "
