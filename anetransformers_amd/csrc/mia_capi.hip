@@ -32,6 +32,8 @@ struct DevCtx {
   size_t layer_work_bytes = 0;
   void *gemm_work = nullptr;  // split-K partial products of the Q4_0 GEMM
   size_t gemm_work_bytes = 0;
+  void *split_work = nullptr;  // the Q4_0 GEMM's activations as fp16 hi and lo planes
+  size_t split_work_bytes = 0;
   // Opt-in kernel timing: an event pair around the main kernel of each call
   // (kind 0 = decode kernel, 1 = flash kernel, 2 = Q4_0 matvec kernel,
   // 3 = Q4_0 GEMM kernel).
@@ -111,6 +113,18 @@ int ensure_layer_work(DevCtx *c, size_t bytes) {
     c->layer_work_bytes = 0;
     HIP_TRY(hipMalloc(&c->layer_work, bytes));
     c->layer_work_bytes = bytes;
+  }
+  return MIA_OK;
+}
+
+int ensure_split_work(DevCtx *c, size_t bytes) {
+  if (bytes > c->split_work_bytes) {
+    HIP_TRY(hipDeviceSynchronize());
+    if (c->split_work) HIP_TRY(hipFree(c->split_work));
+    c->split_work = nullptr;
+    c->split_work_bytes = 0;
+    HIP_TRY(hipMalloc(&c->split_work, bytes));
+    c->split_work_bytes = bytes;
   }
   return MIA_OK;
 }
@@ -303,10 +317,18 @@ int q4_impl(const void *Wq, const void *Wk, const void *Wv, const void *x_q8, co
 // Q4_0 GEMM over up to three stacked matrices (see GemmParams).
 int gemm_impl(DevCtx *c, const void *W0, const void *W1, const void *W2, int rows0, int rows1,
               int rows2, const float *X, int K, int S, float *y0, float *y1, float *y2, int mode,
-              hipStream_t s) {
+              hipStream_t s, bool reuse_split = false) {
+  // X [S][K] as fp16 hi + lo planes in split_work; reuse_split: the planes of
+  // this same X are there from the call before on this stream.
+  const size_t n = (size_t)S * K;
+  if (!reuse_split) {
+    if (int rc = ensure_split_work(c, 2 * n * sizeof(_Float16))) return rc;
+  }
+  _Float16 *const ahi = reinterpret_cast<_Float16 *>(c->split_work), *const alo = ahi + n;
+  if (!reuse_split) HIP_TRY(mia::launch_split_hilo(X, (long)n, ahi, alo, c->num_cus, s));
   mia::GemmParams p{};
-  p.A = X;
-  p.lda = K;
+  p.ahi = ahi;
+  p.alo = alo;
   p.w0 = reinterpret_cast<const uint8_t *>(W0);
   p.w1 = reinterpret_cast<const uint8_t *>(W1);
   p.w2 = reinterpret_cast<const uint8_t *>(W2);
@@ -756,7 +778,7 @@ int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_
                          nullptr, mia::kGemmStore, s))
     return rc;
   if (int rc = gemm_impl(c, lw->w3, nullptr, nullptr, hidden, 0, 0, Xn, dim, S, G, nullptr,
-                         nullptr, mia::kGemmSiluMul, s))
+                         nullptr, mia::kGemmSiluMul, s, /*reuse_split=*/true))
     return rc;
   return gemm_impl(c, lw->w2, nullptr, nullptr, dim, 0, 0, G, hidden, S, X, nullptr, nullptr,
                    mia::kGemmAdd, s);

@@ -121,8 +121,8 @@ hipError_t launch_scale_rows(_Float16 *base, long n_rows, int row_elems, int eve
 // multiple of 64; A 16-byte aligned with lda a multiple of 4.
 enum { kGemmStore = 0, kGemmAdd = 1, kGemmSiluMul = 2 };
 struct GemmParams {
-  const float *A;
-  int lda;
+  // the fp32 activations as fp16 hi + lo planes, [S][K] each (launch_split_hilo)
+  const _Float16 *ahi, *alo;
   const uint8_t *w0, *w1, *w2;
   int rows0, rows01, N;  // rows of w0, of w0 + w1, and in all
   int K, S;
@@ -140,6 +140,9 @@ long gemm_tiles(int N, int S);
 int gemm_pick_ksplit(int N, int K, int S, int num_cus);
 hipError_t launch_q4_gemm(const GemmParams &p, int mode, int num_cus, hipStream_t s,
                           hipEvent_t ev0, hipEvent_t ev1);
+// x [n] fp32 -> hi, lo [n] fp16 with x = hi + lo to ~2^-22 (n a multiple of 8).
+hipError_t launch_split_hilo(const float *x, long n, _Float16 *hi, _Float16 *lo, int num_cus,
+                             hipStream_t s);
 hipError_t launch_rmsnorm(float *out, const float *in, const float *w, int dim, int S, float eps,
                           hipStream_t s);
 

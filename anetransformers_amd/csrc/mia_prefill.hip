@@ -16,6 +16,7 @@
 // K values (two Q4_0 blocks, 36 bytes of each row, 4-byte aligned because the
 // blocks per row are even) into one of two LDS stages, with the global loads
 // issued two iterations ahead of their store.
+#include <algorithm>
 #include <type_traits>
 
 #include "mia_device.h"
@@ -92,9 +93,11 @@ __global__ __launch_bounds__(kGThreads, PF == 3 ? 1 : 2) void q4_gemm_kernel(Gem
   const int wm = wave >> 1, wn = wave & 1;
   const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * BM;
 
-  // A staging: thread -> token row ar, 4 * AF4 values at column ac
+  // A staging: thread -> token row ar, 4 * AF4 values at column ac of the
+  // hi and lo planes
   const int ar = tid / ATPR, ac = (tid % ATPR) * 4 * AF4;
-  const float *aptr = p.A + (size_t)min(m0 + ar, p.S - 1) * p.lda + ac;
+  const size_t aoff = (size_t)min(m0 + ar, p.S - 1) * p.K + ac;
+  const _Float16 *const ahp = p.ahi + aoff, *const alp = p.alo + aoff;
   // B staging: thread -> weight row br, block bb (0, 1) of the iteration's pair
   const int br = tid & (kBN - 1), bb = tid / kBN;
   const uint8_t *bptr;
@@ -108,33 +111,27 @@ __global__ __launch_bounds__(kGThreads, PF == 3 ? 1 : 2) void q4_gemm_kernel(Gem
   // Iteration j's rows live in register slot j % PF from their load to their
   // LDS store.
   constexpr int kSlots = PF;
-  f4 areg_s[kSlots][AF4];
+  static_assert(AF4 % 2 == 0, "whole 8-value pieces of A per thread");
+  u4 ahi_s[kSlots][AF4 / 2], alo_s[kSlots][AF4 / 2];
   unsigned breg_s[kSlots][5];
   auto load = [&](auto slot, int it) {
     constexpr int SL = decltype(slot)::value;
-    const float *a = aptr + (size_t)it * kBK;
 #pragma unroll
-    for (int j = 0; j < AF4; ++j) areg_s[SL][j] = *reinterpret_cast<const f4 *>(a + 4 * j);
+    for (int j = 0; j < AF4 / 2; ++j) {
+      ahi_s[SL][j] = *reinterpret_cast<const u4 *>(ahp + (size_t)it * kBK + 8 * j);
+      alo_s[SL][j] = *reinterpret_cast<const u4 *>(alp + (size_t)it * kBK + 8 * j);
+    }
     const uint8_t *b = bptr + (size_t)it * 36;
 #pragma unroll
     for (int j = 0; j < 5; ++j) breg_s[SL][j] = *reinterpret_cast<const unsigned *>(b + 4 * j);
   };
   auto store = [&](auto slot, GemmLds<BM> &st) {
     constexpr int SL = decltype(slot)::value;
-    const f4 *areg = areg_s[SL];
     const unsigned *breg = breg_s[SL];
 #pragma unroll
-    for (int j = 0; j < AF4; j += 2) {
-      h8 hi, lo;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = e < 4 ? areg[j][e] : areg[j + 1][e - 4];
-        const _Float16 h = (_Float16)x;
-        hi[e] = h;
-        lo[e] = (_Float16)(x - (float)h);
-      }
-      *reinterpret_cast<h8 *>(&st.ahi[ar][ac + 4 * j]) = hi;
-      *reinterpret_cast<h8 *>(&st.alo[ar][ac + 4 * j]) = lo;
+    for (int j = 0; j < AF4 / 2; ++j) {
+      *reinterpret_cast<u4 *>(&st.ahi[ar][ac + 8 * j]) = ahi_s[SL][j];
+      *reinterpret_cast<u4 *>(&st.alo[ar][ac + 8 * j]) = alo_s[SL][j];
     }
     // bb 0: bytes 0-19 of the pair (scale 0-1, nibbles 2-17);
     // bb 1: bytes 16-35 (scale 18-19, nibbles 20-35)
@@ -226,9 +223,8 @@ __global__ __launch_bounds__(kGThreads, PF == 3 ? 1 : 2) void q4_gemm_kernel(Gem
   const int it0 = (int)((long)n_all * blockIdx.z / p.ksplit);
   const int n_it = (int)((long)n_all * (blockIdx.z + 1) / p.ksplit) - it0;
   const int last = it0 + n_it - 1;
-  // The loads of iteration it + PF go out after the store of it + 1; loads
-  // past the end repeat the last iteration (in bounds, stored into a stage
-  // nobody reads).  Unrolled by the slot count so that the slots are
+  // Loads past the end repeat the last iteration (in bounds, stored into a
+  // stage nobody reads).  Unrolled by the slot count so that the slots are
   // registers and the waits exact; the scheduling fence after each step
   // keeps the steps from being interleaved (which would need more VGPRs
   // than two workgroups per CU leave).
@@ -241,10 +237,15 @@ __global__ __launch_bounds__(kGThreads, PF == 3 ? 1 : 2) void q4_gemm_kernel(Gem
   __syncthreads();
   // it counts from 0 within the range (stage parity and slot), it0 + it is
   // the absolute iteration
+  // With two slots the loads of it + 2 go out first: their slot was stored
+  // in the step before, and the store of it + 1 then waits only for loads a
+  // whole step older.  Three slots keep the loads after the store (issued
+  // first they would hold a fourth slot's registers through the compute).
   auto step = [&](auto slot, auto next, int it) {
+    if constexpr (PF == 2) load(slot, min(it0 + it + kSlots, last));
     compute(sm[it & 1]);
     store(next, sm[(it + 1) & 1]);
-    load(slot, min(it0 + it + kSlots, last));
+    if constexpr (PF == 3) load(slot, min(it0 + it + kSlots, last));
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -298,6 +299,29 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
 
 // One workgroup per token row: ss = sum(x^2), scale = 1 / sqrt(ss / dim + eps),
 // out = (x * scale) * w, the reference's two roundings (vsmul then vmul).
+// The GEMM's fp32 activations as fp16 hi + lo planes (x = hi + lo to ~2^-22:
+// hi = fp16(x), lo = fp16(x - hi), both rounded to nearest even), split once
+// per GEMM input instead of once per column tile of the GEMM.
+__global__ __launch_bounds__(256) void split_hilo_kernel(const float *__restrict__ x, long n8,
+                                                         _Float16 *__restrict__ hi,
+                                                         _Float16 *__restrict__ lo) {
+#pragma clang fp contract(off)
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n8; i += (long)gridDim.x * 256) {
+    const f4 a = reinterpret_cast<const f4 *>(x)[2 * i];
+    const f4 b = reinterpret_cast<const f4 *>(x)[2 * i + 1];
+    h8 vh, vl;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = e < 4 ? a[e] : b[e - 4];
+      const _Float16 h = (_Float16)v;
+      vh[e] = h;
+      vl[e] = (_Float16)(v - (float)h);
+    }
+    reinterpret_cast<h8 *>(hi)[i] = vh;
+    reinterpret_cast<h8 *>(lo)[i] = vl;
+  }
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(float *out, const float *in, const float *w,
                                                       int dim, float eps) {
   __shared__ float red[4];
@@ -383,6 +407,16 @@ hipError_t launch_q4_gemm(const GemmParams &p, int mode, int num_cus, hipStream_
   if (mode == kGemmStore) return launch_gemm_mode<kGemmStore>(p, num_cus, s, ev0, ev1);
   if (mode == kGemmAdd) return launch_gemm_mode<kGemmAdd>(p, num_cus, s, ev0, ev1);
   return launch_gemm_mode<kGemmSiluMul>(p, num_cus, s, ev0, ev1);
+}
+
+hipError_t launch_split_hilo(const float *x, long n, _Float16 *hi, _Float16 *lo, int num_cus,
+                             hipStream_t s) {
+  if (n % 8) return hipErrorInvalidValue;
+  const long n8 = n / 8;
+  const long wgs = std::min<long>((n8 + 255) / 256, 8L * num_cus);
+  hipLaunchKernelGGL(split_hilo_kernel, dim3((unsigned)std::max<long>(wgs, 1)), dim3(256), 0, s,
+                     x, n8, hi, lo);
+  return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm(float *out, const float *in, const float *w, int dim, int S, float eps,

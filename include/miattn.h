@@ -16,9 +16,10 @@
  *     [max_seq][n_kv_heads][head_dim] fp16; position p lives in slot
  *     p % max_seq (mistral/kv_cache.h:39).  k_layer / v_layer point at a
  *     layer base (kv_k / kv_v, mistral/kv_cache.h:61-68).
- *   - Calls that use split-K scratch share one per-device scratch area: calls
- *     that overlap on one device (several host threads, or several streams)
- *     race.  The first call at a new size may allocate (not inside a HIP
+ *   - Calls that use device scratch (the split-K partials of the attention
+ *     and GEMM kernels, the GEMM's fp16 hi / lo activation planes) share one
+ *     per-device area of each kind: calls that overlap on one device
+ *     (several host threads, or several streams) race.  The first call at a new size may allocate (not inside a HIP
  *     graph capture: warm up first).
  */
 #ifndef MIATTN_H
@@ -204,8 +205,9 @@ int mia_rmsnorm_f32(float *out, const float *in, const float *w, int dim, int S,
 /* tiled_q4_gemm for Q4_0 weights (mistral/mistral_ane_prefill.h:1018-1042,
  * dequantise + cblas_sgemm): Y[S][out_dim] = X[S][in_dim] . W^T, fp32 X and Y
  * (dev, 16-byte aligned), in_dim a multiple of 64.  fp16 MFMA on X split into
- * hi + lo halves with the block scales applied in fp32: within fp32 rounding
- * of the reference's sums, not bit-identical to them. */
+ * hi + lo halves (per-device scratch of S * in_dim * 4 bytes) with the block
+ * scales applied in fp32: within fp32 rounding of the reference's sums, not
+ * bit-identical to them. */
 int mia_q4_0_gemm_f32(const void *W, const float *X, float *Y, int out_dim, int in_dim, int S,
                       void *stream);
 
