@@ -319,7 +319,8 @@ int gemm_impl(DevCtx *c, const void *W0, const void *W1, const void *W2, int row
               int rows2, const float *X, int K, int S, float *y0, float *y1, float *y2, int mode,
               hipStream_t s, bool reuse_split = false) {
   // X [S][K] as fp16 hi + lo planes in split_work; reuse_split: the planes of
-  // this same X are there from the call before on this stream.
+  // the input are already there (written by the call before on this stream,
+  // or by the RMSNorm that produced them), and X is not read.
   const size_t n = (size_t)S * K;
   if (!reuse_split) {
     if (int rc = ensure_split_work(c, 2 * n * sizeof(_Float16))) return rc;
@@ -750,22 +751,26 @@ int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_
   if (int rc = current_ctx(&c)) return rc;
   hipStream_t s = pick_stream(c, stream);
   const int kv_dim = n_kv_heads * kHD;
-  // Xn [S][dim] | Q [S][dim] | K, V [S][kv_dim] | A [S][dim] | G [S][hidden]
+  // Q [S][dim] | K, V [S][kv_dim] | A [S][dim] | G [S][hidden]; the normalised
+  // rows (the QKV and W1 / W3 inputs) only exist as the GEMM's hi + lo planes
+  // in split_work, written there by the RMSNorm.
   auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
   const size_t bd = al((size_t)S * dim * 4), bk = al((size_t)S * kv_dim * 4),
                bh = al((size_t)S * hidden * 4);
-  if (int rc = ensure_layer_work(c, 3 * bd + 2 * bk + bh)) return rc;
+  if (int rc = ensure_layer_work(c, 2 * bd + 2 * bk + bh)) return rc;
+  if (int rc = ensure_split_work(c, (size_t)S * (dim > hidden ? dim : hidden) * 4)) return rc;
   char *w = reinterpret_cast<char *>(c->layer_work);
-  float *Xn = reinterpret_cast<float *>(w);
-  float *Q = reinterpret_cast<float *>(w + bd);
-  float *K = reinterpret_cast<float *>(w + 2 * bd);
-  float *V = reinterpret_cast<float *>(w + 2 * bd + bk);
-  float *A = reinterpret_cast<float *>(w + 2 * bd + 2 * bk);
-  float *G = reinterpret_cast<float *>(w + 3 * bd + 2 * bk);
+  float *Q = reinterpret_cast<float *>(w);
+  float *K = reinterpret_cast<float *>(w + bd);
+  float *V = reinterpret_cast<float *>(w + bd + bk);
+  float *A = reinterpret_cast<float *>(w + bd + 2 * bk);
+  float *G = reinterpret_cast<float *>(w + 2 * bd + 2 * bk);
+  _Float16 *const xn_hi = reinterpret_cast<_Float16 *>(c->split_work);
+  _Float16 *const xn_lo = xn_hi + (size_t)S * dim;
   // mistral_ane_prefill.h:1092-1110
-  HIP_TRY(mia::launch_rmsnorm(Xn, X, lw->rms_att, dim, S, eps, s));
-  if (int rc = gemm_impl(c, lw->wq, lw->wk, lw->wv, dim, kv_dim, kv_dim, Xn, dim, S, Q, K, V,
-                         mia::kGemmStore, s))
+  HIP_TRY(mia::launch_rmsnorm_split(xn_hi, xn_lo, X, lw->rms_att, dim, S, eps, s));
+  if (int rc = gemm_impl(c, lw->wq, lw->wk, lw->wv, dim, kv_dim, kv_dim, nullptr, dim, S, Q, K,
+                         V, mia::kGemmStore, s, /*reuse_split=*/true))
     return rc;
   if (int rc = mia_attention_step(Q, K, V, theta_inv, k_layer, v_layer, A, n_heads, n_kv_heads,
                                   kHD, max_seq, start_pos, S, s))
@@ -773,11 +778,11 @@ int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_
   if (int rc = gemm_impl(c, lw->wo, nullptr, nullptr, dim, 0, 0, A, dim, S, X, nullptr, nullptr,
                          mia::kGemmAdd, s))
     return rc;
-  HIP_TRY(mia::launch_rmsnorm(Xn, X, lw->rms_ffn, dim, S, eps, s));
-  if (int rc = gemm_impl(c, lw->w1, nullptr, nullptr, hidden, 0, 0, Xn, dim, S, G, nullptr,
-                         nullptr, mia::kGemmStore, s))
+  HIP_TRY(mia::launch_rmsnorm_split(xn_hi, xn_lo, X, lw->rms_ffn, dim, S, eps, s));
+  if (int rc = gemm_impl(c, lw->w1, nullptr, nullptr, hidden, 0, 0, nullptr, dim, S, G, nullptr,
+                         nullptr, mia::kGemmStore, s, /*reuse_split=*/true))
     return rc;
-  if (int rc = gemm_impl(c, lw->w3, nullptr, nullptr, hidden, 0, 0, Xn, dim, S, G, nullptr,
+  if (int rc = gemm_impl(c, lw->w3, nullptr, nullptr, hidden, 0, 0, nullptr, dim, S, G, nullptr,
                          nullptr, mia::kGemmSiluMul, s, /*reuse_split=*/true))
     return rc;
   return gemm_impl(c, lw->w2, nullptr, nullptr, dim, 0, 0, G, hidden, S, X, nullptr, nullptr,

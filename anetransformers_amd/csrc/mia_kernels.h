@@ -143,6 +143,9 @@ hipError_t launch_q4_gemm(const GemmParams &p, int mode, int num_cus, hipStream_
 // x [n] fp32 -> hi, lo [n] fp16 with x = hi + lo to ~2^-22 (n a multiple of 8).
 hipError_t launch_split_hilo(const float *x, long n, _Float16 *hi, _Float16 *lo, int num_cus,
                              hipStream_t s);
+// The same rows written as fp16 hi + lo planes (launch_split_hilo's split).
+hipError_t launch_rmsnorm_split(_Float16 *hi, _Float16 *lo, const float *in, const float *w,
+                                int dim, int S, float eps, hipStream_t s);
 hipError_t launch_rmsnorm(float *out, const float *in, const float *w, int dim, int S, float eps,
                           hipStream_t s);
 

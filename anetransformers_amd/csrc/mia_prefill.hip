@@ -322,8 +322,12 @@ __global__ __launch_bounds__(256) void split_hilo_kernel(const float *__restrict
   }
 }
 
+// With hi set, the normalised rows go out as the Q4_0 GEMM's fp16 hi + lo
+// planes (split exactly as split_hilo_kernel does) instead of fp32 to out.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(float *out, const float *in, const float *w,
-                                                      int dim, float eps) {
+                                                      int dim, float eps, _Float16 *hi,
+                                                      _Float16 *lo) {
+#pragma clang fp contract(off)
   __shared__ float red[4];
   const int t = blockIdx.x, tid = threadIdx.x;
   const float *x = in + (size_t)t * dim;
@@ -337,14 +341,26 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *out, const float *i
   __syncthreads();
   ss = (red[0] + red[1]) + (red[2] + red[3]);
   const float scale = 1.0f / sqrtf(ss / (float)dim + eps);
-  float *o = out + (size_t)t * dim;
+  const size_t row = (size_t)t * dim;
   for (int i = 4 * tid; i < dim; i += 4 * 256) {
     const f4 v = *reinterpret_cast<const f4 *>(x + i);
     const f4 wv = *reinterpret_cast<const f4 *>(w + i);
     f4 r;
 #pragma unroll
     for (int e = 0; e < 4; ++e) r[e] = (v[e] * scale) * wv[e];
-    *reinterpret_cast<f4 *>(o + i) = r;
+    if (hi != nullptr) {
+      h4 vh, vl;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const _Float16 h = (_Float16)r[e];
+        vh[e] = h;
+        vl[e] = (_Float16)(r[e] - (float)h);
+      }
+      *reinterpret_cast<h4 *>(hi + row + i) = vh;
+      *reinterpret_cast<h4 *>(lo + row + i) = vl;
+    } else {
+      *reinterpret_cast<f4 *>(out + row + i) = r;
+    }
   }
 }
 
@@ -421,7 +437,15 @@ hipError_t launch_split_hilo(const float *x, long n, _Float16 *hi, _Float16 *lo,
 
 hipError_t launch_rmsnorm(float *out, const float *in, const float *w, int dim, int S, float eps,
                           hipStream_t s) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(S), dim3(256), 0, s, out, in, w, dim, eps);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(S), dim3(256), 0, s, out, in, w, dim, eps,
+                     (_Float16 *)nullptr, (_Float16 *)nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_split(_Float16 *hi, _Float16 *lo, const float *in, const float *w,
+                                int dim, int S, float eps, hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(S), dim3(256), 0, s, (float *)nullptr, in, w, dim, eps,
+                     hi, lo);
   return hipGetLastError();
 }
 
