@@ -317,19 +317,31 @@ int q4_impl(const void *Wq, const void *Wk, const void *Wv, const void *x_q8, co
 // Q4_0 GEMM over up to three stacked matrices (see GemmParams).
 int gemm_impl(DevCtx *c, const void *W0, const void *W1, const void *W2, int rows0, int rows1,
               int rows2, const float *X, int K, int S, float *y0, float *y1, float *y2, int mode,
-              hipStream_t s, bool reuse_split = false) {
+              hipStream_t s, bool reuse_split = false, const _Float16 *planes = nullptr,
+              _Float16 *out_planes = nullptr) {
   // X [S][K] as fp16 hi + lo planes in split_work; reuse_split: the planes of
   // the input are already there (written by the call before on this stream,
   // or by the RMSNorm that produced them), and X is not read.
+  // planes: the input's planes given by the caller ([S][K] hi, then lo).
+  // out_planes (kGemmSiluMul): the result as planes there instead of in y0.
   const size_t n = (size_t)S * K;
-  if (!reuse_split) {
+  const bool have = reuse_split || planes != nullptr;
+  if (!have) {
     if (int rc = ensure_split_work(c, 2 * n * sizeof(_Float16))) return rc;
   }
-  _Float16 *const ahi = reinterpret_cast<_Float16 *>(c->split_work), *const alo = ahi + n;
-  if (!reuse_split) HIP_TRY(mia::launch_split_hilo(X, (long)n, ahi, alo, c->num_cus, s));
+  const _Float16 *const ahi =
+      planes != nullptr ? planes : reinterpret_cast<const _Float16 *>(c->split_work);
+  const _Float16 *const alo = ahi + n;
+  if (!have)
+    HIP_TRY(mia::launch_split_hilo(X, (long)n, const_cast<_Float16 *>(ahi),
+                                   const_cast<_Float16 *>(alo), c->num_cus, s));
   mia::GemmParams p{};
   p.ahi = ahi;
   p.alo = alo;
+  if (out_planes != nullptr) {
+    p.ohi = out_planes;
+    p.olo = out_planes + (size_t)S * (rows0 + rows1 + rows2);
+  }
   p.w0 = reinterpret_cast<const uint8_t *>(W0);
   p.w1 = reinterpret_cast<const uint8_t *>(W1);
   p.w2 = reinterpret_cast<const uint8_t *>(W2);
@@ -751,20 +763,22 @@ int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_
   if (int rc = current_ctx(&c)) return rc;
   hipStream_t s = pick_stream(c, stream);
   const int kv_dim = n_kv_heads * kHD;
-  // Q [S][dim] | K, V [S][kv_dim] | A [S][dim] | G [S][hidden]; the normalised
-  // rows (the QKV and W1 / W3 inputs) only exist as the GEMM's hi + lo planes
-  // in split_work, written there by the RMSNorm.
+  // Q [S][dim] | K, V [S][kv_dim] | A [S][dim] | G [S][hidden] | H planes
+  // [2][S][hidden] fp16; the normalised rows (the QKV and W1 / W3 inputs) only
+  // exist as the GEMM's hi + lo planes in split_work, written there by the
+  // RMSNorm, and the SwiGLU output H (W2's input) only as the planes after G.
   auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
   const size_t bd = al((size_t)S * dim * 4), bk = al((size_t)S * kv_dim * 4),
                bh = al((size_t)S * hidden * 4);
-  if (int rc = ensure_layer_work(c, 2 * bd + 2 * bk + bh)) return rc;
-  if (int rc = ensure_split_work(c, (size_t)S * (dim > hidden ? dim : hidden) * 4)) return rc;
+  if (int rc = ensure_layer_work(c, 2 * bd + 2 * bk + 2 * bh)) return rc;
+  if (int rc = ensure_split_work(c, (size_t)S * dim * 4)) return rc;  // [2][S][dim] fp16
   char *w = reinterpret_cast<char *>(c->layer_work);
   float *Q = reinterpret_cast<float *>(w);
   float *K = reinterpret_cast<float *>(w + bd);
   float *V = reinterpret_cast<float *>(w + bd + bk);
   float *A = reinterpret_cast<float *>(w + bd + 2 * bk);
   float *G = reinterpret_cast<float *>(w + 2 * bd + 2 * bk);
+  _Float16 *const h_planes = reinterpret_cast<_Float16 *>(w + 2 * bd + 2 * bk + bh);
   _Float16 *const xn_hi = reinterpret_cast<_Float16 *>(c->split_work);
   _Float16 *const xn_lo = xn_hi + (size_t)S * dim;
   // mistral_ane_prefill.h:1092-1110
@@ -783,10 +797,10 @@ int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_
                          nullptr, mia::kGemmStore, s, /*reuse_split=*/true))
     return rc;
   if (int rc = gemm_impl(c, lw->w3, nullptr, nullptr, hidden, 0, 0, nullptr, dim, S, G, nullptr,
-                         nullptr, mia::kGemmSiluMul, s, /*reuse_split=*/true))
+                         nullptr, mia::kGemmSiluMul, s, /*reuse_split=*/true, nullptr, h_planes))
     return rc;
-  return gemm_impl(c, lw->w2, nullptr, nullptr, dim, 0, 0, G, hidden, S, X, nullptr, nullptr,
-                   mia::kGemmAdd, s);
+  return gemm_impl(c, lw->w2, nullptr, nullptr, dim, 0, 0, nullptr, hidden, S, X, nullptr,
+                   nullptr, mia::kGemmAdd, s, false, h_planes);
 }
 
 int mia_quantize_q8_0(const float *x, void *out_q8, int n, void *stream) {

@@ -135,6 +135,10 @@ struct GemmParams {
   // and applies the epilogue.
   int ksplit;
   float *part;
+  // kGemmSiluMul only: when set, the result goes out as fp16 hi + lo planes
+  // [S][N] (the next GEMM's input, launch_split_hilo's split) instead of
+  // into y0.
+  _Float16 *ohi, *olo;
 };
 long gemm_tiles(int N, int S);
 int gemm_pick_ksplit(int N, int K, int S, int num_cus);

@@ -66,10 +66,19 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams &p, int m, int n,
     float *y = p.y0 + (size_t)m * p.N + n;
     *y = *y + v;
   } else {  // kGemmSiluMul: y0 holds the gate; gate * sigmoid(gate) * up
+#pragma clang fp contract(off)
     float *y = p.y0 + (size_t)m * p.N + n;
     const float g = *y;
     const float sig = 1.0f / (1.0f + expf(-g));
-    *y = (g * sig) * v;
+    const float r = (g * sig) * v;
+    if (p.ohi != nullptr) {
+      const size_t i = (size_t)m * p.N + n;
+      const _Float16 h = (_Float16)r;
+      p.ohi[i] = h;
+      p.olo[i] = (_Float16)(r - (float)h);
+    } else {
+      *y = r;
+    }
   }
 }
 
