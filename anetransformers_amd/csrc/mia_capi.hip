@@ -18,7 +18,7 @@ namespace {
 constexpr int kMaxDevices = 16;
 constexpr int kG = 4;
 constexpr int kHD = 128;
-constexpr int kMaxSeq = 1 << 22;  // keeps 32-bit in-layer element offsets exact
+constexpr int kMaxSeq = 1 << 22;  // ring capacity limit; in-layer offsets are 64-bit in every kernel
 
 struct DevCtx {
   bool ready = false;

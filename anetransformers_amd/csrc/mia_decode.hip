@@ -123,16 +123,18 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
         off = (size_t)ring_slot(p.start, t0, p.max_seq) * kv_dim + koff;
       } else {
         const int t = min(t0 + lc, ce - 1);
-        off = (unsigned)ring_slot(p.start, t, p.max_seq) * (unsigned)kv_dim + 8 * lg;
+        off = (size_t)ring_slot(p.start, t, p.max_seq) * kv_dim + 8 * lg;
       }
     }
     const _Float16 *src = kbase + off;
 #pragma unroll
     for (int s = 0; s < 4; ++s) b.k[s] = *reinterpret_cast<const u4 *>(src + 32 * s);
   };
+  // (In-layer offsets reach max_seq * kv_dim elements, beyond 32 bits for
+  // large rings: the per-lane slot offsets are formed in 64 bits.)
   auto issue_v = [&](TileBuf &b, int tt) {
     size_t row0 = 0;
-    unsigned off[4] = {0, 0, 0, 0};
+    size_t off[4] = {0, 0, 0, 0};
     if (tt >= 0) {
       bool linear;
       const int t0 = tile_row0(tt, linear);
@@ -144,7 +146,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           const int t = min(t0 + 4 * lg + m, ce - 1);
-          off[m] = (unsigned)ring_slot(p.start, t, p.max_seq) * (unsigned)kv_dim + 8 * lc;
+          off[m] = (size_t)ring_slot(p.start, t, p.max_seq) * kv_dim + 8 * lc;
         }
       }
     }

@@ -101,9 +101,13 @@ __global__ void __launch_bounds__(128)
 }
 
 // mistral/mistral_ane_prefill.h:189-204: cvt + kv_write at (start+t) % M.
+// The reference writes the tokens in order, so with S > M a slot keeps the
+// last token written to it: tokens t < S - M are overwritten and skipped here
+// (several blocks writing one slot at once would leave any of them).
 __global__ void kv_write_kernel(_Float16 *kc, _Float16 *vc, const float *K, const float *V, int S,
                                 int start_pos, int max_seq, int kv_dim) {
   const int t = blockIdx.y;
+  if (t < S - max_seq) return;
   const size_t slot = (size_t)((start_pos + t) % max_seq);
   for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < kv_dim; e += gridDim.x * blockDim.x) {
     kc[slot * kv_dim + e] = (_Float16)K[(size_t)t * kv_dim + e];
@@ -112,11 +116,14 @@ __global__ void kv_write_kernel(_Float16 *kc, _Float16 *vc, const float *K, cons
 }
 
 // Staged row t of layer blockIdx.z -> ring slot (start_pos + t) % max_seq of
-// that layer; layers are ring_stride / stage_stride elements apart.
+// that layer; layers are ring_stride / stage_stride elements apart.  Rows a
+// later row overwrites (t < S - max_seq) are skipped: the sequential writes
+// leave the last one.
 __global__ void commit_kernel(_Float16 *kc, _Float16 *vc, const _Float16 *kst,
                               const _Float16 *vst, int S, int start_pos, int max_seq, int kv_dim,
                               size_t ring_stride, size_t stage_stride) {
   const int t = blockIdx.y;
+  if (t < S - max_seq) return;
   const size_t slot = (size_t)((start_pos + t) % max_seq);
   kc += blockIdx.z * ring_stride;
   vc += blockIdx.z * ring_stride;

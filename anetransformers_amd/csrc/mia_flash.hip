@@ -444,19 +444,29 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   f16v o[NB][4];
   float m_ref[NB], l_run[NB];
   f16v s_cur[NB];
-  h8 qx[NB];  // extra k-step B operand: -m_ref in element 0 of the half-0 lanes
+  h8 qx[NB];  // extra k-step B operand: -m_ref as fp16 hi, lo in elements 0, 1 of the half-0 lanes
 #pragma unroll
   for (int b = 0; b < NB; ++b) m_ref[b] = -INFINITY;
   const h8 zero8 = {};
-  h8 kx = {};  // extra k-step A operand: a ones column (k = 0) for every key
-  if (half == 0) kx[0] = (_Float16)1.0f;
+  h8 kx = {};  // extra k-step A operand: ones in k = 0, 1 for every key
+  if (half == 0) {
+    kx[0] = (_Float16)1.0f;
+    kx[1] = (_Float16)1.0f;
+  }
   auto set_ref = [&](int b, float m) {
-    // fp16 range; the rounded value is the one applied and reported
-    const float mc = m == -INFINITY ? 0.f : fminf(fmaxf(m, -60000.f), 60000.f);
-    const _Float16 mh = (_Float16)mc;
-    m_ref[b] = m == -INFINITY ? -INFINITY : (float)mh;
+    // m_ref = hi + lo (fp16 each): within ~2^-22 relative of m for |m| up to
+    // ~1.2e5 log2 units, so P <= 1 holds at any realistic score magnitude (a
+    // single fp16 would be off by up to 16 units beyond 32768); the applied
+    // value is the one reported
+    const float mc = m == -INFINITY ? 0.f : fminf(fmaxf(m, -1.2e5f), 1.2e5f);
+    const _Float16 mh = (_Float16)fminf(fmaxf(mc, -6.0e4f), 6.0e4f);
+    const _Float16 ml = (_Float16)(mc - (float)mh);
+    m_ref[b] = m == -INFINITY ? -INFINITY : (float)mh + (float)ml;
     h8 x = {};
-    if (half == 0) x[0] = -mh;
+    if (half == 0) {
+      x[0] = -mh;
+      x[1] = -ml;
+    }
     qx[b] = x;
   };
 
@@ -861,7 +871,8 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(FlashParams p, int rt)
   __shared__ float wmax[4], wsum[4];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int kv_dim = p.n_kv * HD;
-  if (p.commit_k != nullptr && (int)blockIdx.x < p.S) {
+  // (rows t < S - max_seq are overwritten by later rows in the same slot)
+  if (p.commit_k != nullptr && (int)blockIdx.x < p.S && (int)blockIdx.x >= p.S - p.max_seq) {
     const int t = blockIdx.x;
     const size_t slot = (size_t)((p.start_pos + t) % p.max_seq);
     for (int e = 4 * tid; e < kv_dim; e += 4 * 256) {

@@ -45,7 +45,13 @@ typedef struct {
     int len;
 } KVCache;
 
-/* mistral/gguf_loader.h:51-63, same fields in the same order. */
+/* mistral/gguf_loader.h:51-63, same fields in the same order.  The reference's
+ * translation unit includes gguf_loader.h before kv_cache.h
+ * (mistral/mistral_infer.m:12-14), so its MistralConfig is already there:
+ * gguf_loader.h defines GGUF_MAGIC (gguf_loader.h:15), which suppresses this
+ * copy.  A translation unit that includes gguf_loader.h after this header
+ * defines MIA_DROPIN_HAVE_MISTRAL_CONFIG first. */
+#if !defined(GGUF_MAGIC) && !defined(MIA_DROPIN_HAVE_MISTRAL_CONFIG)
 typedef struct {
     int dim;
     int hidden_dim;
@@ -59,6 +65,7 @@ typedef struct {
     float rms_eps;
     int sliding_window;
 } MistralConfig;
+#endif
 
 /* mistral/dequant.h:537-541: 36 bytes, fp32 scale then 32 int8. */
 typedef struct {
