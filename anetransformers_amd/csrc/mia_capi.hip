@@ -13,6 +13,14 @@
 #include "../../include/miattn.h"
 #include "mia_kernels.h"
 
+// Scratch of mia_decode_step_noalloc, one copy per device for the life of the
+// process: the split-K partials (m, l, o) of one decode call, up to 256 chunks
+// x 8 kv heads x 4 query heads x (128 + 2) floats.  Host code never uses this
+// name as an address: mia_init takes each device's address of it once
+// (hipGetSymbolAddress) into DevCtx::noalloc.
+constexpr size_t kNoAllocScratchBytes = 4259840;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 namespace {
 
 constexpr int kMaxDevices = 16;
@@ -24,8 +32,11 @@ struct DevCtx {
   bool ready = false;
   hipStream_t stream = nullptr;
   int num_cus = 256;
-  void *scratch = nullptr;  // split-K partials
-  size_t scratch_bytes = 0;
+  void *split = nullptr;  // split-K partials (allocated on demand)
+  size_t split_bytes = 0;
+  // The address of this device's copy of `scratch` (below), for
+  // mia_decode_step_noalloc; taken once by mia_init.
+  void *noalloc = nullptr;
   void *work = nullptr;  // fp16 draft staging for mia_attention_step
   size_t work_bytes = 0;
   void *layer_work = nullptr;  // activations of mia_prefill_layer
@@ -81,14 +92,14 @@ hipStream_t pick_stream(DevCtx *c, void *stream) {
 // Grows the split-K scratch.  Growth synchronises the device so that no
 // queued kernel still uses the old buffer.
 int ensure_scratch(DevCtx *c, size_t bytes) {
-  if (bytes > c->scratch_bytes) {
+  if (bytes > c->split_bytes) {
     HIP_TRY(hipDeviceSynchronize());
-    if (c->scratch) HIP_TRY(hipFree(c->scratch));
-    c->scratch = nullptr;
-    c->scratch_bytes = 0;
+    if (c->split) HIP_TRY(hipFree(c->split));
+    c->split = nullptr;
+    c->split_bytes = 0;
     size_t sz = bytes + (bytes >> 2);
-    HIP_TRY(hipMalloc(&c->scratch, sz));
-    c->scratch_bytes = sz;
+    HIP_TRY(hipMalloc(&c->split, sz));
+    c->split_bytes = sz;
   }
   return MIA_OK;
 }
@@ -189,13 +200,24 @@ int prof_pair(DevCtx *c, int kind, hipEvent_t *ev0, hipEvent_t *ev1) {
 }
 
 // new_k / new_v (fused only, may be null): where the new token's fp16 rows go
-// instead of its ring slot.
+// instead of its ring slot.  fixed (may be null): partials go there, at most
+// fixed_bytes, instead of into the on-demand split area; the chunk count is
+// capped to fit, and nothing is allocated (no timing events either).
 int decode_impl(const float *q, const float *k, const float *v, const float *theta_inv,
                 uint16_t *k_layer, uint16_t *v_layer, float *out, int n_heads, int n_kv, int max_seq,
                 int pos, bool fused, void *stream, uint16_t *new_k = nullptr,
-                uint16_t *new_v = nullptr) {
+                uint16_t *new_v = nullptr, void *fixed = nullptr, size_t fixed_bytes = 0) {
   DevCtx *c;
-  if (int rc = current_ctx(&c)) return rc;
+  if (fixed != nullptr) {
+    // no mia_init from here: it creates the library's stream
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices || !g_ctx[dev].ready)
+      return set_err(MIA_ERR_NO_DEVICE, "device %d not initialised: call mia_init first", dev);
+    c = &g_ctx[dev];
+  } else if (int rc = current_ctx(&c)) {
+    return rc;
+  }
   const int L = pos + 1 < max_seq ? pos + 1 : max_seq;
   const long start = ((long)pos + 1 - L) % max_seq;
   mia::DecodeParams p{};
@@ -215,15 +237,27 @@ int decode_impl(const float *q, const float *k, const float *v, const float *the
   p.new_slot = pos % max_seq;
   p.n_kv = n_kv;
   p.nchunk = mia::decode_pick_nchunk(L, n_kv, c->num_cus);
+  if (fixed != nullptr) {
+    const size_t per_chunk = mia::decode_scratch_bytes(n_kv, kG, 1);
+    const size_t cap = fixed_bytes / per_chunk;
+    if (cap < 2) p.nchunk = 1;  // a single chunk writes out directly
+    else if ((size_t)p.nchunk > cap) p.nchunk = (int)cap;
+  }
   p.qscale = qscale_log2();
   if (p.nchunk > 1) {
-    if (int rc = ensure_scratch(c, mia::decode_scratch_bytes(n_kv, kG, p.nchunk))) return rc;
-    p.part_o = reinterpret_cast<float *>(c->scratch);
+    if (fixed != nullptr) {
+      p.part_o = reinterpret_cast<float *>(fixed);
+    } else {
+      if (int rc = ensure_scratch(c, mia::decode_scratch_bytes(n_kv, kG, p.nchunk))) return rc;
+      p.part_o = reinterpret_cast<float *>(c->split);
+    }
     p.part_ml = p.part_o + (size_t)n_kv * p.nchunk * kG * kHD;
   }
   hipStream_t s = pick_stream(c, stream);
-  hipEvent_t ev0, ev1;
-  if (int rc = prof_pair(c, 0, &ev0, &ev1)) return rc;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  if (fixed == nullptr) {
+    if (int rc = prof_pair(c, 0, &ev0, &ev1)) return rc;
+  }
   HIP_TRY(mia::launch_decode(p, kG, fused, s, ev0, ev1));
   HIP_TRY(mia::launch_decode_merge(p, s));
   return MIA_OK;
@@ -255,7 +289,7 @@ int flash_impl(DevCtx *c, const float *Q, const float *rope_cs, const uint16_t *
     size_t ntile = (size_t)n_kv * p.n_rtiles;
     if (int rc = ensure_scratch(c, mia::flash_scratch_bytes(n_kv, p.n_rtiles, p.nsplit, rt)))
       return rc;
-    p.part_o = reinterpret_cast<float *>(c->scratch);
+    p.part_o = reinterpret_cast<float *>(c->split);
     p.part_ml = p.part_o + ntile * p.nsplit * rt * kHD;
   }
   hipEvent_t ev0, ev1;
@@ -417,6 +451,7 @@ int mia_init(int device) {
   c.num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   HIP_TRY(mia::prepare_flash());
   HIP_TRY(mia::prepare_gemm());
+  HIP_TRY(hipGetSymbolAddress(&c.noalloc, HIP_SYMBOL(scratch)));
   HIP_TRY(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
   c.ready = true;
   return MIA_OK;
@@ -608,6 +643,22 @@ int mia_decode_step(const float *q, const float *k, const float *v, const float 
   if (int rc = check_pos(pos, 1)) return rc;
   return decode_impl(q, k, v, theta_inv, k_layer, v_layer, out, n_heads, n_kv_heads, max_seq, pos,
                      true, stream);
+}
+
+int mia_decode_step_noalloc(const float *q, const float *k, const float *v,
+                            const float *theta_inv, uint16_t *k_layer, uint16_t *v_layer,
+                            float *out, int n_heads, int n_kv_heads, int hd, int max_seq, int pos,
+                            void *stream) {
+  if (!q || !k || !v || !theta_inv || !out || !k_layer || !v_layer)
+    return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (int rc = check_shape(n_heads, n_kv_heads, hd, max_seq)) return rc;
+  if (int rc = check_pos(pos, 1)) return rc;
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices || !g_ctx[dev].ready || g_ctx[dev].noalloc == nullptr)
+    return set_err(MIA_ERR_NO_DEVICE, "device %d not initialised: call mia_init first", dev);
+  return decode_impl(q, k, v, theta_inv, k_layer, v_layer, out, n_heads, n_kv_heads, max_seq, pos,
+                     true, stream, nullptr, nullptr, g_ctx[dev].noalloc, kNoAllocScratchBytes);
 }
 
 int mia_attention_batch(const float *Q, float *out, const uint16_t *k_layer, const uint16_t *v_layer,

@@ -113,6 +113,21 @@ int mia_decode_step(const float *q, const float *k, const float *v, const float 
                     uint16_t *k_layer, uint16_t *v_layer, float *out, int n_heads,
                     int n_kv_heads, int hd, int max_seq, int pos, void *stream);
 
+/* mia_decode_step with no device allocation.  No counterpart in the
+ * reference: this is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * split-K partials go to a fixed per-device area in the library
+ * (4,259,840 bytes: 256 chunks at 8 kv heads; more kv heads get fewer chunks
+ * rather than an error), set up by mia_init, which must have been called on
+ * the device first (MIA_ERR_NO_DEVICE otherwise).  Results are those of
+ * mia_decode_step.  Every call on a device shares that area: calls that
+ * overlap on one device (several host threads or streams) race.  The call
+ * makes no hipMalloc / hipFree and is not timed by mia_profile_*. */
+int mia_decode_step_noalloc(const float *q, const float *k, const float *v,
+                            const float *theta_inv, uint16_t *k_layer, uint16_t *v_layer,
+                            float *out, int n_heads, int n_kv_heads, int hd, int max_seq, int pos,
+                            void *stream);
+
 /* S>=1 causal GQA attention over the ring as it stands, query t at position
  * start_pos + t.  Replaces attention_batch (mistral/mistral_ane_prefill.h:
  * 207-275).  Q [S][n_heads*128] fp32 dev, rotated; out [S][n_heads*128]. */
