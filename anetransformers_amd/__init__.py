@@ -121,6 +121,14 @@ _SIGS = {
         [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P],
     ),
     "mia_attention_batch": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, _P]),
+    "mia_attention_positions": (
+        c_int,
+        [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P],
+    ),
+    "mia_attention_chunk": (
+        c_int,
+        [_P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P],
+    ),
     "mia_attention_step": (
         c_int,
         [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, _P],
@@ -191,6 +199,10 @@ _SIGS = {
     "mia_dropin_verify_step": (
         None,
         [POINTER(KVCache), c_int, _P, _P, _P, c_int, c_int, _P, c_int, c_int, _P],
+    ),
+    "mia_dropin_prefill_chunk_attention": (
+        None,
+        [POINTER(KVCache), c_int, _P, _P, _P, _P, c_int, _P, c_int, c_int, _P],
     ),
     "mia_dropin_verify_stage": (
         None,

@@ -258,8 +258,48 @@ int decode_impl(const float *q, const float *k, const float *v, const float *the
   if (fixed == nullptr) {
     if (int rc = prof_pair(c, 0, &ev0, &ev1)) return rc;
   }
-  HIP_TRY(mia::launch_decode(p, kG, fused, s, ev0, ev1));
+  HIP_TRY(mia::launch_decode(p, kG, fused ? mia::kDecodeFused : mia::kDecodePlain, s, ev0, ev1));
   HIP_TRY(mia::launch_decode_merge(p, s));
+  return MIA_OK;
+}
+
+// S tokens at their own positions (device int32 [S]) over the ring as it
+// stands, through the decode kernel batched over tokens; theta_inv set: Q is
+// raw and rotated in-kernel.  Every token takes the same chunk count, planned
+// for the longest possible window (max_seq).
+int positions_impl(DevCtx *c, const float *Q, const float *theta_inv, const int *positions,
+                   const uint16_t *k_layer, const uint16_t *v_layer, float *out, int n_kv,
+                   int max_seq, int S, hipStream_t s) {
+  mia::DecodeParams p{};
+  p.q = Q;
+  p.theta_inv = theta_inv;
+  p.kc = reinterpret_cast<_Float16 *>(const_cast<uint16_t *>(k_layer));
+  p.vc = reinterpret_cast<_Float16 *>(const_cast<uint16_t *>(v_layer));
+  p.out = out;
+  p.max_seq = max_seq;
+  p.n_kv = n_kv;
+  p.positions = positions;
+  p.n_tok = S;
+  const int hgroups = (n_kv + 7) / 8;
+  const int target = (c->num_cus + S * hgroups - 1) / (S * hgroups);
+  p.nchunk = mia::decode_pick_nchunk(max_seq, n_kv, target * hgroups);
+  p.qscale = qscale_log2();
+  if (p.nchunk > 1) {
+    if (int rc = ensure_scratch(c, mia::decode_scratch_bytes(n_kv, kG, p.nchunk, S))) return rc;
+    p.part_o = reinterpret_cast<float *>(c->split);
+    p.part_ml = p.part_o + (size_t)S * n_kv * p.nchunk * kG * kHD;
+  }
+  hipEvent_t ev0, ev1;
+  if (int rc = prof_pair(c, 0, &ev0, &ev1)) return rc;
+  HIP_TRY(mia::launch_decode(p, kG, mia::kDecodePositions, s, ev0, ev1));
+  HIP_TRY(mia::launch_decode_merge(p, s));
+  return MIA_OK;
+}
+
+int check_positions(const int *positions, int S) {
+  if (!positions) return set_err(MIA_ERR_INVALID, "positions is NULL");
+  if ((uintptr_t)positions & 3) return set_err(MIA_ERR_INVALID, "positions must be 4-byte aligned");
+  if (S < 1 || S > 65535) return set_err(MIA_ERR_INVALID, "token count %d outside 1..65535", S);
   return MIA_OK;
 }
 
@@ -672,6 +712,40 @@ int mia_attention_batch(const float *Q, float *out, const uint16_t *k_layer, con
   if (int rc = current_ctx(&c)) return rc;
   return flash_impl(c, Q, nullptr, nullptr, nullptr, k_layer, v_layer, out, n_kv_heads, max_seq,
                     start_pos, S, pick_stream(c, stream));
+}
+
+int mia_attention_positions(const float *Q, float *out, const uint16_t *k_layer,
+                            const uint16_t *v_layer, const int *positions, int n_heads,
+                            int n_kv_heads, int hd, int max_seq, int S, void *stream) {
+  if (!Q || !out || !k_layer || !v_layer) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (int rc = check_positions(positions, S)) return rc;
+  if (int rc = check_align16(Q, out, k_layer, v_layer)) return rc;
+  if (int rc = check_shape(n_heads, n_kv_heads, hd, max_seq)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  return positions_impl(c, Q, nullptr, positions, k_layer, v_layer, out, n_kv_heads, max_seq, S,
+                        pick_stream(c, stream));
+}
+
+int mia_attention_chunk(const float *Q, const float *K, const float *V, const int *positions,
+                        const float *theta_inv, uint16_t *k_layer, uint16_t *v_layer, float *out,
+                        int n_heads, int n_kv_heads, int hd, int max_seq, int S, void *stream) {
+  if (!Q || !K || !V || !theta_inv || !out || !k_layer || !v_layer)
+    return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (int rc = check_positions(positions, S)) return rc;
+  if (int rc = check_align16(Q, K, V, out)) return rc;
+  if (int rc = check_align16(k_layer, v_layer, nullptr, nullptr)) return rc;
+  if (int rc = check_shape(n_heads, n_kv_heads, hd, max_seq)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  hipStream_t s = pick_stream(c, stream);
+  // phase 1 (mistral_model.h:935-955), then phase 2 (:961-1044) with Q
+  // rotated in the attention kernel
+  HIP_TRY(mia::launch_rope_kv_positions(K, V, theta_inv, positions, S, n_kv_heads,
+                                        reinterpret_cast<_Float16 *>(k_layer),
+                                        reinterpret_cast<_Float16 *>(v_layer), max_seq, s));
+  return positions_impl(c, Q, theta_inv, positions, k_layer, v_layer, out, n_kv_heads, max_seq, S,
+                        s);
 }
 
 int mia_attention_step(const float *Q, const float *K, const float *V, const float *theta_inv,

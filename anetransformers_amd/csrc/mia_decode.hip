@@ -66,9 +66,34 @@ __device__ __forceinline__ int ring_slot(int start, int t, int max_seq) {
   return s >= max_seq ? s - max_seq : s;
 }
 
-template <bool FUSED>
+// kPlain: q already rotated, one token at p.pos.  kFused: the decode step
+// (RoPE of q and k at p.pos, the new token's write, attention).  kPositions:
+// token blockIdx.y at p.positions[blockIdx.y] over the ring as it stands
+// (the chunked prefill's phase 2), q rotated in-kernel when theta_inv is set.
+enum { kPlain = 0, kFused = 1, kPositions = 2 };
+
+template <int MODE>
 __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   __shared__ DecodeSmem sm;
+  constexpr bool FUSED = MODE == kFused;
+
+  // This workgroup's token: window, query, output and partial rows.
+  int pos = p.pos, win_L = p.L, win_start = p.start;
+  const float *q_in = p.q;
+  float *out = p.out, *part_o = p.part_o, *part_ml = p.part_ml;
+  if (MODE == kPositions) {
+    const int tok = blockIdx.y;
+    pos = p.positions[tok];
+    // mistral_model.h:964-967; a negative position has an empty window
+    win_L = pos < 0 ? 0 : (pos + 1 < p.max_seq ? pos + 1 : p.max_seq);
+    win_start = pos < 0 ? 0 : (int)(((long)pos + 1 - win_L) % p.max_seq);
+    const size_t rows = (size_t)p.n_kv * G;  // query heads
+    q_in += (size_t)tok * rows * HD;
+    out += (size_t)tok * rows * HD;
+    part_o += (size_t)tok * rows * p.nchunk * HD;
+    part_ml += (size_t)tok * rows * p.nchunk * 2;
+  }
+  const bool rope_q = FUSED || (MODE == kPositions && p.theta_inv != nullptr);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -83,7 +108,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   const int kv_dim = p.n_kv * HD;
   // The new token (fused) is attended after the loop, from its fp16 copy in
   // LDS, by the waves of the last chunk; the tiles cover keys [0, ce).
-  const int ce = FUSED ? p.L - 1 : p.L;
+  const int ce = FUSED ? win_L - 1 : win_L;
   const int n_tiles = (ce + kTile - 1) / kTile;
   const bool has_new = FUSED && chunk == p.nchunk - 1;
   // Tiles of this wave: chunk, chunk + nchunk, chunk + 2 nchunk, ...
@@ -104,7 +129,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   for (int m = 0; m < 4; ++m) voff[m] = (unsigned)(4 * lg + m) * kv_dim + 8 * lc;
   auto tile_row0 = [&](int tt, bool &linear) {
     const int t0 = tt * kTile;
-    const int s0 = ring_slot(p.start, t0, p.max_seq);
+    const int s0 = ring_slot(win_start, t0, p.max_seq);
     linear = s0 + kTile <= p.max_seq && t0 + kTile <= ce;
     return t0;
   };
@@ -120,10 +145,10 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
       bool linear;
       const int t0 = tile_row0(tt, linear);
       if (linear) {
-        off = (size_t)ring_slot(p.start, t0, p.max_seq) * kv_dim + koff;
+        off = (size_t)ring_slot(win_start, t0, p.max_seq) * kv_dim + koff;
       } else {
         const int t = min(t0 + lc, ce - 1);
-        off = (size_t)ring_slot(p.start, t, p.max_seq) * kv_dim + 8 * lg;
+        off = (size_t)ring_slot(win_start, t, p.max_seq) * kv_dim + 8 * lg;
       }
     }
     const _Float16 *src = kbase + off;
@@ -139,14 +164,14 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
       bool linear;
       const int t0 = tile_row0(tt, linear);
       if (linear) {
-        row0 = (size_t)ring_slot(p.start, t0, p.max_seq) * kv_dim;
+        row0 = (size_t)ring_slot(win_start, t0, p.max_seq) * kv_dim;
 #pragma unroll
         for (int m = 0; m < 4; ++m) off[m] = voff[m];
       } else {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           const int t = min(t0 + 4 * lg + m, ce - 1);
-          off[m] = (size_t)ring_slot(p.start, t, p.max_seq) * kv_dim + 8 * lc;
+          off[m] = (size_t)ring_slot(win_start, t, p.max_seq) * kv_dim + 8 * lc;
         }
       }
     }
@@ -169,15 +194,17 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
     issue(buf[b], tix[b]);
   }
 
-  if (FUSED) {
+  if (rope_q) {
     if (tid < 64) {
       // angle = fl32(theta_inv[i] * pos) as vDSP_vsmul (mistral_model.h:87-88)
-      float ang = p.theta_inv[tid] * (float)p.pos;
+      float ang = p.theta_inv[tid] * (float)pos;
       float sn, cs;
       sincosf(ang, &sn, &cs);
       sm.cs[tid] = make_float2(cs, sn);
     }
     __syncthreads();
+  }
+  if (FUSED) {
     if (has_new && active) {
       // new k rotated (pair `lane`) and v, rounded to fp16 (mistral_model.h:854-857)
       float2 kv = *reinterpret_cast<const float2 *>(p.knew + (size_t)kvh * HD + 2 * lane);
@@ -204,13 +231,13 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   h8 qhi[4], qlo[4];
   {
     const bool col = lc < G;
-    const float *qsrc = p.q + (size_t)(kvh_c * G + (col ? lc : 0)) * HD + 8 * lg;
+    const float *qsrc = q_in + (size_t)(kvh_c * G + (col ? lc : 0)) * HD + 8 * lg;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const f4 *src = reinterpret_cast<const f4 *>(qsrc + 32 * s);
       f4 a = src[0], b = src[1];
       float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-      if (FUSED) {
+      if (rope_q) {
 #pragma unroll
         for (int pi = 0; pi < 4; ++pi) {
           float2 cs = sm.cs[16 * s + 4 * lg + pi];
@@ -325,7 +352,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
     for (int s = 0; s < 4; ++s) nb.k[s] = *reinterpret_cast<const u4 *>(&sm.knew[w][32 * s + 8 * lg]);
 #pragma unroll
     for (int m = 0; m < 4; ++m) nb.v[m] = *reinterpret_cast<const u4 *>(&sm.vnew[w][8 * lc]);
-    process(nb, p.L - 1, p.L, -1, std::false_type{});
+    process(nb, win_L - 1, win_L, -1, std::false_type{});
   }
 
   // Wave totals: l over the 4 key groups of column lc.
@@ -336,15 +363,16 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   // dim 8*(4*lg + i) + e.
   const size_t row = p.nchunk == 1 ? (size_t)kvh * G + lc
                                    : ((size_t)kvh * p.nchunk + chunk) * G + lc;
-  float *dst = (p.nchunk == 1 ? p.out : p.part_o) + row * HD + 32 * lg;
-  const float sc = p.nchunk == 1 ? 1.0f / l_part : 1.0f;
+  float *dst = (p.nchunk == 1 ? out : part_o) + row * HD + 32 * lg;
+  // (an empty window, only in kPositions, writes zeros)
+  const float sc = p.nchunk == 1 ? (l_part > 0.f ? 1.0f / l_part : 0.f) : 1.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     *reinterpret_cast<f4 *>(dst + 8 * i) = f4{o[0][i], o[1][i], o[2][i], o[3][i]} * sc;
     *reinterpret_cast<f4 *>(dst + 8 * i + 4) = f4{o[4][i], o[5][i], o[6][i], o[7][i]} * sc;
   }
   if (p.nchunk > 1 && lg == 0)
-    *reinterpret_cast<float2 *>(p.part_ml + row * 2) = make_float2(m_lane, l_part);
+    *reinterpret_cast<float2 *>(part_ml + row * 2) = make_float2(m_lane, l_part);
 }
 
 // Cross-chunk log-sum-exp merge.  Workgroup = (kv head, q head, block of
@@ -369,7 +397,9 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
   const int kvh = hg / G, g = hg % G;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int cg = tid / kDW, d = kDW * db + (tid % kDW);
-  const size_t hb = (size_t)kvh * p.nchunk * G;
+  // token blockIdx.y (kPositions; 0 otherwise): its partials and output rows
+  const size_t tok = blockIdx.y;
+  const size_t hb = (size_t)kvh * p.nchunk * G + tok * p.n_kv * p.nchunk * G;
   float2 ml = make_float2(-INFINITY, 0.f);
   if (tid < p.nchunk) ml = *reinterpret_cast<const float2 *>(p.part_ml + (hb + (size_t)tid * G + g) * 2);
   float ov[kPer];
@@ -404,14 +434,15 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
 #pragma unroll
     for (int k = 0; k < kCG; ++k) t += red[k][tid];
     const float Ls = lsum[0] + lsum[1] + lsum[2] + lsum[3];
-    p.out[(size_t)hg * HD + d] = t / Ls;
+    // (Ls = 0 only for an empty window: zeros)
+    p.out[(tok * p.n_kv * G + hg) * HD + d] = Ls > 0.f ? t / Ls : 0.f;
   }
 }
 
 }  // namespace
 
-size_t decode_scratch_bytes(int n_kv, int g, int nchunk) {
-  return (size_t)n_kv * nchunk * g * (HD + 2) * sizeof(float);
+size_t decode_scratch_bytes(int n_kv, int g, int nchunk, int n_tok) {
+  return (size_t)n_tok * n_kv * nchunk * g * (HD + 2) * sizeof(float);
 }
 
 int decode_pick_nchunk(int L, int n_kv, int target_wgs) {
@@ -425,20 +456,28 @@ int decode_pick_nchunk(int L, int n_kv, int target_wgs) {
   return nchunk;
 }
 
-hipError_t launch_decode(const DecodeParams &p, int g, bool fused, hipStream_t s, hipEvent_t ev0,
+hipError_t launch_decode(const DecodeParams &p, int g, int mode, hipStream_t s, hipEvent_t ev0,
                          hipEvent_t ev1) {
   if (g != G) return hipErrorInvalidValue;
   if (p.nchunk < 1 || p.nchunk > kMaxChunks) return hipErrorInvalidValue;
-  dim3 grid(((p.n_kv + kWaves - 1) / kWaves) * p.nchunk), block(kThreads);
-  if (fused)
-    hipExtLaunchKernelGGL(decode_kernel<true>, grid, block, 0, s, ev0, ev1, 0, p);
+  const bool positions = mode == kDecodePositions;
+  if (positions && (p.positions == nullptr || p.n_tok < 1 || p.n_tok > 65535))
+    return hipErrorInvalidValue;
+  dim3 grid(((p.n_kv + kWaves - 1) / kWaves) * p.nchunk, positions ? p.n_tok : 1), block(kThreads);
+  if (mode == kDecodeFused)
+    hipExtLaunchKernelGGL(decode_kernel<kFused>, grid, block, 0, s, ev0, ev1, 0, p);
+  else if (positions)
+    hipExtLaunchKernelGGL(decode_kernel<kPositions>, grid, block, 0, s, ev0, ev1, 0, p);
   else
-    hipExtLaunchKernelGGL(decode_kernel<false>, grid, block, 0, s, ev0, ev1, 0, p);
+    hipExtLaunchKernelGGL(decode_kernel<kPlain>, grid, block, 0, s, ev0, ev1, 0, p);
   return hipGetLastError();
 }
 
 hipError_t launch_decode_merge(const DecodeParams &p, hipStream_t s) {
-  if (p.nchunk > 1) hipLaunchKernelGGL(decode_merge_kernel, dim3(p.n_kv * G * (HD / kMergeDims)), dim3(256), 0, s, p);
+  const int ntok = p.positions != nullptr ? p.n_tok : 1;
+  if (p.nchunk > 1)
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(p.n_kv * G * (HD / kMergeDims), ntok), dim3(256),
+                       0, s, p);
   return hipGetLastError();
 }
 

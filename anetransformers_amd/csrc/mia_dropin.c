@@ -199,6 +199,51 @@ void mia_dropin_attention_batch(const float *Q, float *attn_out, const KVCache *
     TRY("attention_batch", mia_memcpy_d2h(attn_out, dout, nb));
 }
 
+void mia_dropin_prefill_chunk_attention(KVCache *kv, int layer, const float *Q, const float *K,
+                                        const float *V, const int *positions, int chunk_size,
+                                        const float *theta_inv, int n_heads, int n_kv_heads,
+                                        float *attn_out) {
+    const char *what = "prefill_chunk_attention";
+    g_status = 0;
+    if (layer < 0 || layer >= kv->n_layers || chunk_size <= 0 || n_heads <= 0 ||
+        n_kv_heads <= 0 || n_kv_heads * kv->head_dim != kv->kv_dim) {
+        fail(MIA_ERR_INVALID, what);
+        return;
+    }
+    for (int i = 0; i < chunk_size; i++)
+        if (positions[i] < 0) {
+            fail(MIA_ERR_INVALID, "prefill_chunk_attention (negative position)");
+            return;
+        }
+    int hd = kv->head_dim;
+    size_t qb = (size_t)chunk_size * n_heads * hd * sizeof(float);
+    size_t kb = (size_t)chunk_size * kv->kv_dim * sizeof(float);
+    size_t tb = (size_t)(hd / 2) * sizeof(float);
+    size_t pb = (size_t)chunk_size * sizeof(int);
+    size_t a = align256(qb), b = align256(kb), t = align256(tb), pp = align256(pb);
+    TRY(what, dbuf(2 * a + 2 * b + t + pp));
+    float *dq = (float *)g_dbuf;
+    float *dk = (float *)(g_dbuf + a);
+    float *dv = (float *)(g_dbuf + a + b);
+    float *dt = (float *)(g_dbuf + a + 2 * b);
+    int *dp = (int *)(g_dbuf + a + 2 * b + t);
+    float *dout = (float *)(g_dbuf + a + 2 * b + t + pp);
+    TRY(what, mia_memcpy_h2d(dq, Q, qb));
+    TRY(what, mia_memcpy_h2d(dk, K, kb));
+    TRY(what, mia_memcpy_h2d(dv, V, kb));
+    TRY(what, mia_memcpy_h2d(dt, theta_inv, tb));
+    TRY(what, mia_memcpy_h2d(dp, positions, pb));
+    size_t lay = (size_t)layer * kv->max_seq * kv->kv_dim;
+    TRY(what, mia_attention_chunk(dq, dk, dv, dp, dt, (uint16_t *)(kv->k_cache + lay),
+                                  (uint16_t *)(kv->v_cache + lay), dout, n_heads, n_kv_heads, hd,
+                                  kv->max_seq, chunk_size, NULL));
+    TRY(what, mia_stream_sync(NULL));
+    TRY(what, mia_memcpy_d2h(attn_out, dout, qb));
+    /* mistral_model.h:952, per token */
+    for (int i = 0; i < chunk_size; i++)
+        if (kv->len < kv->max_seq && positions[i] + 1 > kv->len) kv->len = positions[i] + 1;
+}
+
 /* Staged verify rows: [n_layers][S][kv_dim] fp16 K, then the same for V, for
  * one batch of drafts (start_pos, S) at a time. */
 static uint16_t *g_stage = NULL;

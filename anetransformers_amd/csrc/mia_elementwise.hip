@@ -100,6 +100,60 @@ __global__ void __launch_bounds__(128)
   }
 }
 
+// Phase 1 of the chunked prefill for K / V (mistral/mistral_model.h:935-955):
+// one workgroup of 128 threads per token t.  k is rotated at positions[t]
+// (angles fl32(theta_inv[i] * pos), mistral_model.h:87-105), k and v are
+// rounded to fp16 and written to slot positions[t] % max_seq -- unless a
+// later token of the chunk takes the same slot: the reference writes the
+// tokens in order, so that later token is what the slot keeps.
+__global__ void __launch_bounds__(128)
+    rope_kv_positions_kernel(const float *K, const float *V, const float *theta_inv,
+                             const int *positions, int S, int n_kv, _Float16 *kc, _Float16 *vc,
+                             int max_seq) {
+  __shared__ float2 cs[HD / 2];
+  __shared__ int overwritten;
+  const int t = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int pos = positions[t];
+  if (pos < 0) return;  // no slot (the attention gives such a token a zero row)
+  const int slot = pos % max_seq;
+  if (tid == 0) overwritten = 0;
+  __syncthreads();
+  for (int u = t + 1 + tid; u < S; u += blockDim.x) {
+    const int pu = positions[u];
+    if (pu >= 0 && pu % max_seq == slot) overwritten = 1;
+  }
+  if (tid < HD / 2) {
+    const float ang = theta_inv[tid] * (float)pos;
+    float sn, c;
+    sincosf(ang, &sn, &c);
+    cs[tid] = make_float2(c, sn);
+  }
+  __syncthreads();
+  if (overwritten) return;  // workgroup-uniform
+  const int kv_dim = n_kv * HD;
+  for (int c = tid; c < n_kv * (HD / 8); c += blockDim.x) {
+    const int e0 = (c >> 4) * HD + 8 * (c & 15);
+    const f4 *ks = reinterpret_cast<const f4 *>(K + (size_t)t * kv_dim + e0);
+    const f4 *vs = reinterpret_cast<const f4 *>(V + (size_t)t * kv_dim + e0);
+    const f4 k0 = ks[0], k1 = ks[1], v0 = vs[0], v1 = vs[1];
+    float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    const int p0 = 4 * (c & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float2 q = cs[p0 + i];
+      rope_pair(kk[2 * i], kk[2 * i + 1], q.x, q.y);
+    }
+    h8 kh, vh;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kh[i] = (_Float16)kk[i];
+    vh[0] = (_Float16)v0.x; vh[1] = (_Float16)v0.y; vh[2] = (_Float16)v0.z; vh[3] = (_Float16)v0.w;
+    vh[4] = (_Float16)v1.x; vh[5] = (_Float16)v1.y; vh[6] = (_Float16)v1.z; vh[7] = (_Float16)v1.w;
+    *reinterpret_cast<h8 *>(kc + (size_t)slot * kv_dim + e0) = kh;
+    *reinterpret_cast<h8 *>(vc + (size_t)slot * kv_dim + e0) = vh;
+  }
+}
+
 // mistral/mistral_ane_prefill.h:189-204: cvt + kv_write at (start+t) % M.
 // The reference writes the tokens in order, so with S > M a slot keeps the
 // last token written to it: tokens t < S - M are overwritten and skipped here
@@ -204,6 +258,15 @@ hipError_t launch_kv_write(_Float16 *kc, _Float16 *vc, const float *K, const flo
   int bx = (kv_dim + 255) / 256;
   hipLaunchKernelGGL(kv_write_kernel, dim3(bx, S), dim3(256), 0, s, kc, vc, K, V, S, start_pos,
                      max_seq, kv_dim);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_kv_positions(const float *K, const float *V, const float *theta_inv,
+                                    const int *positions, int S, int n_kv, _Float16 *kc,
+                                    _Float16 *vc, int max_seq, hipStream_t s) {
+  if (S <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_kv_positions_kernel, dim3(S), dim3(128), 0, s, K, V, theta_inv,
+                     positions, S, n_kv, kc, vc, max_seq);
   return hipGetLastError();
 }
 

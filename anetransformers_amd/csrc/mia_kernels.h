@@ -34,14 +34,20 @@ struct DecodeParams {
   int n_kv;
   int nchunk;              // workgroups per kv head (chunks of whole 16-key tiles)
   float qscale;            // (1/sqrt(128)) * log2(e)
+  // kDecodePositions: n_tok tokens, token t at positions[t] (device int32);
+  // q, out [n_tok][n_kv*G][128], partials per token; pos / L / start unused.
+  // theta_inv set: q is rotated in-kernel at the token's position.
+  const int *positions;
+  int n_tok;
 };
+enum { kDecodePlain = 0, kDecodeFused = 1, kDecodePositions = 2 };
 
 // Scratch needed by launch_decode for a given shape (bytes of part_o+part_ml).
-size_t decode_scratch_bytes(int n_kv, int G, int nchunk);
+size_t decode_scratch_bytes(int n_kv, int G, int nchunk, int n_tok = 1);
 int decode_pick_nchunk(int L, int n_kv, int target_wgs);
 // Main kernel only; launch_decode_merge adds the cross-chunk merge (nchunk > 1).
 // ev0/ev1 (may be null) are stamped at the kernel's start and end.
-hipError_t launch_decode(const DecodeParams &p, int G, bool fused, hipStream_t s, hipEvent_t ev0,
+hipError_t launch_decode(const DecodeParams &p, int G, int mode, hipStream_t s, hipEvent_t ev0,
                          hipEvent_t ev1);
 hipError_t launch_decode_merge(const DecodeParams &p, hipStream_t s);
 
@@ -86,6 +92,13 @@ hipError_t launch_rope_to_ring(const float *K, const float *V, const float *thet
                                float *cs_out, hipStream_t s);
 hipError_t launch_kv_write(_Float16 *kc, _Float16 *vc, const float *K, const float *V, int S,
                            int start_pos, int max_seq, int kv_dim, hipStream_t s);
+// The chunked prefill's phase 1 (mistral_model.h:935-955) for the K / V side:
+// token t's k rotated at positions[t] (device int32), k and v rounded to fp16
+// and written to slot positions[t] % max_seq unless a later token of the
+// chunk takes the same slot (the reference's in-order writes leave the last).
+hipError_t launch_rope_kv_positions(const float *K, const float *V, const float *theta_inv,
+                                    const int *positions, int S, int n_kv, _Float16 *kc,
+                                    _Float16 *vc, int max_seq, hipStream_t s);
 // Staged rows 0..S-1 -> ring slots (start_pos + t) % max_seq, for n_layers
 // layers ring_stride / stage_stride elements apart.
 hipError_t launch_commit(_Float16 *kc, _Float16 *vc, const _Float16 *kst, const _Float16 *vst,

@@ -113,6 +113,19 @@ void mia_dropin_verify_step(KVCache *kv, int layer, const float *Q, const float 
                             int start_pos, int S, const float *theta_inv, int n_heads,
                             int n_kv_heads, float *out);
 
+/* The attention of mistral_layer_prefill_chunk (mistral/mistral_model.h:
+ * 908-1075) for one layer: every token's q and k rotated at positions[i], k / v
+ * written to slot positions[i] % max_seq (in order: a later token in the same
+ * slot wins) with the len update of :952, then each token attends its window
+ * over the ring as written (phase 2, :961-1044).  Q, K, V [chunk_size][...]
+ * host fp32 raw projections (not modified), positions host int (>= 0),
+ * attn_out [chunk_size][n_heads*head_dim] host.  The projections, Wo and the
+ * FFN around it stay with the caller. */
+void mia_dropin_prefill_chunk_attention(KVCache *kv, int layer, const float *Q, const float *K,
+                                        const float *V, const int *positions, int chunk_size,
+                                        const float *theta_inv, int n_heads, int n_kv_heads,
+                                        float *attn_out);
+
 /* Speculative verify with accept-only commit (mistral/speculative.h:81-105,
  * 242-341): mia_dropin_verify_stage runs one layer's attention for the S
  * verify tokens like mia_dropin_verify_step but leaves the ring untouched,

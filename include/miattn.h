@@ -135,6 +135,29 @@ int mia_attention_batch(const float *Q, float *out, const uint16_t *k_layer,
                         const uint16_t *v_layer, int n_heads, int n_kv_heads, int hd,
                         int max_seq, int start_pos, int S, void *stream);
 
+/* Attention of S tokens, each at its own position over the ring as it
+ * stands: token t attends the window [pos-L+1, pos], L = min(pos+1, max_seq),
+ * pos = positions[t] -- phase 2 of mistral_layer_prefill_chunk
+ * (mistral/mistral_model.h:961-1044), which is gqa_attention_neon per token.
+ * Q [S][n_heads*128] fp32 dev, rotated; positions [S] int32 dev (any order,
+ * >= 0; a negative position gives a zero row); out [S][n_heads*128].
+ * 1 <= S <= 65535.  Each token reads its own window, so contiguous runs of
+ * positions are cheaper through mia_attention_batch. */
+int mia_attention_positions(const float *Q, float *out, const uint16_t *k_layer,
+                            const uint16_t *v_layer, const int *positions, int n_heads,
+                            int n_kv_heads, int hd, int max_seq, int S, void *stream);
+
+/* The attention of mistral_layer_prefill_chunk (mistral/mistral_model.h:
+ * 908-1075), phases 1 and 2: every token's k rotated at positions[t], k and v
+ * rounded to fp16 and written to slot positions[t] % max_seq (in token order:
+ * a later token in the same slot wins), then mia_attention_positions over the
+ * ring so written, with q rotated at positions[t].  Q [S][n_heads*128], K, V
+ * [S][n_kv_heads*128] raw fp32 dev (not modified); theta_inv [64] dev.  The
+ * caller keeps the len bookkeeping (mistral_model.h:952). */
+int mia_attention_chunk(const float *Q, const float *K, const float *V, const int *positions,
+                        const float *theta_inv, uint16_t *k_layer, uint16_t *v_layer, float *out,
+                        int n_heads, int n_kv_heads, int hd, int max_seq, int S, void *stream);
+
 /* S tokens through steps 4-6 with sequential semantics: the result equals S
  * calls of mia_decode_step at start_pos, start_pos+1, ... (the verify loop of
  * mistral/speculative.h:92-101), also when the ring has wrapped: drafts are

@@ -426,6 +426,38 @@ void ora_verify_steps(OraKV *kv, int layer, float *Q, float *K, const float *V, 
                         n_kv_heads, att, out + (size_t)t * dim);
 }
 
+/* mistral/mistral_model.h:908-1075, phases 1 and 2 without the projections,
+ * Wo and the FFN.  Phase 2's loop body (:961-1044: q pre-scaled by
+ * 1/sqrtf(hd), the four-accumulator dot, softmax_vec, the zero-skipping AV)
+ * is the arithmetic of gqa_attention_neon (:362-487), restated above as
+ * ora_gqa_attention. */
+void ora_prefill_chunk_attention(OraKV *kv, int layer, float *Q, float *K, const float *V,
+                                 const int *positions, int S, const float *theta_inv,
+                                 int n_heads, int n_kv_heads, float *att, float *out) {
+    int hd = kv->head_dim;
+    int kv_dim = kv->kv_dim;
+    int dim = n_heads * hd;
+    int max_seq = kv->max_seq;
+    uint16_t *k16 = (uint16_t *)malloc((size_t)kv_dim * sizeof(uint16_t));
+    uint16_t *v16 = (uint16_t *)malloc((size_t)kv_dim * sizeof(uint16_t));
+    for (int ti = 0; ti < S; ti++) { /* phase 1, :935-955 */
+        int pos = positions[ti];
+        float *qb = Q + (size_t)ti * dim;
+        float *kb = K + (size_t)ti * kv_dim;
+        ora_apply_rope(qb, kb, pos, theta_inv, n_heads, n_kv_heads, hd); /* :946 */
+        ora_cvt_f32_to_f16(kb, k16, kv_dim);                              /* :949-950 */
+        ora_cvt_f32_to_f16(V + (size_t)ti * kv_dim, v16, kv_dim);
+        ora_kv_write(kv, layer, pos % max_seq, k16, v16);                 /* :951 */
+        if (kv->len < max_seq && pos + 1 > kv->len) kv->len = pos + 1;   /* :952 */
+    }
+    free(k16);
+    free(v16);
+    for (int ti = 0; ti < S; ti++) /* phase 2, :961-1044 */
+        ora_gqa_attention(Q + (size_t)ti * dim, att, out + (size_t)ti * dim, ora_kv_k(kv, layer),
+                          ora_kv_v(kv, layer), n_heads, n_heads / n_kv_heads, hd, max_seq,
+                          positions[ti]);
+}
+
 /* tests/test_cpu_ref.h:113-147 */
 void ora_ref_gqa_attention(float *out, const float *q, const float *k, const float *v, int S,
                            int n_heads, int n_kv_heads, int head_dim) {

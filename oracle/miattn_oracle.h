@@ -23,6 +23,9 @@
  *                                     steps (unwrapped), textbook causal    pinned
  *   ora_ref_gqa_attention             float64 brute force                   pinned
  *   ora_decode_step / ora_verify_steps  compositions of the above           pinned
+ *   ora_prefill_chunk_attention       == sequential steps (unwrapped, in
+ *                                     order), float64 brute force over the
+ *                                     final ring for any positions          pinned
  * The transcendental boundary (Accelerate vvsincosf / vvexpf, replaced here by
  * libm sinf/cosf/expf) is parity-unpinned: no reference test fixes those
  * outputs; ulp-level differences are inside the attention tolerance.
@@ -107,6 +110,17 @@ void ora_decode_step(OraKV *kv, int layer, float *q, float *k, const float *v, i
 void ora_verify_steps(OraKV *kv, int layer, float *Q, float *K, const float *V, int start_pos,
                       int S, const float *theta_inv, int n_heads, int n_kv_heads, float *att,
                       float *out);
+
+/* mistral/mistral_model.h:908-1075, the attention of the chunked prefill
+ * layer: phase 1 (:935-955) rotates q and k of every token at positions[t],
+ * writes fp16 k / v to slot positions[t] % max_seq in token order (a later
+ * token in the same slot wins) and updates len; phase 2 (:961-1044) attends
+ * every token over the ring as phase 1 left it, at pos = positions[t].  Q, K
+ * [S][...] raw fp32, overwritten (Q ends rotated and pre-scaled, as Q_all).
+ * The projections, Wo and the FFN of that function are not part of this. */
+void ora_prefill_chunk_attention(OraKV *kv, int layer, float *Q, float *K, const float *V,
+                                 const int *positions, int S, const float *theta_inv,
+                                 int n_heads, int n_kv_heads, float *att, float *out);
 
 /* tests/test_cpu_ref.h:113-147: textbook causal GQA over contiguous
  * [S][n_kv][hd] K/V starting at position 0. */

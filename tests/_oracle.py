@@ -56,6 +56,10 @@ _SIGS = {
         [POINTER(OraKV), c_int, _P, _P, _P, c_int, c_int, _P, c_int, c_int, _P, _P],
     ),
     "ora_ref_gqa_attention": (None, [_P, _P, _P, _P, c_int, c_int, c_int, c_int]),
+    "ora_prefill_chunk_attention": (
+        None,
+        [POINTER(OraKV), c_int, _P, _P, _P, _P, c_int, _P, c_int, c_int, _P, _P],
+    ),
     "ora_decode_layers": (
         None,
         [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
@@ -207,6 +211,22 @@ def verify_steps(kc, vc, Q, K, V, start_pos, S, th, n_heads, n_kv, hd, max_seq):
     load().ora_verify_steps(ctypes.byref(kv), 0, _p(QQ), _p(KK), _p(VV), start_pos, S, _p(th),
                             n_heads, n_kv, _p(att), _p(out))
     return out
+
+
+def prefill_chunk_attention(kc, vc, Q, K, V, positions, th, n_heads, n_kv, hd, max_seq):
+    """Phases 1 + 2 of mistral_layer_prefill_chunk on copies of Q/K; kc/vc
+    updated.  Returns (out, len)."""
+    kv = make_kv(kc, vc, n_kv, hd, max_seq)
+    QQ = np.array(Q, dtype=np.float32, copy=True)
+    KK = np.array(K, dtype=np.float32, copy=True)
+    VV = np.ascontiguousarray(V, dtype=np.float32)
+    P = np.ascontiguousarray(positions, dtype=np.int32)
+    S = len(P)
+    att = np.zeros(n_heads * max_seq, dtype=np.float32)
+    out = np.empty((S, n_heads * hd), dtype=np.float32)
+    load().ora_prefill_chunk_attention(ctypes.byref(kv), 0, _p(QQ), _p(KK), _p(VV), _p(P), S,
+                                       _p(th), n_heads, n_kv, _p(att), _p(out))
+    return out, kv.len
 
 
 def ref_gqa_attention(q, k, v, S, n_heads, n_kv, hd):

@@ -261,3 +261,31 @@ def test_binding_fails_loudly_without_library(tmp_path):
             mia.load(str(tmp_path / "nope.so"))
     finally:
         mia._lib = saved
+
+
+def test_positions_argument_errors_without_device_work():
+    lib = mia.load()
+    buf = np.zeros(64, np.float32)
+    p = buf.ctypes.data
+    pos = np.array([3, 4], np.int32)
+    pp = pos.ctypes.data
+    assert lib.mia_attention_positions(p, p, p, p, None, 32, 8, 128, 64, 2, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_attention_positions(p, p, p, p, pp, 32, 8, 128, 64, 0, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_attention_positions(p, p, p, p, pp + 2, 32, 8, 128, 64, 2,
+                                       None) == mia.MIA_ERR_INVALID
+    assert lib.mia_attention_positions(p, p, p, p, pp, 32, 8, 64, 64, 2,
+                                       None) == mia.MIA_ERR_UNSUPPORTED
+    assert lib.mia_attention_chunk(p, p, p, pp, None, p, p, p, 32, 8, 128, 64, 2,
+                                   None) == mia.MIA_ERR_INVALID
+    assert lib.mia_attention_chunk(p + 4, p, p, pp, p, p, p, p, 32, 8, 128, 64, 2,
+                                   None) == mia.MIA_ERR_INVALID          # Q not 16-byte aligned
+    lib.mia_dropin_set_abort(0)
+    try:
+        kv = mia.KVCache()
+        kv.n_layers, kv.n_kv_heads, kv.head_dim, kv.kv_dim, kv.max_seq = 1, 8, 128, 1024, 64
+        neg = np.array([5, -2], np.int32)
+        lib.mia_dropin_prefill_chunk_attention(ctypes.byref(kv), 0, p, p, p, neg.ctypes.data, 2,
+                                               p, 32, 8, p)
+        assert lib.mia_dropin_status() == mia.MIA_ERR_INVALID
+    finally:
+        lib.mia_dropin_set_abort(1)

@@ -308,3 +308,88 @@ def test_verify_steps_wrapped_window_float64():
         qrot = D.rope_f64(Q[t], pos, th, 32, 128)
         ref = D.gqa_decode_f64(qrot, ktab, vtab, 32, 8, 128, M, pos)
         assert np.max(np.abs(out[t] - ref)) < 1e-5, t
+
+
+# ------------------------------------------- chunked prefill (positions) --
+
+def _chunk_inputs(g, S):
+    return D.normal(g, (S, 4096)), D.normal(g, (S, 1024)), D.normal(g, (S, 1024))
+
+
+def test_prefill_chunk_contiguous_equals_sequential_steps():
+    # mistral_prefill's positions start + i (mistral_model.h:1089) on a ring
+    # that does not wrap: phase 2 sees no later token in any window, so the
+    # chunk is the verify loop's sequence of decode steps, bit for bit.
+    g = D.rng(17)
+    M, start, S = 128, 40, 32
+    kc, vc = D.ring(g, M, filled=start)
+    th = O.theta_inv(1e6, 128)
+    Q, K, V = _chunk_inputs(g, S)
+    kc1, vc1, kc2, vc2 = kc.copy(), vc.copy(), kc.copy(), vc.copy()
+    out1, ln = O.prefill_chunk_attention(kc1, vc1, Q, K, V, np.arange(start, start + S), th, 32,
+                                         8, 128, M)
+    out2 = O.verify_steps(kc2, vc2, Q, K, V, start, S, th, 32, 8, 128, M)
+    assert np.array_equal(out1, out2)
+    assert np.array_equal(kc1, kc2) and np.array_equal(vc1, vc2)
+    assert ln == start + S
+
+
+@pytest.mark.parametrize("M,positions", [
+    (64, [100, 130, 101, 37, 500]),      # unsorted; 130 lands in the window of 100
+    (64, [10, 74, 11, 138]),             # 10, 74 and 138 share slot 10: the last wins
+    (256, [0, 1, 2, 255, 3]),            # an unwrapped run plus a far token
+    (48, [1000, 999, 998, 997]),         # descending on a wrapped ring
+])
+def test_prefill_chunk_positions_float64(M, positions):
+    # Phase 1 writes every token (token order, last writer wins per slot),
+    # then phase 2 attends each token's window [pos-L+1, pos] over that final
+    # ring: float64 attention on the rotated q against the final ring, whose
+    # rows are checked separately (V bit-exact, K the rounded rotation).
+    g = D.rng(18 + M + len(positions))
+    positions = np.asarray(positions)
+    S = len(positions)
+    kc, vc = D.ring(g, M)
+    th = O.theta_inv(1e6, 128)
+    Q, K, V = _chunk_inputs(g, S)
+    kc2, vc2 = kc.copy(), vc.copy()
+    out, ln = O.prefill_chunk_attention(kc2, vc2, Q, K, V, positions, th, 32, 8, 128, M)
+    owner = {}
+    for t, p in enumerate(positions):
+        owner[int(p) % M] = t
+    vt = vc.copy()
+    for slot, t in owner.items():
+        vt[slot] = D.to_f16_bits(V[t])
+    assert np.array_equal(vc2, vt)
+    slots = np.array(sorted(owner))
+    D.check_rotated_k(kc2[slots], K[[owner[s] for s in slots]],
+                      positions[[owner[s] for s in slots]], th, what="chunk ring")
+    others = np.setdiff1d(np.arange(M), slots)
+    assert np.array_equal(kc2[others], kc[others])
+    for t, p in enumerate(positions):
+        qrot = D.rope_f64(Q[t], int(p), th, 32, 128)
+        ref = D.gqa_decode_f64(qrot, kc2, vc2, 32, 8, 128, M, int(p))
+        assert np.max(np.abs(out[t] - ref)) < 1e-5, (t, p)
+    # len bookkeeping of mistral_model.h:952 (it can pass max_seq once; never
+    # read by the attention)
+    want = 0
+    for p in positions:
+        if want < M and p + 1 > want:
+            want = int(p) + 1
+    assert ln == want
+
+
+def test_prefill_chunk_sees_later_tokens_in_recycled_slots():
+    # The write-all-then-attend order differs from sequential steps exactly
+    # when a later token's slot falls in an earlier token's window: token 0
+    # (position 100, window 37..100 on a 64-slot ring) sees position 130 in
+    # slot 2, where sequential steps would still hold position 66.
+    g = D.rng(19)
+    M, positions = 64, np.array([100, 130])
+    kc, vc = D.ring(g, M)
+    th = O.theta_inv(1e6, 128)
+    Q, K, V = _chunk_inputs(g, 2)
+    V[1] = 50.0
+    K[1] = 0.0
+    out, _ = O.prefill_chunk_attention(kc.copy(), vc.copy(), Q, K, V, positions, th, 32, 8, 128, M)
+    seq = O.verify_steps(kc.copy(), vc.copy(), Q, K, V, 100, 1, th, 32, 8, 128, M)
+    assert np.max(np.abs(out[0] - seq[0])) > 1e-2
