@@ -231,9 +231,11 @@ __device__ __forceinline__ void mfma_pv(f16v &acc, const h8 &a, const h8 &b) {
   asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 // acc = 0 through the MFMA itself (0 x 0 + 0), so the accumulators are only
-// ever written by AGPR-destination MFMAs.
+// ever written by AGPR-destination MFMAs.  The leading wait states cover a
+// VALU write of z just before (a reload of the zero operand, for instance),
+// which the hazard recognizer does not see inside inline assembly.
 __device__ __forceinline__ void mfma_zero(f16v &acc, const h8 &z) {
-  asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %1, 0" : "=a"(acc) : "v"(z));
+  asm volatile("s_nop 4\n\tv_mfma_f32_32x32x16_f16 %0, %1, %1, 0" : "=a"(acc) : "v"(z));
 }
 // Before VALU reads of accumulators written by mfma_pv: the MFMA result
 // latency (wait states the compiler cannot see), and a data dependence on
@@ -244,6 +246,18 @@ __device__ __forceinline__ void pv_drain(f16v (&o)[NB][4]) {
   for (int b = 0; b < NB; ++b)
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
                  : "+a"(o[b][0]), "+a"(o[b][1]), "+a"(o[b][2]), "+a"(o[b][3]));
+}
+
+// The same for both row blocks of a 64-row wave with one set of wait states
+// (24, more than an 8-pass MFMA's result latency).
+template <int NB>
+__device__ __forceinline__ void pv_drain_all(f16v (&o)[NB][4]) {
+  if constexpr (NB == 2)
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+                 : "+a"(o[0][0]), "+a"(o[0][1]), "+a"(o[0][2]), "+a"(o[0][3]), "+a"(o[1][0]),
+                   "+a"(o[1][1]), "+a"(o[1][2]), "+a"(o[1][3]));
+  else
+    pv_drain<NB>(o);
 }
 
 // Combine the two key halves of a row (lanes l and l^32).  ds_bpermute via
@@ -280,19 +294,14 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   const int ks = klo + split * p.split_keys;
   const int ke = min(ks + p.split_keys, khi + 1);
   const int nt = ke > ks ? (ke - ks + kKT - 1) / kKT : 0;
-  // When the range ends at the causal edge, its last key group holds the
-  // masked tiles, the short last tile with its per-lane loads and the keys
-  // just written by the K rotation, about two plain tiles' worth: the range
-  // is then split as if it had two tiles more, the last group's share ending
-  // at the real end.
-  const int extra = ke == khi + 1 ? 2 : 0;
-  auto group_start = [&](int g) {
-    return g == kWaves ? nt : min(nt, (int)((long)g * (nt + extra) / kWaves));
-  };
-  const int g_first = group_start(w);
-  const int g_count = group_start(w + 1) - g_first;
-  const int kb0 = ks + kKT * g_first;
-  constexpr int kStride = kKT;
+  // Key groups interleaved by tile: wave w takes tiles w, w + 4, w + 8, ...
+  // of the range.  The waves then share the masked tiles at the causal edge
+  // evenly, and every row tile of a kv head walks the same keys in the same
+  // order, so its first tiles (and most later ones) are L2 hits after the
+  // first workgroup of the head has fetched them.
+  const int g_count = nt > w ? (nt - w + kWaves - 1) / kWaves : 0;
+  const int kb0 = ks + kKT * w;
+  constexpr int kStride = kKT * kWaves;
 
   // This lane's row in each 32-row block and its window; block-uniform bounds
   // (keys in [lo_max, hi_min] are inside every row's window of the block).
@@ -351,17 +360,38 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   const _Float16 *const kc = p.kc, *const vc = p.vc;
   const _Float16 *const kst = p.kstage, *const vst = p.vstage;
   auto tile_slot = [&](int i) { return (kb0 + kStride * i) % p.max_seq; };
+  // Ring slots of the next K and V tiles to load, advanced by one stride per
+  // load (no division in the tile loop).
+  int kslot = 0, vslot = 0;
+  auto advance = [&](int s) {
+    s += kStride;
+    return s < p.max_seq ? s : (s - p.max_seq < p.max_seq ? s - p.max_seq : s % p.max_seq);
+  };
 #define MIA_LOAD_K(i, buf)                                                                  \
   load_tile(kc, kst, kb0 + kStride * (i), tile_slot(i), ke, p.start_pos, p.max_seq, kv_dim, \
             kvh * HD, boff, lane, kt_a[buf])
 #define MIA_LOAD_V(i, buf)                                                                  \
   load_tile(vc, vst, kb0 + kStride * (i), tile_slot(i), ke, p.start_pos, p.max_seq, kv_dim, \
             kvh * HD, boff, lane, vt_a[buf])
+#define MIA_LOAD_K_NEXT(i, buf)                                                            \
+  do {                                                                                     \
+    load_tile(kc, kst, kb0 + kStride * (i), kslot, ke, p.start_pos, p.max_seq, kv_dim,     \
+              kvh * HD, boff, lane, kt_a[buf]);                                            \
+    kslot = advance(kslot);                                                                \
+  } while (0)
+#define MIA_LOAD_V_NEXT(i, buf)                                                            \
+  do {                                                                                     \
+    load_tile(vc, vst, kb0 + kStride * (i), vslot, ke, p.start_pos, p.max_seq, kv_dim,     \
+              kvh * HD, boff, lane, vt_a[buf]);                                            \
+    vslot = advance(vslot);                                                                \
+  } while (0)
   // K0, K1, then V0: V(i) is first needed one step after K(i+1).
   auto issue_first_tiles = [&]() {
     if (g_count > 0) MIA_LOAD_K(0, 0);
     if (g_count > 1) MIA_LOAD_K(1, 1);
     if (g_count > 0) MIA_LOAD_V(0, 0);
+    kslot = tile_slot(2);
+    vslot = tile_slot(1);
   };
   // Q rows -> fp16 in LDS: RoPE (table of fl32(theta_inv[i] * pos) cos/sin
   // written by the K rotation, mistral_model.h:87-105) and the score scale
@@ -605,7 +635,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     for (int b = 0; b < NB; ++b) qk(0, b);
     fence();
     // K(it) was consumed by the previous step: its buffer takes K(it+2)
-    if (it + 2 < g_count) MIA_LOAD_K(it + 2, it & 1);
+    if (it + 2 < g_count) MIA_LOAD_K_NEXT(it + 2, it & 1);
     exp_slice(1);
     fence();
 #pragma unroll
@@ -663,7 +693,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     }
     if (it + 1 < g_count) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // V(it-1) reads done
-      MIA_LOAD_V(it + 1, (it + 1) & 1);
+      MIA_LOAD_V_NEXT(it + 1, (it + 1) & 1);
     }
     // Window mask of tile it+1, only where it crosses a window edge.
     const int kbn = kb0 + kStride * (it + 1);
@@ -691,6 +721,180 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pb[b][1]);
+  };
+
+  // NB = 2 (prefill): the same step as one MFMA per slot, 34 slots, each
+  // followed by one exponential of tile it (with its fp16 packing and row-sum
+  // work every second slot), so a 16-cycle transcendental issue sits under
+  // every 32-cycle MFMA instead of the exponentials queueing behind half of
+  // them.  All K and V^T operands of the step are read from LDS at its start.
+  // Scores and P live in two register sets that alternate between steps
+  // (s_in -> s_out, p_in -> p_out), so nothing is copied at the step's end.
+  auto step2 = [&](int it, auto with_pv, f16v(&s_in)[NB], f16v(&s_out)[NB], h8(&p_in)[NB][2],
+                   h8(&p_out)[NB][2]) {
+    const unsigned kab = ka_b[(it + 1) & 1];
+    const unsigned vab = va_b[(it + 1) & 1];
+    // Operands in halves, each read eight slots (~256 cycles) ahead of its
+    // first use: K k-steps 0-3 and V^T keys 0-15 now, k-steps 4-7 in slot 11,
+    // V^T keys 16-31 in slot 19 (into the registers the first halves free).
+    h8 ka[8], vlo[4], vhi[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) ka[st] = lds_read_h8(kab ^ (unsigned)(st << 5));
+    if (with_pv) {
+      vlo[0] = read_va<0, 0>(vab);
+      vlo[1] = read_va<0, 1>(vab);
+      vlo[2] = read_va<0, 2>(vab);
+      vlo[3] = read_va<0, 3>(vab);
+    }
+    fence();
+    float ls[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) ls[b] = l_run[b];
+    u4 pw[NB][2];
+    float ex[4];
+    // Element k of exponential slice j: score e = 4 (j % 4) + k of row block
+    // j / 4; odd k packs the pair (e-1, e) into fp16 and adds it to the sum.
+    // (The results are pinned where they are formed: they are only read at
+    // the step's end, and would otherwise be sunk there, behind the MFMAs.)
+    auto E = [&](int j, int k) {
+      const int b = j >> 2, e = 4 * (j & 3) + k;
+      ex[k] = fast_exp2(s_in[b][e]);
+      if (k & 1) {
+        const h2 pp = __builtin_convertvector((f2){ex[k - 1], ex[k]}, h2);
+        ls[b] = __builtin_amdgcn_fdot2(pp, ones, ls[b], false);
+        pw[b][e >> 3][((e - 1) & 7) >> 1] = __builtin_bit_cast(unsigned, pp);
+        asm volatile("" ::"v"(pp), "v"(ls[b]));
+      } else {
+        asm volatile("" ::"v"(ex[k]));
+      }
+    };
+    auto REF = [&](int b) {
+      f16v z;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) z[i] = 0.f;
+      s_out[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kx, qx[b], z, 0, 0, 0);
+    };
+    auto QK = [&](int st, int b) {
+      s_out[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st], s_out[b], 0, 0, 0);
+    };
+    auto PVL = [&](int db, int b) {
+      if (with_pv) mfma_pv(o[b][db], vlo[db], p_in[b][0]);
+    };
+    auto PVH = [&](int db, int b) {
+      if (with_pv) mfma_pv(o[b][db], vhi[db], p_in[b][1]);
+    };
+    // slots 1-10: reference k-steps and k-steps 0-3; exponential slices 0-2
+    REF(0); fence(); E(0, 0); fence();
+    REF(1); fence(); E(0, 1); fence();
+    QK(0, 0); fence(); E(0, 2); fence();
+    QK(0, 1); fence(); E(0, 3); fence();
+    // K(it) was consumed by the previous step: its buffer takes K(it+2)
+    QK(1, 0); fence(); E(1, 0);
+    if (it + 2 < g_count) MIA_LOAD_K_NEXT(it + 2, it & 1);
+    fence();
+    QK(1, 1); fence(); E(1, 1); fence();
+    QK(2, 0); fence(); E(1, 2); fence();
+    QK(2, 1); fence(); E(1, 3); fence();
+    QK(3, 0); fence(); E(2, 0); fence();
+    QK(3, 1); fence(); E(2, 1); fence();
+    // The P.V MFMAs are inline assembly, so the compiler does not know how
+    // long they read their V^T and P registers: a register whose last reader
+    // is one of them is kept alive (keep) past the next slot's MFMA, one MFMA
+    // duration later, before anything may be written into it.  Each slot's
+    // MFMA (and keep) is fenced off from its exponential, which the compiler
+    // would otherwise place first.
+    auto keep = [&](const h8 &x) {
+      if (with_pv) asm volatile("" ::"v"(x));
+    };
+    // slots 11-18: P.V of tile it-1, keys 0-15
+#pragma unroll
+    for (int st = 4; st < 8; ++st) ka[st] = lds_read_h8(kab ^ (unsigned)(st << 5));
+    PVL(0, 0); fence(); E(2, 2); fence();
+    PVL(0, 1); fence(); E(2, 3); fence();
+    PVL(1, 0); keep(vlo[0]); fence(); E(3, 0); fence();
+    PVL(1, 1); fence(); E(3, 1); fence();
+    PVL(2, 0); keep(vlo[1]); fence(); E(3, 2); fence();
+    PVL(2, 1); fence(); E(3, 3); fence();
+    PVL(3, 0); keep(vlo[2]); fence(); E(4, 0); fence();
+    PVL(3, 1); fence(); E(4, 1); fence();
+    // slots 19-26: k-steps 4-7
+    QK(4, 0);
+    keep(vlo[3]);
+    keep(p_in[0][0]);
+    keep(p_in[1][0]);
+    fence();
+    if (with_pv) {
+      vhi[0] = read_va<1, 0>(vab);
+      vhi[1] = read_va<1, 1>(vab);
+      vhi[2] = read_va<1, 2>(vab);
+      vhi[3] = read_va<1, 3>(vab);
+    }
+    E(4, 2); fence();
+    QK(4, 1); fence(); E(4, 3); fence();
+    QK(5, 0); fence(); E(5, 0); fence();
+    QK(5, 1); fence(); E(5, 1); fence();
+    QK(6, 0); fence(); E(5, 2); fence();
+    QK(6, 1); fence(); E(5, 3); fence();
+    QK(7, 0); fence(); E(6, 0); fence();
+    QK(7, 1); fence(); E(6, 1); fence();
+    // slots 27-34: P.V keys 16-31; V(it+1) goes into V(it-1)'s buffer once
+    // every LDS read of the step is done
+    PVH(0, 0); fence(); E(6, 2); fence();
+    PVH(0, 1); fence(); E(6, 3); fence();
+    PVH(1, 0); keep(vhi[0]); fence(); E(7, 0); fence();
+    PVH(1, 1); fence(); E(7, 1); fence();
+    PVH(2, 0); keep(vhi[1]); fence(); E(7, 2); fence();
+    PVH(2, 1); fence(); E(7, 3); fence();
+    PVH(3, 0);
+    keep(vhi[2]);
+    fence();
+    if (it + 1 < g_count) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      MIA_LOAD_V_NEXT(it + 1, (it + 1) & 1);
+    }
+    fence();
+    PVH(3, 1);
+    // The P.V MFMAs are inline assembly: the compiler neither sees that they
+    // write the accumulators nor pads what it places after them.  Wait for
+    // their results here, so that no register copy it may insert later (at
+    // a loop edge or a branch join) reads an accumulator still in flight.
+    if (with_pv) pv_drain_all(o);
+    fence();
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      l_run[b] = ls[b];
+      p_out[b][0] = __builtin_bit_cast(h8, pw[b][0]);
+      p_out[b][1] = __builtin_bit_cast(h8, pw[b][1]);
+    }
+    // Window mask of tile it+1, only where it crosses a window edge.
+    const int kbn = kb0 + kStride * (it + 1);
+    if (needs_mask(kbn)) mask_tile(s_out, kbn);
+  };
+  // O += P.V of the wave's last tile (its V in vt[(g_count-1)&1]) from P.
+  // The MFMAs are inline assembly, invisible to the compiler's hazard
+  // checks: the leading wait states keep them from reading P registers the
+  // step just wrote.
+  auto last_pv_of = [&](h8(&pl)[NB][2]) {
+    asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
+    const unsigned vab = va_b[(g_count - 1) & 1];
+    h8 va[4];
+    va[0] = read_va<0, 0>(vab);
+    va[1] = read_va<0, 1>(vab);
+    va[2] = read_va<0, 2>(vab);
+    va[3] = read_va<0, 3>(vab);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pl[b][0]);
+    va[0] = read_va<1, 0>(vab);
+    va[1] = read_va<1, 1>(vab);
+    va[2] = read_va<1, 2>(vab);
+    va[3] = read_va<1, 3>(vab);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pl[b][1]);
+    pv_drain_all(o);
   };
 
   for (int pass = 0; pass < 2; ++pass) {
@@ -740,17 +944,46 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     // Loads are issued in the order K0 K1 V0 | K2 V1 | K3 V2 | ... (step it
     // issues K(it+2), then V(it+1)).  Step it needs K(it+1) and V(it-1): only
     // V(it), the last load issued, may still be pending.
-    if (g_count > 0) {
-      wait_vmcnt<8>();
-      step(0, std::false_type{});
-    }
-    for (int it = 1; it < g_count; ++it) {
-      wait_vmcnt<8>();
-      step(it, std::true_type{});
-    }
-    if (g_count > 0) {
-      wait_vmcnt<0>();
-      last_pv();
+    if constexpr (NB == 2) {
+      f16v s_alt[NB];
+      h8 p_a[NB][2], p_b[NB][2];
+      if (g_count > 0) {
+        wait_vmcnt<8>();
+        step2(0, std::false_type{}, s_cur, s_alt, p_a, p_b);  // P(0) -> p_b
+      }
+      int it = 1;
+      for (; it + 1 < g_count; it += 2) {
+        wait_vmcnt<8>();
+        step2(it, std::true_type{}, s_alt, s_cur, p_b, p_a);
+        wait_vmcnt<8>();
+        step2(it + 1, std::true_type{}, s_cur, s_alt, p_a, p_b);
+      }
+      if (it < g_count) {
+        wait_vmcnt<8>();
+        step2(it, std::true_type{}, s_alt, s_cur, p_b, p_a);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {  // P of the last tile where last_pv_of reads it
+          p_b[b][0] = p_a[b][0];
+          p_b[b][1] = p_a[b][1];
+        }
+      }
+      if (g_count > 0) {
+        wait_vmcnt<0>();
+        last_pv_of(p_b);
+      }
+    } else {
+      if (g_count > 0) {
+        wait_vmcnt<8>();
+        step(0, std::false_type{});
+      }
+      for (int it = 1; it < g_count; ++it) {
+        wait_vmcnt<8>();
+        step(it, std::true_type{});
+      }
+      if (g_count > 0) {
+        wait_vmcnt<0>();
+        last_pv();
+      }
     }
     // Row sums: overflow (not finite) or underflow (< 2^-8 with keys in range)
     // means the reference did not suit the row.
@@ -765,6 +998,8 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   }
 #undef MIA_LOAD_K
 #undef MIA_LOAD_V
+#undef MIA_LOAD_K_NEXT
+#undef MIA_LOAD_V_NEXT
 
   // ---- merge of the four key groups ----
   pv_drain<NB>(o);
