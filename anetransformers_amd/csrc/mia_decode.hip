@@ -45,8 +45,12 @@ constexpr int kDepth = 2;        // register tile buffers per wave (3, 4 measure
 constexpr int kMaxChunks = 256;  // merge capacity per kv head
 constexpr int G = 4;             // query heads per kv head
 
+// Every part of it is private to one wave: the prologue has no workgroup
+// barrier, so each wave starts its loop as soon as its own q has arrived
+// (at launch these small loads queue among every wave's first tile
+// requests, and waiting for the slowest of 8 waves costs microseconds).
 struct DecodeSmem {
-  float2 cs[64];                 // RoPE (cos, sin) for the 64 pair indices
+  float2 cs[kWaves][64];         // RoPE (cos, sin) for the 64 pair indices
   _Float16 knew[kWaves][HD];     // rotated fp16 new key of each kv head
   _Float16 vnew[kWaves][HD];
 };
@@ -102,7 +106,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   const int lg = lane >> 4;  // MFMA k group / V key group
   const int hgroups = (p.n_kv + kWaves - 1) / kWaves;
   const int kvh = (blockIdx.x % hgroups) * kWaves + w;
-  const bool active = kvh < p.n_kv;  // waves past the last head only join the barriers
+  const bool active = kvh < p.n_kv;  // waves past the last head have no tiles
   const int chunk = blockIdx.x / hgroups;
   const int kvh_c = active ? kvh : 0;  // idle waves keep in-bounds addresses
   const int kv_dim = p.n_kv * HD;
@@ -184,8 +188,26 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
     issue_v(b, tt);
   };
 
-  // The first kDepth tiles are requested before the prologue so that their
-  // latency overlaps the RoPE table, the new-token write and the q set-up.
+  // The prologue's own loads (q, theta_inv, the new token) are issued before
+  // the first kDepth tiles: loads complete in issue order, so the q set-up
+  // waits only for its own data, not for the tiles.
+  const bool col = lc < G;
+  f4 qraw[8];
+  {
+    const f4 *qsrc = reinterpret_cast<const f4 *>(q_in + (size_t)(kvh_c * G + (col ? lc : 0)) * HD + 8 * lg);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      qraw[2 * s] = qsrc[8 * s];
+      qraw[2 * s + 1] = qsrc[8 * s + 1];
+    }
+  }
+  const float th_in = rope_q ? p.theta_inv[lane] : 0.f;
+  float2 knew_in = make_float2(0.f, 0.f), vnew_in = make_float2(0.f, 0.f);
+  if (FUSED) {  // (every wave: a branch here would make the join wait for the loads)
+    knew_in = *reinterpret_cast<const float2 *>(p.knew + (size_t)kvh_c * HD + 2 * lane);
+    vnew_in = *reinterpret_cast<const float2 *>(p.vnew + (size_t)kvh_c * HD + 2 * lane);
+  }
+
   TileBuf buf[kDepth];
   int tix[kDepth];
 #pragma unroll
@@ -193,31 +215,31 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
     tix[b] = next_tile();
     issue(buf[b], tix[b]);
   }
+  // (keeps the compiler from converting the new token before the tile loads
+  // are issued, which would wait for its loads there)
+  if (FUSED) asm volatile("" : "+v"(knew_in.x), "+v"(knew_in.y), "+v"(vnew_in.x), "+v"(vnew_in.y));
 
+  float2 cs_lane = make_float2(1.f, 0.f);  // (cos, sin) of pair `lane`
   if (rope_q) {
-    if (tid < 64) {
-      // angle = fl32(theta_inv[i] * pos) as vDSP_vsmul (mistral_model.h:87-88)
-      float ang = p.theta_inv[tid] * (float)pos;
-      float sn, cs;
-      sincosf(ang, &sn, &cs);
-      sm.cs[tid] = make_float2(cs, sn);
-    }
-    __syncthreads();
+    // angle = fl32(theta_inv[i] * pos) as vDSP_vsmul (mistral_model.h:87-88)
+    const float ang = th_in * (float)pos;
+    float sn, cs;
+    sincosf(ang, &sn, &cs);
+    cs_lane = make_float2(cs, sn);
+    sm.cs[w][lane] = cs_lane;
+    wave_lds_sync();
   }
-  if (FUSED) {
-    if (has_new && active) {
-      // new k rotated (pair `lane`) and v, rounded to fp16 (mistral_model.h:854-857)
-      float2 kv = *reinterpret_cast<const float2 *>(p.knew + (size_t)kvh * HD + 2 * lane);
-      float2 cs = sm.cs[lane];
-      rope_pair(kv.x, kv.y, cs.x, cs.y);
-      float2 vv = *reinterpret_cast<const float2 *>(p.vnew + (size_t)kvh * HD + 2 * lane);
-      sm.knew[w][2 * lane] = (_Float16)kv.x;
-      sm.knew[w][2 * lane + 1] = (_Float16)kv.y;
-      sm.vnew[w][2 * lane] = (_Float16)vv.x;
-      sm.vnew[w][2 * lane + 1] = (_Float16)vv.y;
-    }
-    __syncthreads();
-    if (has_new && active && lane < 16) {  // write of the new row (256 B per tensor)
+  if (FUSED && has_new && active) {
+    // new k rotated (pair `lane`) and v, rounded to fp16 (mistral_model.h:854-857)
+    float2 kv = knew_in;
+    rope_pair(kv.x, kv.y, cs_lane.x, cs_lane.y);
+    const float2 vv = vnew_in;
+    sm.knew[w][2 * lane] = (_Float16)kv.x;
+    sm.knew[w][2 * lane + 1] = (_Float16)kv.y;
+    sm.vnew[w][2 * lane] = (_Float16)vv.x;
+    sm.vnew[w][2 * lane + 1] = (_Float16)vv.y;
+    wave_lds_sync();
+    if (lane < 16) {  // write of the new row (256 B per tensor)
       const size_t row = p.new_k ? 0 : (size_t)p.new_slot * kv_dim;
       _Float16 *kd = (p.new_k ? p.new_k : p.kc) + row, *vd = (p.new_v ? p.new_v : p.vc) + row;
       const size_t off = (size_t)kvh * HD + 8 * lane;
@@ -230,17 +252,14 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   // 32*s + 8*lg .. +8 (the same dims the A lanes load), hi and lo parts.
   h8 qhi[4], qlo[4];
   {
-    const bool col = lc < G;
-    const float *qsrc = q_in + (size_t)(kvh_c * G + (col ? lc : 0)) * HD + 8 * lg;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const f4 *src = reinterpret_cast<const f4 *>(qsrc + 32 * s);
-      f4 a = src[0], b = src[1];
+      const f4 a = qraw[2 * s], b = qraw[2 * s + 1];
       float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
       if (rope_q) {
 #pragma unroll
         for (int pi = 0; pi < 4; ++pi) {
-          float2 cs = sm.cs[16 * s + 4 * lg + pi];
+          float2 cs = sm.cs[w][16 * s + 4 * lg + pi];
           rope_pair(v[2 * pi], v[2 * pi + 1], cs.x, cs.y);
         }
       }
