@@ -111,6 +111,10 @@ _SIGS = {
     "mia_profile_end": (c_int, [c_int, POINTER(c_int), POINTER(ctypes.c_double)]),
     "mia_fill_normal_f16": (c_int, [_P, c_size_t, c_uint64, _P]),
     "mia_scale_rows_f16": (c_int, [_P, c_long, c_int, c_int, c_int, c_float, _P]),
+    # measured peaks (bench)
+    "mia_peak_read_stream": (c_int, [_P, c_size_t, _P]),
+    "mia_peak_read_ring": (c_int, [_P, _P, c_int, c_int, c_int, c_int, _P]),
+    "mia_peak_mfma_f16": (c_int, [c_int, POINTER(ctypes.c_double), _P]),
     # hot path
     "mia_rope_f32": (c_int, [_P, _P, c_int, c_int, _P, c_int, c_int, c_int, _P]),
     "mia_kv_write_f32": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, _P]),

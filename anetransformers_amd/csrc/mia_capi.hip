@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "../../include/miattn.h"
+#include "../../include/mia_peaks.h"
 #include "mia_kernels.h"
 
 // Scratch of mia_decode_step_noalloc, one copy per device for the life of the
@@ -622,6 +623,37 @@ int mia_fill_normal_f16(uint16_t *dst, size_t n, uint64_t seed, void *stream) {
   if (int rc = current_ctx(&c)) return rc;
   if (!dst && n) return set_err(MIA_ERR_INVALID, "dst is NULL");
   HIP_TRY(mia::launch_fill_normal(reinterpret_cast<_Float16 *>(dst), n, seed, pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_peak_read_stream(const void *buf, size_t bytes, void *stream) {
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  if (!buf || bytes == 0 || bytes % 16 != 0)
+    return set_err(MIA_ERR_INVALID, "peak_read_stream: need a buffer of a positive multiple of 16 bytes");
+  HIP_TRY(mia::launch_peak_read_stream(buf, bytes, c->num_cus, pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_peak_read_ring(const uint16_t *k_layer, const uint16_t *v_layer, int n_kv_heads,
+                       int max_seq, int L, int start, void *stream) {
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  if (!k_layer || !v_layer) return set_err(MIA_ERR_INVALID, "peak_read_ring: NULL ring");
+  if (n_kv_heads < 1 || max_seq < 1 || L < 1 || L > max_seq || start < 0 || start >= max_seq)
+    return set_err(MIA_ERR_INVALID, "peak_read_ring: need 1 <= L <= max_seq, 0 <= start < max_seq");
+  const int nchunk = mia::decode_pick_nchunk(L, n_kv_heads, c->num_cus);
+  HIP_TRY(mia::launch_peak_read_ring(reinterpret_cast<const _Float16 *>(k_layer),
+                                     reinterpret_cast<const _Float16 *>(v_layer), n_kv_heads,
+                                     max_seq, L, start, nchunk, pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_peak_mfma_f16(int iters, double *flop, void *stream) {
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  if (iters < 1 || !flop) return set_err(MIA_ERR_INVALID, "peak_mfma_f16: iters >= 1 and flop");
+  HIP_TRY(mia::launch_peak_mfma_f16(iters, c->num_cus, flop, pick_stream(c, stream)));
   return MIA_OK;
 }
 

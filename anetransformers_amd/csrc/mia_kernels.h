@@ -106,6 +106,12 @@ hipError_t launch_commit(_Float16 *kc, _Float16 *vc, const _Float16 *kst, const 
                          int n_layers = 1, size_t ring_stride = 0, size_t stage_stride = 0);
 hipError_t launch_fill_normal(_Float16 *dst, size_t n, uint64_t seed, hipStream_t s);
 
+// Peak microbenchmarks (mia_peaks.hip).
+hipError_t launch_peak_read_stream(const void *buf, size_t bytes, int num_cus, hipStream_t s);
+hipError_t launch_peak_read_ring(const _Float16 *kc, const _Float16 *vc, int n_kv, int max_seq,
+                                 int L, int start, int nchunk, hipStream_t s);
+hipError_t launch_peak_mfma_f16(int iters, int num_cus, double *flop, hipStream_t s);
+
 // W4A8 projections (mistral/dequant.h).  x [nblocks*32] fp32, 16-byte aligned
 // -> nblocks Q8_0 blocks of 36 bytes.
 hipError_t launch_quantize_q8_0(const float *x, uint8_t *out, int nblocks, hipStream_t s);

@@ -1,0 +1,148 @@
+// mia_peaks.hip -- measured peaks of the two roofs the attention kernels sit
+// under: HBM read bandwidth (a plain stream, and one layer's ring read in the
+// decode kernel's own access pattern with no arithmetic) and the fp16 MFMA
+// rate.  The counterpart of the reference's peak benchmark (inmem_peak.m:89-111),
+// which measures the ANE's throughput ceiling beside its kernels.
+//
+// The kernels fold what they read into a checksum that is stored only when it
+// equals a value no input produces, so nothing is written and nothing is
+// optimised away.
+#include "mia_device.h"
+#include "mia_kernels.h"
+
+namespace mia {
+
+// Written only when a checksum equals kNever.  External linkage: a sink the
+// compiler could prove unread would let it drop the stores, and with them
+// every load feeding them.
+__device__ unsigned g_peak_sink[64];
+
+namespace {
+
+constexpr unsigned kNever = 0x9e3779b9u;
+
+// Grid-stride read of n 16-byte words, UNROLL independent loads in flight per
+// thread.
+template <int UNROLL>
+__global__ void __launch_bounds__(256) read_stream_kernel(const u4 *__restrict__ p, size_t n) {
+  u4 acc = {0u, 0u, 0u, 0u};
+  const size_t stride = (size_t)gridDim.x * 256 * UNROLL;
+  for (size_t i = (size_t)blockIdx.x * 256 * UNROLL + threadIdx.x; i < n; i += stride) {
+    u4 v[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) v[u] = i + 256 * u < n ? p[i + 256 * u] : u4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) acc ^= v[u];
+  }
+  const unsigned r = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  if (r == kNever) g_peak_sink[threadIdx.x & 63] = r;
+}
+
+// One layer's K and V window read as decode_kernel reads it: one workgroup
+// per chunk, one wave per kv head, chunk c = the 16-slot tiles c, c + nchunk,
+// ... of the window starting at slot `start`, two tiles in flight per wave;
+// K as 16 rows x 64 B per load (the MFMA A-operand layout), V as 4 rows x
+// 256 B.  Slots wrap at max_seq per lane.
+__global__ void __launch_bounds__(512, 1) read_ring_kernel(const _Float16 *__restrict__ kc,
+                                                           const _Float16 *__restrict__ vc,
+                                                           int n_kv, int max_seq, int L,
+                                                           int start, int nchunk) {
+  constexpr int kWaves = 8, kTile = 16;
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int lc = lane & 15, lg = lane >> 4;
+  const int hgroups = (n_kv + kWaves - 1) / kWaves;
+  const int kvh = (blockIdx.x % hgroups) * kWaves + w;
+  const int chunk = blockIdx.x / hgroups;
+  if (kvh >= n_kv) return;
+  const size_t kv_dim = (size_t)n_kv * HD;
+  const int n_tiles = (L + kTile - 1) / kTile;
+  const int count = chunk < n_tiles ? (n_tiles - 1 - chunk) / nchunk + 1 : 0;
+  const _Float16 *kb = kc + (size_t)kvh * HD, *vb = vc + (size_t)kvh * HD;
+  auto slot = [&](int t) {  // window position t (clamped to the window) -> ring row
+    t = t < L ? t : L - 1;
+    const int s = start + t;
+    return (size_t)(s >= max_seq ? s - max_seq : s);
+  };
+  auto issue = [&](u4 (&b)[8], int i) {
+    const int t0 = (chunk + nchunk * (i < count ? i : count - 1)) * kTile;
+    const _Float16 *ks = kb + slot(t0 + lc) * kv_dim + 8 * lg;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) b[s] = *reinterpret_cast<const u4 *>(ks + 32 * s);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      b[4 + m] = *reinterpret_cast<const u4 *>(vb + slot(t0 + 4 * lg + m) * kv_dim + 8 * lc);
+  };
+  if (count == 0) return;
+  u4 b0[8], b1[8];
+  u4 acc = {0u, 0u, 0u, 0u};
+  issue(b0, 0);
+  issue(b1, 1);
+  for (int i = 0; i < count; i += 2) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) acc ^= b0[s];
+    issue(b0, i + 2);
+    if (i + 1 >= count) break;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) acc ^= b1[s];
+    issue(b1, i + 3);
+  }
+  const unsigned r = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  if (r == kNever) g_peak_sink[lane] = r;
+}
+
+// kChains independent accumulators per wave, each a chain of `iters`
+// v_mfma_f32_32x32x16_f16 (32 x 32 x 16 x 2 = 32768 FLOP each).
+constexpr int kChains = 4;
+constexpr int kMfmaWgsPerCu = 2;  // x 4 waves: two waves per SIMD
+
+__global__ void __launch_bounds__(256) mfma_f16_kernel(int iters) {
+  const int lane = threadIdx.x & 63;
+  h8 a, b;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    a[e] = (_Float16)((lane + e) & 7) * (_Float16)0.125f;
+    b[e] = (_Float16)((lane * 3 + e) & 7) * (_Float16)0.0625f;
+  }
+  f16v acc[kChains];
+#pragma unroll
+  for (int c = 0; c < kChains; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[c][e] = 0.f;
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int c = 0; c < kChains; ++c)
+      acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[c], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < kChains; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += acc[c][e];
+  if (s == -1.0f) g_peak_sink[lane] = kNever;  // sums of products of non-negative values
+}
+
+}  // namespace
+
+hipError_t launch_peak_read_stream(const void *buf, size_t bytes, int num_cus, hipStream_t s) {
+  hipLaunchKernelGGL(read_stream_kernel<4>, dim3(4 * num_cus), dim3(256), 0, s,
+                     reinterpret_cast<const u4 *>(buf), bytes / 16);
+  return hipGetLastError();
+}
+
+hipError_t launch_peak_read_ring(const _Float16 *kc, const _Float16 *vc, int n_kv, int max_seq,
+                                 int L, int start, int nchunk, hipStream_t s) {
+  const int hgroups = (n_kv + 7) / 8;
+  hipLaunchKernelGGL(read_ring_kernel, dim3(hgroups * nchunk), dim3(512), 0, s, kc, vc, n_kv,
+                     max_seq, L, start, nchunk);
+  return hipGetLastError();
+}
+
+hipError_t launch_peak_mfma_f16(int iters, int num_cus, double *flop, hipStream_t s) {
+  const int wgs = kMfmaWgsPerCu * num_cus;
+  *flop = (double)wgs * 4 * kChains * iters * 32768.0;
+  hipLaunchKernelGGL(mfma_f16_kernel, dim3(wgs), dim3(256), 0, s, iters);
+  return hipGetLastError();
+}
+
+}  // namespace mia

@@ -21,6 +21,11 @@ configs: the other config shapes (a 513-position single layer, a 4097-position
 32-layer decode, the 8-draft verify on a wrapped 65536-slot ring), each with
 its oracle CPU timing: reported beside the headline, not as it.
 
+peaks: measured roofs on this part (include/mia_peaks.h): a plain HBM read
+stream, the decode kernel's own load pattern over the headline's rings with no
+arithmetic, and an fp16 MFMA loop; the roofline objects quote their fraction
+of both the published and the measured peak.
+
 dropin: the same decode step through the C drop-in (mia_dropin_decode_step)
 with host q/k/v/out buffers, synchronous per layer as the reference's call
 site is: the PCIe-inclusive rate, reported beside the headline, never as it.
@@ -220,6 +225,48 @@ def kernel_avg_ms(lib, fn, steps: int, kind: int) -> float:
     tot = ctypes.c_double()
     check(lib.mia_profile_end(kind, ctypes.byref(n), ctypes.byref(tot)))
     return tot.value / max(n.value, 1)
+
+
+def measure_peaks(lib, dec: "Decode", reps: int = 10) -> dict:
+    """Measured HBM read and fp16 MFMA peaks (mean over `reps` launches)."""
+    nb = 2 << 30
+    buf = DeviceBuffer(nb)
+    # N(0,1) fp16 like the rings: random bits toggle the HBM bus (constant
+    # data reads about 4 % faster on this part)
+    check(lib.mia_fill_normal_f16(buf.ptr, nb // 2, 77, None))
+    st_ms = timed(lib, lambda: check(lib.mia_peak_read_stream(buf.ptr, nb, None)), reps, 2)
+    del buf
+    lay = DECODE_M * KV_DIM * 2
+    start = (DECODE_POS + 1 - DECODE_L) % DECODE_M
+
+    def ring_pass():
+        for l in range(N_LAYERS):
+            check(lib.mia_peak_read_ring(dec.kc.ptr + l * lay, dec.vc.ptr + l * lay, N_KV,
+                                         DECODE_M, DECODE_L, start, None))
+
+    rg_ms = timed(lib, ring_pass, max(reps // 4, 2), 1) / N_LAYERS
+    flop = ctypes.c_double()
+    iters = 1024
+    mf_ms = timed(lib, lambda: check(lib.mia_peak_mfma_f16(iters, ctypes.byref(flop), None)),
+                  reps, 2)
+    return {
+        "hbm_read_stream": {
+            "value": round(nb / (st_ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+            "workload": "one 2 GiB grid-stride read (N(0,1) fp16 data), 1024 workgroups x "
+                        "256 threads, four 16-byte loads in flight per thread",
+            "ms_per_launch": round(st_ms, 4)},
+        "hbm_read_decode_pattern": {
+            "value": round(DECODE_BYTES_PER_LAYER / (rg_ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+            "workload": "the headline's 32 rings (K and V, 134 MB each layer) read back to back "
+                        "in decode_kernel's chunking and load pattern, no arithmetic",
+            "us_per_layer": round(rg_ms * 1e3, 2)},
+        "mfma_f16": {
+            "value": round(flop.value / (mf_ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s",
+            "workload": f"{iters} rounds of 4 independent v_mfma_f32_32x32x16_f16 chains, "
+                        "2 waves per SIMD on every CU",
+            "ms_per_launch": round(mf_ms, 4)},
+        "published": {"hbm_gbs": HBM_PEAK_GBS, "mfma_f16_tfs": MFMA_F16_PEAK_TFS},
+    }
 
 
 def cpu_baseline_decode(n_layers: int = 8, reps: int = 3):
@@ -688,6 +735,7 @@ def main() -> int:
                     help="skip the W4A8 projection line (profiling)")
     ap.add_argument("--skip-configs", action="store_true",
                     help="skip the side configs 1, 2 and 5 (profiling)")
+    ap.add_argument("--skip-peaks", action="store_true", help="skip the measured-peaks leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 5 device-to-device copies of 512 MiB (a copy kernel of known "
                          "size, to scale HBM byte counters)")
@@ -709,12 +757,18 @@ def main() -> int:
         check(lib.mia_device_sync())
         del src, dst
     dec_ms = kern_ms = float("nan")
-    dropin = projections = None
+    dropin = projections = peaks = None
     if not args.skip_decode:
         log("decode: allocating 32 x 32768-slot rings (4 GiB)")
         dec = Decode(lib)
         dec_ms = timed(lib, dec.step, args.steps, args.warmup)
         kern_ms = kernel_avg_ms(lib, dec.step, args.steps, 0)
+        if not args.skip_peaks:
+            log("peaks: HBM read stream, decode load pattern, fp16 MFMA loop")
+            peaks = measure_peaks(lib, dec)
+            log(f"peaks: stream {peaks['hbm_read_stream']['value']} GB/s, decode pattern "
+                f"{peaks['hbm_read_decode_pattern']['value']} GB/s, fp16 MFMA "
+                f"{peaks['mfma_f16']['value']} TFLOP/s")
         dd = DropinDecode(lib, dec)
         di_ms = wall_ms(dd.step, args.steps, args.warmup)
         dropin = {"value": round(N_LAYERS * DECODE_BYTES_PER_LAYER / (di_ms * 1e-3) / 1e9, 2),
@@ -781,6 +835,10 @@ def main() -> int:
                          "frac": round(fl_tfs / MFMA_F16_PEAK_TFS, 4),
                          "traffic": load_traffic("flash_prefill")},
         }
+        if peaks is not None:
+            mp = peaks["mfma_f16"]["value"]
+            prefill["roofline"]["measured_peak"] = mp
+            prefill["roofline"]["frac_of_measured"] = round(fl_tfs / mp, 4)
         del pf
 
     gguf = None
@@ -869,6 +927,13 @@ def main() -> int:
             for k, v in cpu_other_configs().items():
                 configs[k]["cpu_baseline"] = v
 
+    roof = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic("decode_32k")}
+    if peaks is not None:
+        mp = peaks["hbm_read_decode_pattern"]["value"]
+        roof["measured_peak"] = mp
+        roof["frac_of_measured"] = round(achieved / mp, 4)
+        roof["measured_peak_is"] = "hbm_read_decode_pattern (peaks)"
     line = {
         "metric": "decode attn HBM GB/s (% peak) @32K ctx; prefill attn TFLOPS (% MFMA peak)",
         "value": round(value, 2),
@@ -891,10 +956,9 @@ def main() -> int:
             "decode_kernel_us": round(kern_ms * 1e3, 2),
             "arithmetic": "fp16 MFMA operands (q split hi+lo), fp32 accumulate and softmax",
         },
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": load_traffic("decode_32k")},
+        "roofline": roof,
         "cpu_baseline": cpu,
+        "peaks": peaks,
         "dropin": dropin,
         "prefill": prefill,
         "configs": configs,

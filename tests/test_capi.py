@@ -19,7 +19,7 @@ CLANG = "/opt/rocm/llvm/bin/clang"
 
 def declared_functions():
     names = set()
-    for h in ("miattn.h", "mia_dropin.h", "mia_gguf.h"):
+    for h in ("miattn.h", "mia_dropin.h", "mia_gguf.h", "mia_peaks.h"):
         text = open(os.path.join(INCLUDE, h)).read()
         # top-level prototypes "type name(" ending in ");" (not static inline wrappers)
         for m in re.finditer(r"^(?:const\s+)?[A-Za-z_][\w \*]*?\b(mia_\w+)\s*\(", text, re.M):
