@@ -4,31 +4,33 @@
 // fused variant, steps 4-6 of mistral/mistral_model.h:849-863 (RoPE on q/k,
 // fp16 round of k/v, ring write at pos % max_seq, attention).
 //
-// Grid: one workgroup per (group of 8 kv heads, chunk of the window), one
-// wave per kv head.  The waves of a workgroup walk the same ring slots, so
-// each slot's full K and V rows (8 heads x 256 B, contiguous) are read
-// together: streaming one head's 256 B pieces per workgroup instead leaves
-// some heads' pieces consistently slower to fetch than others.  Chunk c is
-// the 16-key tiles c, c + nchunk, c + 2 nchunk, ... of the window: spread
-// over the whole ring rather than one contiguous block, every workgroup
-// draws on all memory channels alike, and the workgroups end closer together.
+// Grid: one workgroup per (kv head, chunk of the window), 8 waves per
+// workgroup, all on that head.  Chunk c is the 16-key tiles c, c + nchunk,
+// c + 2 nchunk, ... of the window: spread over the whole ring rather than one
+// contiguous block, every workgroup draws on all memory channels alike; wave
+// w of the workgroup takes every 8th of its chunk's tiles.  The heads of one
+// chunk are consecutive workgroups, which the dispatcher spreads over the
+// XCDs.  32 chunks at 8 kv heads fill 256 CUs with 8x fewer split-K partials
+// than one wave per head and chunk would leave.
 //
-// Each wave is an independent pipeline over the 16-key tiles of its chunk,
-// held in a ring of register buffers so that the next tiles' loads are in
-// flight while one tile is computed:
-//   scores  v_mfma_f32_16x16x32_f16: A = 16 key rows straight from the
-//           loads (lane = key row, 64 contiguous bytes), B = the G=4 query
-//           heads of the group with q split into fp16 hi + lo parts along K
-//           (q = hi + lo to ~2^-22), so the scores carry fp32 q accuracy.
+// Each wave is an independent pipeline over its tiles, held in a ring of
+// register buffers so that the next tiles' loads are in flight while one
+// tile is computed.  Every load instruction reads 4 rows x 256 B (whole
+// 128-byte lines; loads of 16 rows x 64 B each read a measured 6 % slower):
+//   scores  v_mfma_f32_16x16x32_f16: A = 16 key rows (lane = key row), from
+//           the loaded K rows re-laid through a per-wave LDS tile; B = the
+//           G=4 query heads of the group with q split into fp16 hi + lo
+//           parts along K (q = hi + lo to ~2^-22), so the scores carry fp32 q
+//           accuracy.
 //   softmax wave-local online max / sum in the log2 domain.
 //   P.V     v_mfma_f32_16x16x16_f16 computing O^T = V^T P^T: the score
 //           accumulator layout (lane = 4 keys of one head) is already the B
 //           operand layout with keys along K, so P (fp16 hi + lo) never
 //           leaves its lane; V^T comes from the 4 loaded V rows of the lane
 //           (4 keys x 8 dims) by byte permutes.
-// A wave's result is final for its head and chunk: it is written as the
-// chunk partial (m, l, o) directly; a second, small kernel does the
-// log-sum-exp merge over chunks.
+// The 8 waves' results merge through LDS into the chunk's partial (m, l, o)
+// (the final output when there is one chunk); a second, small kernel does
+// the log-sum-exp merge over chunks.
 #include <type_traits>
 
 #include "mia_device.h"
@@ -38,26 +40,29 @@ namespace mia {
 
 namespace {
 
-constexpr int kWaves = 8;         // kv heads per workgroup, one wave each
+constexpr int kWaves = 8;         // waves per workgroup, all on one kv head
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 16;        // keys per wave tile
-constexpr int kDepth = 2;        // register tile buffers per wave (3, 4 measured no faster)
+constexpr int kDepth = 2;        // register tile buffers per wave
 constexpr int kMaxChunks = 256;  // merge capacity per kv head
 constexpr int G = 4;             // query heads per kv head
+// Bytes per staged K row: 16 B of padding put the 16 rows of a column read
+// on 16 different bank groups.
+constexpr int kKPitch = HD * 2 + 16;
+static_assert(kThreads == G * HD, "the in-workgroup merge gives each thread one output element");
 
-// Every part of it is private to one wave: the prologue has no workgroup
-// barrier, so each wave starts its loop as soon as its own q has arrived
-// (at launch these small loads queue among every wave's first tile
-// requests, and waiting for the slowest of 8 waves costs microseconds).
 struct DecodeSmem {
-  float2 cs[kWaves][64];         // RoPE (cos, sin) for the 64 pair indices
-  _Float16 knew[kWaves][HD];     // rotated fp16 new key of each kv head
-  _Float16 vnew[kWaves][HD];
+  float2 cs[kWaves][64];                  // per-wave RoPE (cos, sin) of the 64 pair indices
+  unsigned char kst[kWaves][kTile * kKPitch];  // per-wave K tile in row-major order
+  _Float16 knew[HD];                      // rotated fp16 new key (the wave that attends it)
+  _Float16 vnew[HD];
+  float mo[kWaves][G][HD];                // in-workgroup merge: each wave's o
+  float2 mlw[kWaves][G];                  // ... and its (m, l)
 };
 
 struct TileBuf {
-  u4 k[4];  // MFMA A operand, k-step s: key row lane%16, dims 32*s + 8*(lane/16) .. +8
-  u4 v[4];  // V rows: keys 4*(lane/16) + m, dims 8*(lane%16) .. +8
+  u4 k[4];  // K rows 4*(lane/16) + m, dims 8*(lane%16) .. +8
+  u4 v[4];  // V rows 4*(lane/16) + m, dims 8*(lane%16) .. +8
 };
 
 // Value of x in lane `src` (uniform result).
@@ -104,33 +109,31 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lc = lane & 15;  // MFMA column / V dim block
   const int lg = lane >> 4;  // MFMA k group / V key group
-  const int hgroups = (p.n_kv + kWaves - 1) / kWaves;
-  const int kvh = (blockIdx.x % hgroups) * kWaves + w;
-  const bool active = kvh < p.n_kv;  // waves past the last head have no tiles
-  const int chunk = blockIdx.x / hgroups;
-  const int kvh_c = active ? kvh : 0;  // idle waves keep in-bounds addresses
+  const int kvh = blockIdx.x % p.n_kv;
+  const int chunk = blockIdx.x / p.n_kv;
   const int kv_dim = p.n_kv * HD;
   // The new token (fused) is attended after the loop, from its fp16 copy in
-  // LDS, by the waves of the last chunk; the tiles cover keys [0, ce).
+  // LDS, by the last wave of the last chunk; the tiles cover keys [0, ce).
   const int ce = FUSED ? win_L - 1 : win_L;
   const int n_tiles = (ce + kTile - 1) / kTile;
-  const bool has_new = FUSED && chunk == p.nchunk - 1;
-  // Tiles of this wave: chunk, chunk + nchunk, chunk + 2 nchunk, ...
+  const bool has_new = FUSED && chunk == p.nchunk - 1 && w == kWaves - 1;
+  // Tiles of this wave: chunk + nchunk * (w + kWaves * i), i = 0, 1, ...
+  const int t_first = chunk + p.nchunk * w, t_step = p.nchunk * kWaves;
   int s_next = 0;
-  const int s_end = active && chunk < n_tiles ? (n_tiles - 1 - chunk) / p.nchunk + 1 : 0;
-  auto next_tile = [&]() -> int { return s_next < s_end ? chunk + p.nchunk * s_next++ : -1; };
+  const int s_end = t_first < n_tiles ? (n_tiles - 1 - t_first) / t_step + 1 : 0;
+  auto next_tile = [&]() -> int { return s_next < s_end ? t_first + t_step * s_next++ : -1; };
 
-  const _Float16 *kbase = p.kc + (size_t)kvh_c * HD;
-  const _Float16 *vbase = p.vc + (size_t)kvh_c * HD;
+  const _Float16 *kbase = p.kc + (size_t)kvh * HD;
+  const _Float16 *vbase = p.vc + (size_t)kvh * HD;
 
-  // Tile loads.  A tile whose 16 slots are contiguous in the ring and inside
-  // the window (all but the tile across the ring's end and the window's last
+  // Tile loads: lane (lc, lg) reads rows 4*lg + m, dims 8*lc .. +8 of K and
+  // of V.  A tile whose 16 slots are contiguous in the ring and inside the
+  // window (all but the tile across the ring's end and the window's last
   // tile) is addressed as one wave-uniform row base plus fixed per-lane
   // offsets; the others clamp and wrap per lane.
-  const unsigned koff = (unsigned)lc * kv_dim + 8 * lg;  // K: row lc, dims 8*lg (+32*s)
-  unsigned voff[4];                                       // V: row 4*lg+m, dims 8*lc
+  unsigned roff[4];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) voff[m] = (unsigned)(4 * lg + m) * kv_dim + 8 * lc;
+  for (int m = 0; m < 4; ++m) roff[m] = (unsigned)(4 * lg + m) * kv_dim + 8 * lc;
   auto tile_row0 = [&](int tt, bool &linear) {
     const int t0 = tt * kTile;
     const int s0 = ring_slot(win_start, t0, p.max_seq);
@@ -143,25 +146,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   // buffer it needs instead of for all outstanding loads.
   // (Offsets rather than pointers are selected, so that every load keeps
   // the global address space of the kernel argument.)
-  auto issue_k = [&](TileBuf &b, int tt) {
-    size_t off = 0;
-    if (tt >= 0) {
-      bool linear;
-      const int t0 = tile_row0(tt, linear);
-      if (linear) {
-        off = (size_t)ring_slot(win_start, t0, p.max_seq) * kv_dim + koff;
-      } else {
-        const int t = min(t0 + lc, ce - 1);
-        off = (size_t)ring_slot(win_start, t, p.max_seq) * kv_dim + 8 * lg;
-      }
-    }
-    const _Float16 *src = kbase + off;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) b.k[s] = *reinterpret_cast<const u4 *>(src + 32 * s);
-  };
   // (In-layer offsets reach max_seq * kv_dim elements, beyond 32 bits for
   // large rings: the per-lane slot offsets are formed in 64 bits.)
-  auto issue_v = [&](TileBuf &b, int tt) {
+  auto issue_rows = [&](u4 (&dst)[4], const _Float16 *base, int tt) {
     size_t row0 = 0;
     size_t off[4] = {0, 0, 0, 0};
     if (tt >= 0) {
@@ -170,7 +157,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
       if (linear) {
         row0 = (size_t)ring_slot(win_start, t0, p.max_seq) * kv_dim;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) off[m] = voff[m];
+        for (int m = 0; m < 4; ++m) off[m] = roff[m];
       } else {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
@@ -179,10 +166,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
         }
       }
     }
-    const _Float16 *src = vbase + row0;
+    const _Float16 *src = base + row0;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) b.v[m] = *reinterpret_cast<const u4 *>(src + off[m]);
+    for (int m = 0; m < 4; ++m) dst[m] = *reinterpret_cast<const u4 *>(src + off[m]);
   };
+  auto issue_k = [&](TileBuf &b, int tt) { issue_rows(b.k, kbase, tt); };
+  auto issue_v = [&](TileBuf &b, int tt) { issue_rows(b.v, vbase, tt); };
   auto issue = [&](TileBuf &b, int tt) {
     issue_k(b, tt);
     issue_v(b, tt);
@@ -194,7 +183,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   const bool col = lc < G;
   f4 qraw[8];
   {
-    const f4 *qsrc = reinterpret_cast<const f4 *>(q_in + (size_t)(kvh_c * G + (col ? lc : 0)) * HD + 8 * lg);
+    const f4 *qsrc = reinterpret_cast<const f4 *>(q_in + (size_t)(kvh * G + (col ? lc : 0)) * HD + 8 * lg);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       qraw[2 * s] = qsrc[8 * s];
@@ -204,8 +193,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   const float th_in = rope_q ? p.theta_inv[lane] : 0.f;
   float2 knew_in = make_float2(0.f, 0.f), vnew_in = make_float2(0.f, 0.f);
   if (FUSED) {  // (every wave: a branch here would make the join wait for the loads)
-    knew_in = *reinterpret_cast<const float2 *>(p.knew + (size_t)kvh_c * HD + 2 * lane);
-    vnew_in = *reinterpret_cast<const float2 *>(p.vnew + (size_t)kvh_c * HD + 2 * lane);
+    knew_in = *reinterpret_cast<const float2 *>(p.knew + (size_t)kvh * HD + 2 * lane);
+    vnew_in = *reinterpret_cast<const float2 *>(p.vnew + (size_t)kvh * HD + 2 * lane);
   }
 
   TileBuf buf[kDepth];
@@ -229,22 +218,22 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
     sm.cs[w][lane] = cs_lane;
     wave_lds_sync();
   }
-  if (FUSED && has_new && active) {
+  if (has_new) {
     // new k rotated (pair `lane`) and v, rounded to fp16 (mistral_model.h:854-857)
     float2 kv = knew_in;
     rope_pair(kv.x, kv.y, cs_lane.x, cs_lane.y);
     const float2 vv = vnew_in;
-    sm.knew[w][2 * lane] = (_Float16)kv.x;
-    sm.knew[w][2 * lane + 1] = (_Float16)kv.y;
-    sm.vnew[w][2 * lane] = (_Float16)vv.x;
-    sm.vnew[w][2 * lane + 1] = (_Float16)vv.y;
+    sm.knew[2 * lane] = (_Float16)kv.x;
+    sm.knew[2 * lane + 1] = (_Float16)kv.y;
+    sm.vnew[2 * lane] = (_Float16)vv.x;
+    sm.vnew[2 * lane + 1] = (_Float16)vv.y;
     wave_lds_sync();
     if (lane < 16) {  // write of the new row (256 B per tensor)
       const size_t row = p.new_k ? 0 : (size_t)p.new_slot * kv_dim;
       _Float16 *kd = (p.new_k ? p.new_k : p.kc) + row, *vd = (p.new_v ? p.new_v : p.vc) + row;
       const size_t off = (size_t)kvh * HD + 8 * lane;
-      *reinterpret_cast<u4 *>(kd + off) = *reinterpret_cast<const u4 *>(&sm.knew[w][8 * lane]);
-      *reinterpret_cast<u4 *>(vd + off) = *reinterpret_cast<const u4 *>(&sm.vnew[w][8 * lane]);
+      *reinterpret_cast<u4 *>(kd + off) = *reinterpret_cast<const u4 *>(&sm.knew[8 * lane]);
+      *reinterpret_cast<u4 *>(vd + off) = *reinterpret_cast<const u4 *>(&sm.vnew[8 * lane]);
     }
   }
 
@@ -286,18 +275,27 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
 
   // One 16-key tile starting at key t0; keys >= cend are masked.  With
   // `refill` the buffer is refilled with tile `next`: its K half as soon as
-  // the score MFMAs have read the keys, its V half after the P.V MFMAs.
+  // the K rows are in LDS, its V half after the P.V MFMAs.
+  unsigned char *kst = sm.kst[w];
   auto process = [&](TileBuf &b, int t0, int cend, int next, auto refill) {
+    // K rows -> LDS (row-major) -> A operand of k-step s: key row lc, dims
+    // 32*s + 8*lg .. +8.
+    wave_lds_sync();  // (the previous tile's reads of kst come first)
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      *reinterpret_cast<u4 *>(kst + (4 * lg + m) * kKPitch + 16 * lc) = b.k[m];
+    wave_lds_sync();
+    if (refill) issue_k(b, next);
     h8 ka[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) ka[s] = __builtin_bit_cast(h8, b.k[s]);
+    for (int s = 0; s < 4; ++s)
+      ka[s] = *reinterpret_cast<const h8 *>(kst + lc * kKPitch + 64 * s + 16 * lg);
     f4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s], qhi[s], d, 0, 0, 0);
       d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s], qlo[s], d, 0, 0, 0);
     }
-    if (refill) issue_k(b, next);
     // d[i]: score of key t0 + 4*lg + i for head lc (lanes lc < G).
     float sc[4];
     float mx = -INFINITY;
@@ -364,34 +362,54 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
       tix[b] = nt;
     }
   }
-  if (has_new && active) {
+  if (has_new) {
     // Every row of this tile is the new key / value; only key 0 is unmasked.
     TileBuf nb;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) nb.k[s] = *reinterpret_cast<const u4 *>(&sm.knew[w][32 * s + 8 * lg]);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) nb.v[m] = *reinterpret_cast<const u4 *>(&sm.vnew[w][8 * lc]);
+    for (int m = 0; m < 4; ++m) {
+      nb.k[m] = *reinterpret_cast<const u4 *>(&sm.knew[8 * lc]);
+      nb.v[m] = *reinterpret_cast<const u4 *>(&sm.vnew[8 * lc]);
+    }
     process(nb, win_L - 1, win_L, -1, std::false_type{});
   }
 
   // Wave totals: l over the 4 key groups of column lc.
   l_part += __shfl_xor(l_part, 16);
   l_part += __shfl_xor(l_part, 32);
-  if (!active || lc >= G) return;
-  // Lane (lc, lg) holds dims 32*lg .. +32 of head lc: element i of o[e] is
-  // dim 8*(4*lg + i) + e.
-  const size_t row = p.nchunk == 1 ? (size_t)kvh * G + lc
-                                   : ((size_t)kvh * p.nchunk + chunk) * G + lc;
-  float *dst = (p.nchunk == 1 ? out : part_o) + row * HD + 32 * lg;
-  // (an empty window, only in kPositions, writes zeros)
-  const float sc = p.nchunk == 1 ? (l_part > 0.f ? 1.0f / l_part : 0.f) : 1.0f;
+  // The waves' (m, l, o) into LDS: lane (lc, lg) holds dims 32*lg .. +32 of
+  // head lc, element i of o[e] being dim 8*(4*lg + i) + e.
+  if (lc < G) {
+    float *mo = sm.mo[w][lc] + 32 * lg;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    *reinterpret_cast<f4 *>(dst + 8 * i) = f4{o[0][i], o[1][i], o[2][i], o[3][i]} * sc;
-    *reinterpret_cast<f4 *>(dst + 8 * i + 4) = f4{o[4][i], o[5][i], o[6][i], o[7][i]} * sc;
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<f4 *>(mo + 8 * i) = f4{o[0][i], o[1][i], o[2][i], o[3][i]};
+      *reinterpret_cast<f4 *>(mo + 8 * i + 4) = f4{o[4][i], o[5][i], o[6][i], o[7][i]};
+    }
+    if (lg == 0) sm.mlw[w][lc] = make_float2(m_lane, l_part);
   }
-  if (p.nchunk > 1 && lg == 0)
-    *reinterpret_cast<float2 *>(part_ml + row * 2) = make_float2(m_lane, l_part);
+  __syncthreads();
+  // Thread (g, d) merges element d of head g over the waves (a wave without
+  // keys has m = -inf, l = 0).
+  const int g = tid / HD, d = tid % HD;
+  float M = -INFINITY;
+#pragma unroll
+  for (int v = 0; v < kWaves; ++v) M = fmaxf(M, sm.mlw[v][g].x);
+  float L = 0.f, O = 0.f;
+#pragma unroll
+  for (int v = 0; v < kWaves; ++v) {
+    const float2 ml = sm.mlw[v][g];
+    const float e = ml.x == -INFINITY ? 0.f : fast_exp2(ml.x - M);
+    L = __builtin_fmaf(e, ml.y, L);
+    O = __builtin_fmaf(e, sm.mo[v][g][d], O);
+  }
+  if (p.nchunk == 1) {
+    // (an empty window, only in kPositions, writes zeros)
+    out[((size_t)kvh * G + g) * HD + d] = L > 0.f ? O / L : 0.f;
+  } else {
+    const size_t row = ((size_t)kvh * p.nchunk + chunk) * G + g;
+    part_o[row * HD + d] = O;
+    if (d == 0) *reinterpret_cast<float2 *>(part_ml + row * 2) = make_float2(M, L);
+  }
 }
 
 // Cross-chunk log-sum-exp merge.  Workgroup = (kv head, q head, block of
@@ -466,10 +484,11 @@ size_t decode_scratch_bytes(int n_kv, int g, int nchunk, int n_tok) {
 
 int decode_pick_nchunk(int L, int n_kv, int target_wgs) {
   const int n_tiles = (L + kTile - 1) / kTile;
-  // at least one tile per chunk, at most kMaxChunks chunks
-  const int hgroups = (n_kv + kWaves - 1) / kWaves;
-  int nchunk = (target_wgs + hgroups - 1) / hgroups;
-  if (nchunk > n_tiles) nchunk = n_tiles;
+  // one workgroup per (kv head, chunk), about target_wgs of them; at least
+  // one tile per wave, at most kMaxChunks chunks
+  int nchunk = (target_wgs + n_kv - 1) / n_kv;
+  const int per_wave = (n_tiles + kWaves - 1) / kWaves;
+  if (nchunk > per_wave) nchunk = per_wave;
   if (nchunk > kMaxChunks) nchunk = kMaxChunks;
   if (nchunk < 1) nchunk = 1;
   return nchunk;
@@ -482,7 +501,7 @@ hipError_t launch_decode(const DecodeParams &p, int g, int mode, hipStream_t s, 
   const bool positions = mode == kDecodePositions;
   if (positions && (p.positions == nullptr || p.n_tok < 1 || p.n_tok > 65535))
     return hipErrorInvalidValue;
-  dim3 grid(((p.n_kv + kWaves - 1) / kWaves) * p.nchunk, positions ? p.n_tok : 1), block(kThreads);
+  dim3 grid(p.n_kv * p.nchunk, positions ? p.n_tok : 1), block(kThreads);
   if (mode == kDecodeFused)
     hipExtLaunchKernelGGL(decode_kernel<kFused>, grid, block, 0, s, ev0, ev1, 0, p);
   else if (positions)

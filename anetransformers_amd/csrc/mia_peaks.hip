@@ -39,10 +39,10 @@ __global__ void __launch_bounds__(256) read_stream_kernel(const u4 *__restrict__
 }
 
 // One layer's K and V window read as decode_kernel reads it: one workgroup
-// per chunk, one wave per kv head, chunk c = the 16-slot tiles c, c + nchunk,
-// ... of the window starting at slot `start`, two tiles in flight per wave;
-// K as 16 rows x 64 B per load (the MFMA A-operand layout), V as 4 rows x
-// 256 B.  Slots wrap at max_seq per lane.
+// per (kv head, chunk), 8 waves on that head, chunk c = the 16-slot tiles c,
+// c + nchunk, ... of the window starting at slot `start`, wave w taking every
+// 8th of them, two tiles in flight per wave; every load 4 rows x 256 B.
+// Slots wrap at max_seq per lane.
 __global__ void __launch_bounds__(512, 1) read_ring_kernel(const _Float16 *__restrict__ kc,
                                                            const _Float16 *__restrict__ vc,
                                                            int n_kv, int max_seq, int L,
@@ -51,13 +51,12 @@ __global__ void __launch_bounds__(512, 1) read_ring_kernel(const _Float16 *__res
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int lc = lane & 15, lg = lane >> 4;
-  const int hgroups = (n_kv + kWaves - 1) / kWaves;
-  const int kvh = (blockIdx.x % hgroups) * kWaves + w;
-  const int chunk = blockIdx.x / hgroups;
-  if (kvh >= n_kv) return;
+  const int kvh = blockIdx.x % n_kv;
+  const int chunk = blockIdx.x / n_kv;
   const size_t kv_dim = (size_t)n_kv * HD;
   const int n_tiles = (L + kTile - 1) / kTile;
-  const int count = chunk < n_tiles ? (n_tiles - 1 - chunk) / nchunk + 1 : 0;
+  const int first = chunk + nchunk * w, step = nchunk * kWaves;
+  const int count = first < n_tiles ? (n_tiles - 1 - first) / step + 1 : 0;
   const _Float16 *kb = kc + (size_t)kvh * HD, *vb = vc + (size_t)kvh * HD;
   auto slot = [&](int t) {  // window position t (clamped to the window) -> ring row
     t = t < L ? t : L - 1;
@@ -65,13 +64,13 @@ __global__ void __launch_bounds__(512, 1) read_ring_kernel(const _Float16 *__res
     return (size_t)(s >= max_seq ? s - max_seq : s);
   };
   auto issue = [&](u4 (&b)[8], int i) {
-    const int t0 = (chunk + nchunk * (i < count ? i : count - 1)) * kTile;
-    const _Float16 *ks = kb + slot(t0 + lc) * kv_dim + 8 * lg;
+    const int t0 = (first + step * (i < count ? i : count - 1)) * kTile;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) b[s] = *reinterpret_cast<const u4 *>(ks + 32 * s);
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-      b[4 + m] = *reinterpret_cast<const u4 *>(vb + slot(t0 + 4 * lg + m) * kv_dim + 8 * lc);
+    for (int m = 0; m < 4; ++m) {
+      const size_t off = slot(t0 + 4 * lg + m) * kv_dim + 8 * lc;
+      b[m] = *reinterpret_cast<const u4 *>(kb + off);
+      b[4 + m] = *reinterpret_cast<const u4 *>(vb + off);
+    }
   };
   if (count == 0) return;
   u4 b0[8], b1[8];
@@ -132,8 +131,7 @@ hipError_t launch_peak_read_stream(const void *buf, size_t bytes, int num_cus, h
 
 hipError_t launch_peak_read_ring(const _Float16 *kc, const _Float16 *vc, int n_kv, int max_seq,
                                  int L, int start, int nchunk, hipStream_t s) {
-  const int hgroups = (n_kv + 7) / 8;
-  hipLaunchKernelGGL(read_ring_kernel, dim3(hgroups * nchunk), dim3(512), 0, s, kc, vc, n_kv,
+  hipLaunchKernelGGL(read_ring_kernel, dim3(n_kv * nchunk), dim3(512), 0, s, kc, vc, n_kv,
                      max_seq, L, start, nchunk);
   return hipGetLastError();
 }
