@@ -322,6 +322,13 @@ def cpu_baseline_prefill(n_layers: int = 2):
     O.attention_batch_layers(Q, kc, vc, n_layers, N_HEADS, N_KV, HD, PF_M, PF_START, PF_S,
                              threads=threads)
     dt = time.perf_counter() - t0
+    # one thread: the last 64 tokens of one layer (the longest windows)
+    n1 = 64
+    t0 = time.perf_counter()
+    O.attention_batch_layers(Q[:1, PF_S - n1:], kc[:1], vc[:1], 1, N_HEADS, N_KV, HD, PF_M,
+                             PF_START + PF_S - n1, n1, threads=1)
+    dt1 = time.perf_counter() - t0
+    flop1 = 4 * N_HEADS * HD * sum(PF_START + PF_S - n1 + 1 + i for i in range(n1))
     return {
         "value": round(n_layers * PF_FLOP_PER_LAYER / dt / 1e12, 4),
         "unit": "TFLOP/s",
@@ -330,6 +337,9 @@ def cpu_baseline_prefill(n_layers: int = 2):
         "sample": f"{n_layers} of 32 layers of the same prefill chunk (attention_batch over "
                   f"1536 cached + 512 new); oracle AVX2+F16C timing build, OpenMP over "
                   f"(layer, token, head)",
+        "single_thread_value": round(flop1 / dt1 / 1e12, 5),
+        "single_thread_sample": f"one thread, the last {n1} tokens of one layer "
+                                f"(windows of {PF_START + PF_S - n1 + 1}..{PF_START + PF_S} keys)",
     }
 
 
@@ -390,6 +400,22 @@ class OtherConfigs:
                                               self.vc.ptr + l * lay,
                                               self.out.ptr + l * 8 * N_HEADS * HD * 4, N_HEADS,
                                               N_KV, HD, 65536, 70000, 8, None), "attention_step")
+
+    def c5_sequential(self) -> None:
+        """Config 5 as the reference verifies without a batch path
+        (speculative.h:92-101): 8 decode steps per layer, drafts at positions
+        70000..70007, each written and attended in turn."""
+        lay = 65536 * KV_DIM * 2
+        for l in range(N_LAYERS):
+            for t in range(8):
+                q = self.q.ptr + (l * 8 + t) * N_HEADS * HD * 4
+                k = self.k.ptr + (l * 8 + t) * KV_DIM * 4
+                v = self.v.ptr + (l * 8 + t) * KV_DIM * 4
+                check(self.lib.mia_decode_step(q, k, v, self.th.ptr, self.kc.ptr + l * lay,
+                                               self.vc.ptr + l * lay,
+                                               self.out.ptr + (l * 8 + t) * N_HEADS * HD * 4,
+                                               N_HEADS, N_KV, HD, 65536, 70000 + t, None),
+                      "decode_step")
 
     def c5_staged(self, n_keep: int = 5) -> None:
         """Config 5 with the ring left alone during the 32 layers' attention
@@ -685,8 +711,13 @@ def cpu_other_configs():
     for _ in range(20):
         O.decode_layers(Q, kc, vc, 1, N_HEADS, N_HEADS // N_KV, HD, 4096, 512, threads=threads)
     dt = (time.perf_counter() - t0) / 20
+    t0 = time.perf_counter()
+    for _ in range(5):
+        O.decode_layers(Q, kc, vc, 1, N_HEADS, N_HEADS // N_KV, HD, 4096, 512, threads=1)
+    dt1 = (time.perf_counter() - t0) / 5
     res["1"] = {"value": round(4096 * 513 / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
-                "kind": "port", "sample": "the whole config (1 layer), mean of 20"}
+                "kind": "port", "sample": "the whole config (1 layer), mean of 20",
+                "single_thread_value": round(4096 * 513 / dt1 / 1e9, 3)}
     # config 2: 4 of 32 layers, M 65536, pos 4096 (L 4097)
     n = 4
     kc = g.standard_normal((n, 65536, KV_DIM), np.float32).astype(np.float16).view(np.uint16)
@@ -695,15 +726,26 @@ def cpu_other_configs():
     t0 = time.perf_counter()
     O.decode_layers(Q, kc, vc, n, N_HEADS, N_HEADS // N_KV, HD, 65536, 4096, threads=threads)
     dt = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    O.decode_layers(Q[:1], kc[:1], vc[:1], 1, N_HEADS, N_HEADS // N_KV, HD, 65536, 4096, threads=1)
+    dt1 = time.perf_counter() - t0
     res["2"] = {"value": round(n * 4096 * 4097 / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
-                "kind": "port", "sample": f"{n} of 32 layers"}
+                "kind": "port", "sample": f"{n} of 32 layers",
+                "single_thread_value": round(4096 * 4097 / dt1 / 1e9, 3),
+                "single_thread_sample": "1 layer"}
     # config 5: 1 of 32 layers, 8 queries over the wrapped 65536-slot window
     Q = g.standard_normal((1, 8, N_HEADS * HD), np.float32)
     t0 = time.perf_counter()
     O.attention_batch_layers(Q, kc[:1], vc[:1], 1, N_HEADS, N_KV, HD, 65536, 70000, 8,
                              threads=threads)
     dt = time.perf_counter() - t0
+    Q1 = Q[:, :2]
+    t0 = time.perf_counter()
+    O.attention_batch_layers(Q1, kc[:1], vc[:1], 1, N_HEADS, N_KV, HD, 65536, 70000, 2, threads=1)
+    dt1 = (time.perf_counter() - t0) * 4  # 2 of the 8 queries
     res["5"] = {"value": round(4096 * 65536 / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "single_thread_value": round(4096 * 65536 / dt1 / 1e9, 3),
+                "single_thread_sample": "one thread, 2 of the 8 queries of 1 layer, scaled to 8",
                 "kind": "port",
                 "sample": "1 of 32 layers: attention of the 8 queries over the wrapped window "
                           "(attention_batch on the same shape; the drafts' ring writes are not "
@@ -887,6 +929,7 @@ def main() -> int:
         c2 = timed(lib, oc.c2, args.steps, args.warmup)
         c5 = timed(lib, oc.c5, args.steps, args.warmup)
         c5s = timed(lib, oc.c5_staged, args.steps, args.warmup)
+        c5q = timed(lib, oc.c5_sequential, max(args.steps // 4, 2), 1)
         del oc
         configs = {
             "1": {"workload": "1 layer decode step, 512 filled positions + new token (L 513), M 4096",
@@ -903,6 +946,12 @@ def main() -> int:
                   "value": round(N_LAYERS * 4096 * 65536 / (c5 * 1e-3) / 1e9, 2), "unit": "GB/s",
                   "ms_per_step": round(c5, 4),
                   "accept_only_ms_per_step": round(c5s, 4),
+                  "sequential_ms_per_step": round(c5q, 4),
+                  "sequential_value": round(N_LAYERS * 8 * 4096 * 65536 / (c5q * 1e-3) / 1e9, 2),
+                  "sequential": "the reference's verify without a batch path: 8 x "
+                                "mia_decode_step per layer (fused RoPE, ring write, attention) "
+                                "at positions 70000..70007; value counts the window read once "
+                                "per draft",
                   "accept_only": "mia_attention_step_staged per layer (ring untouched), then one "
                                  "mia_commit_staged of 5 accepted drafts for all 32 layers"},
         }

@@ -94,7 +94,62 @@ def _zero_scales(Wq):
     return B.reshape(Wq.shape)
 
 
+def _identity_q4_0(n):
+    """Q4_0 rows of the n x n identity, exact: in the block holding the
+    diagonal d = 0.25 and that weight's nibble is 12 (0.25 * (12 - 8) = 1);
+    every other nibble is 8 (0) and every other block has d = 0."""
+    nb = n // 32
+    B = np.zeros((n, nb, 18), np.uint8)
+    B[:, :, 2:] = 0x88
+    r = np.arange(n)
+    b, i = r // 32, r % 32
+    B[r, b, 0:2] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+    lo = i < 16
+    B[r[lo], b[lo], 2 + i[lo]] = 0x8C
+    B[r[~lo], b[~lo], 2 + i[~lo] - 16] = 0xC8
+    return B.reshape(n, nb * 18)
+
+
+def test_identity_q4_0_is_exact():
+    W = O.dequant_q4_0(_identity_q4_0(128), 128, 128)
+    assert np.array_equal(W, np.eye(128))
+
+
+@pytest.mark.parametrize("dim,hidden,nh,nkv,M,start,S", [
+    (4096, 1024, 32, 8, 4096, 100, 64),
+    # the prefill workload's sequence shape (S 512 after 1536, 4 q heads per
+    # kv head, hd 128) at 8 q / 2 kv heads, which the oracle runs in seconds
+    (1024, 1024, 8, 2, 4096, 1536, 512),
+    (1024, 1024, 8, 2, 1024, 1500, 200),     # windows past a wrapped ring
+])
+def test_prefill_layer_attention_output(dim, hidden, nh, nkv, M, start, S):
+    # Wo = identity (exact in Q4_0) and W2 = 0: the layer's output minus its
+    # input is then its attention output, held to the attention tolerance
+    # (2e-3 abs / 1e-2 rel) against the oracle's.
+    G.say(f"prefill: layer attention output dim={dim} M={M} start={start} S={S}")
+    L = G.lib()
+    g = np.random.default_rng(7 * S + start)
+    W = _layer(g, dim, hidden, nh, nkv)
+    W["wo"] = _identity_q4_0(dim)
+    W["w2"] = _zero_scales(W["w2"])
+    kvd = dim // nh * nkv
+    kc, vc = D.ring(g, M, kv_dim=kvd, filled=min(start, M))
+    X = g.standard_normal((S, dim)).astype(np.float32)
+    th = O.theta_inv(D.THETA, 128)
+    dev = {k: DB.from_array(v) for k, v in W.items()}
+    lw = mia.LayerWeights(*[dev[n].ptr for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3",
+                                                  "rms_att", "rms_ffn")])
+    dX, dth, dkc, dvc = DB.from_array(X), DB.from_array(th), DB.from_array(kc), DB.from_array(vc)
+    check(L.mia_prefill_layer(dX.ptr, ctypes.byref(lw), dth.ptr, dkc.ptr, dvc.ptr, dim, hidden,
+                              nh, nkv, 1e-5, M, start, S, None), "prefill_layer")
+    check(L.mia_stream_sync(None), "sync")
+    got = dX.download(X.shape, np.float32).astype(np.float64) - X
+    ref = O.prefill_layer(W, X, kc.copy(), vc.copy(), start, S, dim, hidden, nh, nkv, th)
+    D.check_close(got, ref.astype(np.float64) - X, what=f"layer attention S={S} start={start}")
+
+
 @pytest.mark.parametrize("dim,hidden,nh,nkv,M,start,S,wo_zero", [
+    (1024, 1024, 8, 2, 4096, 1536, 512, False),    # S 512 after 1536 (see above)
     (512, 1024, 4, 1, 64, 10, 20, False),
     (512, 1024, 4, 1, 64, 10, 20, True),
     (512, 1024, 4, 1, 256, 0, 130, False),
