@@ -114,3 +114,29 @@ def mistral_like(g, dim=256, n_layers=2, n_heads=8, n_kv=2, hidden=512, vocab=40
     tensors.append(("output_norm.weight", GGML_F32, (dim,),
                     np.ones(dim, np.float32).tobytes()))
     return meta, tensors
+
+
+def malformed_variants(blob: bytes, data_offset: int) -> dict:
+    """Byte-level corruptions of a valid file that a loader must refuse (each
+    one is an error, never a read past the mapping): bad magic and versions,
+    an absurd count, and cuts inside the metadata, the tensor records and
+    the data section."""
+    return {
+        "magic": b"GGUX" + blob[4:],
+        "version1": blob[:4] + (1).to_bytes(4, "little") + blob[8:],
+        "version4": blob[:4] + (4).to_bytes(4, "little") + blob[8:],
+        "huge_count": blob[:8] + (1 << 40).to_bytes(8, "little") + blob[16:],
+        "cut_in_metadata": blob[:200],
+        "cut_in_tensor_infos": blob[:data_offset - 40],
+        "cut_in_data": blob[:data_offset + 100],
+        "short": blob[:10],
+    }
+
+
+def bad_offset_file(path) -> None:
+    """A one-tensor file whose tensor offset points past the end."""
+    write(path, [], [("t", GGML_F32, (8,), bytes(32))])
+    b = bytearray(open(path, "rb").read())
+    i = b.index(b"t") + 1 + 4 + 8 + 4            # name, n_dims, ne[0], type
+    b[i:i + 8] = (1 << 20).to_bytes(8, "little")
+    open(path, "wb").write(bytes(b))

@@ -205,16 +205,7 @@ def test_k_quant_sizes(tmp_path):
 def test_malformed_files_are_errors_not_reads_past_the_end(tmp_path, model_file):
     path, meta, tensors, offs = model_file
     blob = path.read_bytes()
-    cases = {
-        "magic": b"GGUX" + blob[4:],
-        "version1": blob[:4] + (1).to_bytes(4, "little") + blob[8:],
-        "version4": blob[:4] + (4).to_bytes(4, "little") + blob[8:],
-        "huge_count": blob[:8] + (1 << 40).to_bytes(8, "little") + blob[16:],
-        "cut_in_metadata": blob[:200],
-        "cut_in_tensor_infos": blob[:offs["__data__"] - 40],
-        "cut_in_data": blob[:offs["__data__"] + 100],
-        "short": blob[:10],
-    }
+    cases = W.malformed_variants(blob, offs["__data__"])
     for name, data in cases.items():
         p = tmp_path / f"bad_{name}.gguf"
         p.write_bytes(data)
@@ -222,10 +213,6 @@ def test_malformed_files_are_errors_not_reads_past_the_end(tmp_path, model_file)
         assert rc in (mia.MIA_ERR_INVALID, mia.MIA_ERR_UNSUPPORTED), name
     # a tensor offset pointing past the file
     bad = tmp_path / "bad_offset.gguf"
-    W.write(bad, [], [("t", W.GGML_F32, (8,), bytes(32))])
-    b = bytearray(bad.read_bytes())
-    i = b.index(b"t") + 1 + 4 + 8 + 4            # name, n_dims, ne[0], type
-    b[i:i + 8] = (1 << 20).to_bytes(8, "little")
-    bad.write_bytes(bytes(b))
+    W.bad_offset_file(bad)
     assert open_rc(bad) == mia.MIA_ERR_INVALID
     assert open_rc(tmp_path / "missing.gguf") == mia.MIA_ERR_INVALID
