@@ -943,8 +943,17 @@ int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_
   if (int rc = gemm_impl(c, lw->wq, lw->wk, lw->wv, dim, kv_dim, kv_dim, nullptr, dim, S, Q, K,
                          V, mia::kGemmStore, s, /*reuse_split=*/true))
     return rc;
-  if (int rc = mia_attention_step(Q, K, V, theta_inv, k_layer, v_layer, A, n_heads, n_kv_heads,
-                                  kHD, max_seq, start_pos, S, s))
+  // apply_rope_batch, kv_write_batch, attention_batch (:1097-1098): every
+  // token's K/V go into the ring first and each query attends the ring as
+  // it then stands; the (cos, sin) table of the positions lands in the work
+  // buffer, from which the attention kernel rotates Q.
+  if (int rc = ensure_work(c, (size_t)S * kHD * sizeof(float))) return rc;
+  float *cs = reinterpret_cast<float *>(c->work);
+  HIP_TRY(mia::launch_rope_to_ring(K, V, theta_inv, S, start_pos, n_kv_heads,
+                                   reinterpret_cast<_Float16 *>(k_layer),
+                                   reinterpret_cast<_Float16 *>(v_layer), max_seq, cs, s));
+  if (int rc = flash_impl(c, Q, cs, nullptr, nullptr, k_layer, v_layer, A, n_kv_heads, max_seq,
+                          start_pos, S, s))
     return rc;
   if (int rc = gemm_impl(c, lw->wo, nullptr, nullptr, dim, 0, 0, A, dim, S, X, nullptr, nullptr,
                          mia::kGemmAdd, s))

@@ -42,6 +42,9 @@ __global__ void rope_kernel(float *q, float *k, int S, int start_pos, const floa
 // dims (4 adjacent pairs, mistral_model.h:100-105) of one kv head of K, rounds
 // K and V to fp16 (RNE, mistral_model.h:160-169) and writes them to the ring
 // slot pos % max_seq (kv_write, kv_cache.h:53-57) or to a dense staging row.
+// With more tokens than ring slots, token t shares its slot with t + max_seq:
+// the reference writes in token order (kv_write_batch), so tokens
+// t < S - max_seq write nothing (their (cos, sin) rows are still stored).
 __global__ void __launch_bounds__(128)
     rope_kv_f16_kernel(const float *K, const float *V, const float *theta_inv, int S, int start_pos,
                        int n_kv, _Float16 *kdst, _Float16 *vdst, int max_seq, bool ring,
@@ -72,6 +75,7 @@ __global__ void __launch_bounds__(128)
     if (cs_out) reinterpret_cast<float2 *>(cs_out)[(size_t)t * (HD / 2) + tid] = make_float2(c, sn);
   }
   __syncthreads();
+  if (ring && t < S - max_seq) return;
   const size_t drow = ring ? (size_t)(pos % max_seq) : (size_t)t;
   for (int c = tid; c < n_items; c += blockDim.x) {
     const int e0 = (c >> 4) * HD + 8 * (c & 15);

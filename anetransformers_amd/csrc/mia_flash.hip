@@ -15,7 +15,11 @@
 //   K, V tiles        global -> LDS directly (global_load_lds, 16 B per lane),
 //                     double-buffered, issued one tile ahead of use
 //   S^T = K . Q^T     v_mfma_f32_32x32x16_f16, A = K rows (ds_read_b128),
-//                     B = Q^T held in registers (fp16, RoPE and scale applied)
+//                     B = Q^T held in registers as two fp16 parts, hi and
+//                     lo (q = hi + lo to ~2^-22, RoPE and scale applied):
+//                     each k-step is two MFMAs, so the scores carry fp32 q
+//                     accuracy (fp16 q alone errs by 2^-12 |q| |k| per
+//                     score, visible in the output once scores are large)
 //   online softmax    one row per lane (the D column): running max and sum
 //                     stay lane-local; the two key halves of a row meet via
 //                     a lane exchange; P rounded to fp16 with v_cvt_pk and
@@ -423,6 +427,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   if (g_count > 1) wait_vmcnt<24>();
   else if (g_count == 1) wait_vmcnt<16>();
   else wait_vmcnt<0>();
+  u4 q_lo_keep[2 * NB];
 #pragma unroll
   for (int k = 0; k < 2 * NB; ++k) {
     const int u = lane + 64 * k;
@@ -441,25 +446,44 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       rope_pair(v[4], v[5], c1.x, c1.y);
       rope_pair(v[6], v[7], c1.z, c1.w);
     }
-    u4 packed = {0u, 0u, 0u, 0u};
+    u4 packed = {0u, 0u, 0u, 0u}, packed_lo = {0u, 0u, 0u, 0u};
     if (t < p.S) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        packed[e] = __builtin_bit_cast(
-            unsigned, __builtin_convertvector(
-                          (f2){v[2 * e] * p.qscale, v[2 * e + 1] * p.qscale}, h2));
+      for (int e = 0; e < 4; ++e) {
+        const f2 x = {v[2 * e] * p.qscale, v[2 * e + 1] * p.qscale};
+        const h2 hi = __builtin_convertvector(x, h2);
+        const h2 lo = __builtin_convertvector(x - __builtin_convertvector(hi, f2), h2);
+        packed[e] = __builtin_bit_cast(unsigned, hi);
+        packed_lo[e] = __builtin_bit_cast(unsigned, lo);
+      }
     }
     *(lds_u4 *)(qs + rl * HD + 8 * (ch ^ swz(rl))) = packed;
+    q_lo_keep[k] = packed_lo;
   }
   __syncthreads();
 
-  // Q^T operands: column = row, k-step st covers dims 16*st + 8*half .. +8.
-  h8 qb[NB][8];
+  // Q^T operands: column = row, k-step st covers dims 16*st + 8*half .. +8;
+  // the hi parts, then (through the same LDS rows) the lo parts.
+  h8 qb[NB][8], ql[NB][8];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int st = 0; st < 8; ++st)
       qb[b][st] = *(lds_h8 *)(qs + (32 * b + col) * HD + 8 * ((2 * st + half) ^ swz(col)));
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 2 * NB; ++k) {
+    const int u = lane + 64 * k;
+    const int rw = u >> 4, ch = u & 15;
+    const int rl = 8 * NB * w + rw;
+    *(lds_u4 *)(qs + rl * HD + 8 * (ch ^ swz(rl))) = q_lo_keep[k];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int st = 0; st < 8; ++st)
+      ql[b][st] = *(lds_h8 *)(qs + (32 * b + col) * HD + 8 * ((2 * st + half) ^ swz(col)));
 
   // Softmax reference per row, fixed for the whole key range of the wave:
   // the max of the row's scores in its first tile (p <= 1 there), rounded to
@@ -561,8 +585,10 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) sc[b][i] = 0.f;
 #pragma unroll
-      for (int st = 0; st < 8; ++st)
+      for (int st = 0; st < 8; ++st) {
         sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st], sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], ql[b][st], sc[b], 0, 0, 0);
+      }
     }
     if (needs_mask(kb)) mask_tile(sc, kb);
   };
@@ -620,6 +646,8 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     auto qk = [&](int st, int b) {
       s_next[b] =
           __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st & 3], qb[b][st], s_next[b], 0, 0, 0);
+      s_next[b] =
+          __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st & 3], ql[b][st], s_next[b], 0, 0, 0);
     };
     // scores of tile it+1: reference k-step, then k-steps 0-3
 #pragma unroll
@@ -776,6 +804,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     };
     auto QK = [&](int st, int b) {
       s_out[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st], s_out[b], 0, 0, 0);
+      s_out[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], ql[b][st], s_out[b], 0, 0, 0);
     };
     auto PVL = [&](int db, int b) {
       if (with_pv) mfma_pv(o[b][db], vlo[db], p_in[b][0]);
