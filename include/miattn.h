@@ -260,12 +260,14 @@ typedef struct {
  * X [S][dim] fp32 dev is updated in place (X += attention(...) . Wo^T, then
  * X += SwiGLU(...) . W2^T), the layer's ring gets the S rotated fp16 K/V at
  * slots (start_pos + t) % max_seq.  dim = n_heads * 128, hidden and dim
- * multiples of 64.  The attention step is mia_attention_step's, i.e. the
- * sequential semantics: the same as the reference's write-all-then-attend
- * whenever start_pos + S <= max_seq; when a chunk wraps the ring, earlier
- * tokens do not see later tokens' K/V in recycled slots (the reference's
- * attention_batch does).  Activations live in a per-device work area
- * (58 MB at S = 512). */
+ * multiples of 64.  The attention step is the reference's
+ * apply_rope_batch + kv_write_batch + attention_batch (:1096-1098): all S
+ * tokens' K/V are written first (a token that a later token of the chunk
+ * overwrites writes nothing, as the in-order writes leave it), then every
+ * query attends the ring as it then stands, so when a chunk wraps the ring
+ * earlier tokens see later tokens' K/V in recycled slots, as the reference's
+ * do.  (mia_attention_step instead has the sequential-verify semantics.)
+ * Activations live in a per-device work area (58 MB at S = 512). */
 int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_inv,
                       uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden, int n_heads,
                       int n_kv_heads, float eps, int max_seq, int start_pos, int S,
