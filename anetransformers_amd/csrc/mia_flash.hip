@@ -27,8 +27,11 @@
 //   O^T += V^T . P^T  P^T straight from the S^T accumulator layout, V^T via
 //                     the transposing LDS read ds_read_b64_tr_b16
 // The scores of tile i+1 are computed on MFMA while the exponentials of tile
-// i are formed.  The running max moves lazily (only when a score exceeds it
-// by more than 8 in log2 units), so the accumulators are rarely rescaled.
+// i are formed.  Each row's softmax reference is fixed for the whole key
+// range (its first tile's max, subtracted inside the score MFMA by one extra
+// k-step), so the loop neither tracks maxima nor rescales; a row whose later
+// scores overflow or underflow the fp16 P shows it in its row sum, and its
+// wave runs again from the exact row maxima.
 //
 // Query t at position start+t attends the window [pos-L+1, pos], L =
 // min(pos+1, max_seq) (mistral_ane_prefill.h:220-241); positions >= start come
