@@ -273,7 +273,14 @@ __device__ __forceinline__ void pv_drain_all(f16v (&o)[NB][4]) {
 __device__ __forceinline__ float half_swap_max(float m) { return fmaxf(m, __shfl_xor(m, 32)); }
 __device__ __forceinline__ float half_swap_sum(float x) { return x + __shfl_xor(x, 32); }
 
-template <int NB>
+// FAST: every key range starts at key 0 of an unwrapped ring with no staged
+// rows and holds at least one whole tile (flash_fast_ok), so every tile's 32
+// rows are 32 consecutive ring slots: all loads take the uniform-base form,
+// and the last, partial tile of a range is loaded as the 32 keys ending at
+// the range end, with the keys before the tile's own start masked.  The
+// generic kernel handles wrapped windows, staged rows and short ranges with
+// per-lane addresses on the tiles that need them.
+template <int NB, bool FAST>
 __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   using L = Lay<NB>;
   constexpr int RT = 32 * NB;  // rows per workgroup
@@ -367,6 +374,8 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   const _Float16 *const kc = p.kc, *const vc = p.vc;
   const _Float16 *const kst = p.kstage, *const vst = p.vstage;
   auto tile_slot = [&](int i) { return (kb0 + kStride * i) % p.max_seq; };
+  // FAST: first key (= ring slot) of the 32 rows loaded for tile i.
+  auto fast_slot = [&](int i) { return min(kb0 + kStride * i, ke - kKT); };
   // Ring slots of the next K and V tiles to load, advanced by one stride per
   // load (no division in the tile loop).
   int kslot = 0, vslot = 0;
@@ -374,31 +383,56 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     s += kStride;
     return s < p.max_seq ? s : (s - p.max_seq < p.max_seq ? s - p.max_seq : s % p.max_seq);
   };
-#define MIA_LOAD_K(i, buf)                                                                  \
-  load_tile(kc, kst, kb0 + kStride * (i), tile_slot(i), ke, p.start_pos, p.max_seq, kv_dim, \
-            kvh * HD, boff, lane, kt_a[buf])
-#define MIA_LOAD_V(i, buf)                                                                  \
-  load_tile(vc, vst, kb0 + kStride * (i), tile_slot(i), ke, p.start_pos, p.max_seq, kv_dim, \
-            kvh * HD, boff, lane, vt_a[buf])
-#define MIA_LOAD_K_NEXT(i, buf)                                                            \
-  do {                                                                                     \
-    load_tile(kc, kst, kb0 + kStride * (i), kslot, ke, p.start_pos, p.max_seq, kv_dim,     \
-              kvh * HD, boff, lane, kt_a[buf]);                                            \
-    kslot = advance(kslot);                                                                \
+#define MIA_LOAD_FAST(ring, i, dst)                                        \
+  do {                                                                     \
+    const _Float16 *base_ = (ring) + (size_t)fast_slot(i) * kv_dim;        \
+    dma8_sb(base_, base_ + (size_t)16 * kv_dim, boff, dst);                \
   } while (0)
-#define MIA_LOAD_V_NEXT(i, buf)                                                            \
-  do {                                                                                     \
-    load_tile(vc, vst, kb0 + kStride * (i), vslot, ke, p.start_pos, p.max_seq, kv_dim,     \
-              kvh * HD, boff, lane, vt_a[buf]);                                            \
-    vslot = advance(vslot);                                                                \
+#define MIA_LOAD_K(i, buf)                                                                    \
+  do {                                                                                        \
+    if constexpr (FAST)                                                                       \
+      MIA_LOAD_FAST(kc, i, kt_a[buf]);                                                        \
+    else                                                                                      \
+      load_tile(kc, kst, kb0 + kStride * (i), tile_slot(i), ke, p.start_pos, p.max_seq,       \
+                kv_dim, kvh * HD, boff, lane, kt_a[buf]);                                     \
+  } while (0)
+#define MIA_LOAD_V(i, buf)                                                                    \
+  do {                                                                                        \
+    if constexpr (FAST)                                                                       \
+      MIA_LOAD_FAST(vc, i, vt_a[buf]);                                                        \
+    else                                                                                      \
+      load_tile(vc, vst, kb0 + kStride * (i), tile_slot(i), ke, p.start_pos, p.max_seq,       \
+                kv_dim, kvh * HD, boff, lane, vt_a[buf]);                                     \
+  } while (0)
+#define MIA_LOAD_K_NEXT(i, buf)                                                              \
+  do {                                                                                       \
+    if constexpr (FAST) {                                                                    \
+      MIA_LOAD_FAST(kc, i, kt_a[buf]);                                                       \
+    } else {                                                                                 \
+      load_tile(kc, kst, kb0 + kStride * (i), kslot, ke, p.start_pos, p.max_seq, kv_dim,     \
+                kvh * HD, boff, lane, kt_a[buf]);                                            \
+      kslot = advance(kslot);                                                                \
+    }                                                                                        \
+  } while (0)
+#define MIA_LOAD_V_NEXT(i, buf)                                                              \
+  do {                                                                                       \
+    if constexpr (FAST) {                                                                    \
+      MIA_LOAD_FAST(vc, i, vt_a[buf]);                                                       \
+    } else {                                                                                 \
+      load_tile(vc, vst, kb0 + kStride * (i), vslot, ke, p.start_pos, p.max_seq, kv_dim,     \
+                kvh * HD, boff, lane, vt_a[buf]);                                            \
+      vslot = advance(vslot);                                                                \
+    }                                                                                        \
   } while (0)
   // K0, K1, then V0: V(i) is first needed one step after K(i+1).
   auto issue_first_tiles = [&]() {
     if (g_count > 0) MIA_LOAD_K(0, 0);
     if (g_count > 1) MIA_LOAD_K(1, 1);
     if (g_count > 0) MIA_LOAD_V(0, 0);
-    kslot = tile_slot(2);
-    vslot = tile_slot(1);
+    if constexpr (!FAST) {
+      kslot = tile_slot(2);
+      vslot = tile_slot(1);
+    }
   };
   // Q rows -> fp16 in LDS: RoPE (table of fl32(theta_inv[i] * pos) cos/sin
   // written by the K rotation, mistral_model.h:87-105) and the score scale
@@ -535,14 +569,15 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       m = m || !bfull[b] || kb < lo_max[b] || kb + kKT - 1 > hi_min[b];
     return m;
   };
-  // Keys outside the row's window become -inf; s[i] is key
-  // kb + (i/4)*8 + 4*half + (i%4) for the lane's row.
+  // Keys outside the row's window, and keys before kb, become -inf; s[i] is
+  // key kbl + (i/4)*8 + 4*half + (i%4) for the lane's row, kbl the tile's
+  // first loaded key (kb except for a FAST kernel's last tile).
   // (The row bounds pass through an empty asm so that the compiler cannot
   // evaluate the per-score compares once for all tiles, ahead of the loop:
   // masks are rare, and the hoisted lane masks would be spilled.)
-  auto mask_block = [&](f16v &s, int b, int kb) {
-    int lo = valid[b] ? lo_t[b] - kb - 4 * half : INT_MAX;
-    int hi = min(hi_t[b], ke - 1) - kb - 4 * half;
+  auto mask_block = [&](f16v &s, int b, int kb, int kbl) {
+    int lo = valid[b] ? max(lo_t[b], kb) - kbl - 4 * half : INT_MAX;
+    int hi = min(hi_t[b], ke - 1) - kbl - 4 * half;
     asm volatile("" : "+v"(lo), "+v"(hi));
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -560,7 +595,8 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     for (int i = 0; i < 16; ++i) s[i] = (i >> 2) * 8 + (i & 3) <= hr ? s[i] : -INFINITY;
   };
   auto mask_tile = [&](f16v (&sc)[NB], int kb) {
-    bool lo_free = true;
+    const int kbl = FAST ? min(kb, ke - kKT) : kb;
+    bool lo_free = kbl == kb;
 #pragma unroll
     for (int b = 0; b < NB; ++b) lo_free = lo_free && kb >= lo_max[b];
     if (lo_free) {
@@ -568,7 +604,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       for (int b = 0; b < NB; ++b) mask_hi(sc[b], b, kb);
     } else {
 #pragma unroll
-      for (int b = 0; b < NB; ++b) mask_block(sc[b], b, kb);
+      for (int b = 0; b < NB; ++b) mask_block(sc[b], b, kb, kbl);
     }
   };
   // Row max of a score block over both key halves.
@@ -1028,6 +1064,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     }
     if (pass == 1 || __builtin_amdgcn_ballot_w64(bad) == 0) break;
   }
+#undef MIA_LOAD_FAST
 #undef MIA_LOAD_K
 #undef MIA_LOAD_V
 #undef MIA_LOAD_K_NEXT
@@ -1208,27 +1245,44 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(FlashParams p, int rt)
   }
 }
 
-template <int NB>
+template <int NB, bool FAST>
 hipError_t set_lds_limit() {
-  return hipFuncSetAttribute((const void *)flash_kernel<NB>,
+  return hipFuncSetAttribute((const void *)flash_kernel<NB, FAST>,
                              hipFuncAttributeMaxDynamicSharedMemorySize, Lay<NB>::kBytes);
+}
+
+int rows_per_tile(int S) { return S * 4 <= 32 ? 32 : 64; }
+
+// The FAST kernel's conditions: no staged rows, no key split, no window
+// reaching past the ring's end (every row's window starts at key 0 and no
+// tile wraps), and every workgroup's key range at least one tile long (the
+// shortest is the first row tile's, start_pos + its query count).
+bool flash_fast_ok(const FlashParams &p) {
+  const int first_rows = rows_per_tile(p.S) / 4;
+  return p.kstage == nullptr && p.vstage == nullptr && p.nsplit == 1 &&
+         (long)p.start_pos + p.S <= (long)p.max_seq &&
+         (long)p.start_pos + (p.S < first_rows ? p.S : first_rows) >= kKT;
 }
 
 template <int NB>
 hipError_t launch_variant(const FlashParams &p, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   using L = Lay<NB>;
   dim3 grid(p.n_kv * p.n_rtiles * p.nsplit);
-  hipExtLaunchKernelGGL((flash_kernel<NB>), grid, dim3(256), L::kBytes, s, ev0, ev1, 0, p);
+  if (flash_fast_ok(p))
+    hipExtLaunchKernelGGL((flash_kernel<NB, true>), grid, dim3(256), L::kBytes, s, ev0, ev1, 0, p);
+  else
+    hipExtLaunchKernelGGL((flash_kernel<NB, false>), grid, dim3(256), L::kBytes, s, ev0, ev1, 0,
+                          p);
   return hipGetLastError();
 }
-
-int rows_per_tile(int S) { return S * 4 <= 32 ? 32 : 64; }
 
 }  // namespace
 
 hipError_t prepare_flash() {
-  hipError_t e = set_lds_limit<1>();
-  return e != hipSuccess ? e : set_lds_limit<2>();
+  hipError_t e = set_lds_limit<1, false>();
+  if (e == hipSuccess) e = set_lds_limit<2, false>();
+  if (e == hipSuccess) e = set_lds_limit<1, true>();
+  return e != hipSuccess ? e : set_lds_limit<2, true>();
 }
 
 size_t flash_scratch_bytes(int n_kv, int n_rtiles, int nsplit, int rows_per_tile) {

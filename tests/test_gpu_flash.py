@@ -59,6 +59,28 @@ def test_attention_batch_shapes(start, S):
     D.check_close(out, ref, what=f"start={start} S={S}")
 
 
+@pytest.mark.parametrize("start,S", [(16, 16), (17, 40), (15, 50), (100, 9), (1536, 200), (27, 5),
+                                     (28, 8), (40, 3), (24, 5), (2000, 48)])
+def test_attention_batch_slots_past_range_unread(start, S):
+    # Every ring slot from start + S on holds fp16 NaN: a key range whose
+    # last tile is partial must neither read those slots nor let them reach
+    # the output (0 x NaN in P.V).  The cases put the range end on and off
+    # the 32-key tile grid, with ranges of exactly one tile (16 + 16,
+    # 27 + 5), a last tile of 1..31 keys, 32- and 64-row tiles, and starts
+    # that take the per-lane load path (15, 24) and the uniform one.
+    G.say(f"attention_batch NaN past the range start={start} S={S}")
+    g = D.rng(70 + start + S)
+    M = 4096
+    kc, vc = D.ring(g, M, filled=start + S)
+    kc[start + S:] = 0x7E00
+    vc[start + S:] = 0x7E00
+    Q = D.normal(g, (S, 4096))
+    out = G.attention_batch(Q, kc, vc, M, start, S)
+    assert np.isfinite(out).all(), f"non-finite output start={start} S={S}"
+    ref = O.attention_batch(Q, kc, vc, 32, 8, 128, M, start, S)
+    D.check_close(out, ref, what=f"NaN past range start={start} S={S}")
+
+
 @pytest.mark.parametrize("sigma", [2.0, 4.0, 6.0])
 def test_attention_batch_large_scores(sigma):
     # Q ~ sigma N(0,1) fp32 and K ~ sigma N(0,1) fp16: scores of order
