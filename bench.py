@@ -932,14 +932,26 @@ def main() -> int:
         c5 = timed(lib, oc.c5, args.steps, args.warmup)
         c5s = timed(lib, oc.c5_staged, args.steps, args.warmup)
         c5q = timed(lib, oc.c5_sequential, max(args.steps // 4, 2), 1)
+        # the main kernel of each config (kind 0 decode, 1 flash) from the
+        # dispatch-stamped events, against its algorithmic window bytes
+        k1 = kernel_avg_ms(lib, oc.c1, 50, 0)
+        k2 = kernel_avg_ms(lib, oc.c2, 2, 0)
+        k5 = kernel_avg_ms(lib, oc.c5, 2, 1)
         del oc
+
+        def kroof(nbytes: int, ms: float) -> dict:
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            return {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
         configs = {
             "1": {"workload": "1 layer decode step, 512 filled positions + new token (L 513), M 4096",
                   "value": round(4096 * 513 / (c1 * 1e-3) / 1e9, 2), "unit": "GB/s",
-                  "ms_per_step": round(c1, 5)},
+                  "ms_per_step": round(c1, 5), "kernel_us": round(k1 * 1e3, 2),
+                  "roofline": kroof(4096 * 513, k1)},
             "2": {"workload": "32-layer decode step, 4096 filled + new token (L 4097), M 65536",
                   "value": round(N_LAYERS * 4096 * 4097 / (c2 * 1e-3) / 1e9, 2), "unit": "GB/s",
-                  "ms_per_step": round(c2, 4)},
+                  "ms_per_step": round(c2, 4), "kernel_us": round(k2 * 1e3, 2),
+                  "roofline": kroof(4096 * 4097, k2)},
             "3": {"workload": "the headline (value)"},
             "4": {"workload": "the prefill object"},
             "5": {"workload": "32-layer speculative verify, 8 drafts at positions 70000..70007 "
@@ -947,6 +959,10 @@ def main() -> int:
                               "attention)",
                   "value": round(N_LAYERS * 4096 * 65536 / (c5 * 1e-3) / 1e9, 2), "unit": "GB/s",
                   "ms_per_step": round(c5, 4),
+                  "kernel_us": round(k5 * 1e3, 2),
+                  "kernel": "flash_kernel (32-row tiles, key range split over workgroups); "
+                            "the split merge and the commit of the drafts are in ms_per_step",
+                  "roofline": kroof(4096 * 65536, k5),
                   "accept_only_ms_per_step": round(c5s, 4),
                   "sequential_ms_per_step": round(c5q, 4),
                   "sequential_value": round(N_LAYERS * 8 * 4096 * 65536 / (c5q * 1e-3) / 1e9, 2),
@@ -958,7 +974,8 @@ def main() -> int:
                                  "mia_commit_staged of 5 accepted drafts for all 32 layers"},
         }
         log(f"config 1: {c1 * 1e3:.1f} us; config 2: {c2:.3f} ms; config 5: {c5:.3f} ms "
-            f"({c5s:.3f} ms staged + accept-only commit)")
+            f"({c5s:.3f} ms staged + accept-only commit); kernels {k1 * 1e3:.2f} / "
+            f"{k2 * 1e3:.2f} / {k5 * 1e3:.2f} us")
 
     cpu = None
     if not args.no_cpu_baseline:
