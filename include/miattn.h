@@ -245,7 +245,12 @@ int mia_rmsnorm_f32(float *out, const float *in, const float *w, int dim, int S,
  * (dev, 16-byte aligned), in_dim a multiple of 64.  fp16 MFMA on X split into
  * hi + lo halves (per-device scratch of S * in_dim * 4 bytes) with the block
  * scales applied in fp32: within fp32 rounding of the reference's sums, not
- * bit-identical to them. */
+ * bit-identical to them.  Range: the hi half is fp16, so every |x| must be
+ * below 65504 (larger values give non-finite outputs, where the reference's
+ * fp32 product stays finite); below 2^-3 the lo half is subnormal and x is
+ * carried to 2^-25 absolute rather than 2^-22 relative.  The same holds for
+ * every GEMM input of mia_prefill_layer (the RMSNorm outputs, the attention
+ * output and the SwiGLU product). */
 int mia_q4_0_gemm_f32(const void *W, const float *X, float *Y, int out_dim, int in_dim, int S,
                       void *stream);
 

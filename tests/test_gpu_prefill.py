@@ -102,6 +102,31 @@ def _zero_scales(Wq):
     return B.reshape(Wq.shape)
 
 
+def test_q4_gemm_activation_range():
+    # The fp16 hi half bounds the activations: rows whose entries reach
+    # 6e4 (hi ulp 32, lo still exact) meet the GEMM bound; a row holding
+    # 7e4 (above the fp16 maximum 65504) comes out non-finite, as the
+    # header states, and leaves the other rows untouched.
+    G.say("prefill: q4 gemm activation range")
+    S, out_dim, in_dim = 6, 64, 256
+    g = np.random.default_rng(77)
+    W = O.make_q4_0(g, out_dim, in_dim)
+    X = g.standard_normal((S, in_dim)).astype(np.float32)
+    X[1, ::7] = 6.0e4 * np.sign(X[1, ::7])
+    X[2, 5] = -65000.0
+    X[4, 9] = 7.0e4
+    got = gpu_gemm(W, X, out_dim, in_dim)
+    ref = O.q4_0_gemm(W, out_dim, in_dim, X)
+    ok = [0, 1, 2, 3, 5]
+    assert not np.isfinite(got[4]).any()
+    assert np.isfinite(got[ok]).all()
+    Wd = O.dequant_q4_0(W, out_dim, in_dim)
+    mag = np.abs(X[ok].astype(np.float64)) @ np.abs(Wd).T
+    bound = 2 * in_dim * 2.0 ** -24 * mag + in_dim * 6e-8 * np.abs(Wd).max()
+    err = np.abs(got[ok].astype(np.float64) - ref[ok])
+    assert np.all(err <= bound), float((err / bound).max())
+
+
 def _identity_q4_0(n):
     """Q4_0 rows of the n x n identity, exact: in the block holding the
     diagonal d = 0.25 and that weight's nibble is 12 (0.25 * (12 - 8) = 1);
