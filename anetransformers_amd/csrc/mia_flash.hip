@@ -22,8 +22,11 @@
 //                     score, visible in the output once scores are large)
 //   online softmax    one row per lane (the D column): running max and sum
 //                     stay lane-local; the two key halves of a row meet via
-//                     a lane exchange; P rounded to fp16 with v_cvt_pk and
-//                     summed in fp32 with v_dot2 (the same P feeds P.V)
+//                     a lane exchange; the fp32 exponentials are summed in
+//                     fp32 and rounded to fp16 for P.V with v_cvt_pk (a
+//                     v_dot2 of the fp16 pairs would hold up the next MFMA's
+//                     issue by ~17 cycles; fp16 P then differs from the
+//                     summed weights by at most 2^-12 relative)
 //   O^T += V^T . P^T  P^T straight from the S^T accumulator layout, V^T via
 //                     the transposing LDS read ds_read_b64_tr_b16
 // The scores of tile i+1 are computed on MFMA while the exponentials of tile
@@ -529,9 +532,11 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   // tracks maxima and never rescales the accumulators.  P is fp16, so a later
   // score more than ~16 (log2 units) above the reference overflows, and a row
   // whose scores all sit far below an unset reference underflows: both show in
-  // the row sum at the end of the pass (not finite, or below 2^-8).  Such a
-  // wave sweeps its tiles for the exact row maxima and runs once more with
-  // them as the reference.
+  // the fp32 row sum of the unrounded P at the end of the pass (a P that
+  // rounds to fp16 infinity, >= 65520, makes the sum at least that; an
+  // underflowing row sums below 2^-8).  Such a wave sweeps its tiles for the
+  // exact row maxima and runs once more with them as the reference (a row
+  // whose sum is merely large, >= 65504 with no P overflowing, reruns too).
   f16v o[NB][4];
   float m_ref[NB], l_run[NB];
   f16v s_cur[NB];
@@ -632,7 +637,6 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     if (needs_mask(kb)) mask_tile(sc, kb);
   };
 
-  const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
   // One tile step, with P.V one tile behind the scores: P of tile it from
   // s_cur (already shifted by the reference) into pb_next, shifted scores of
   // tile it+1 into s_cur, and (from it = 1 on) O += P.V of tile it-1 from
@@ -673,8 +677,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       const float p2 = fast_exp2(s_cur[b][i + 2]), p3 = fast_exp2(s_cur[b][i + 3]);
       const h2 pp0 = __builtin_convertvector((f2){p0, p1}, h2);
       const h2 pp1 = __builtin_convertvector((f2){p2, p3}, h2);
-      ls[b] = __builtin_amdgcn_fdot2(pp0, ones, ls[b], false);
-      ls[b] = __builtin_amdgcn_fdot2(pp1, ones, ls[b], false);
+      ls[b] = ((ls[b] + p0) + p1) + (p2 + p3);
       pw[b][i >> 3][(i & 7) >> 1] = __builtin_bit_cast(unsigned, pp0);
       pw[b][i >> 3][((i & 7) >> 1) + 1] = __builtin_bit_cast(unsigned, pp1);
       // used only by the next step: pinned here so that the work is not
@@ -826,13 +829,13 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     auto E = [&](int j, int k) {
       const int b = j >> 2, e = 4 * (j & 3) + k;
       ex[k] = fast_exp2(s_in[b][e]);
+      ls[b] += ex[k];
       if (k & 1) {
         const h2 pp = __builtin_convertvector((f2){ex[k - 1], ex[k]}, h2);
-        ls[b] = __builtin_amdgcn_fdot2(pp, ones, ls[b], false);
         pw[b][e >> 3][((e - 1) & 7) >> 1] = __builtin_bit_cast(unsigned, pp);
         asm volatile("" ::"v"(pp), "v"(ls[b]));
       } else {
-        asm volatile("" ::"v"(ex[k]));
+        asm volatile("" ::"v"(ex[k]), "v"(ls[b]));
       }
     };
     auto REF = [&](int b) {
@@ -1053,14 +1056,15 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
         last_pv();
       }
     }
-    // Row sums: overflow (not finite) or underflow (< 2^-8 with keys in range)
-    // means the reference did not suit the row.
+    // Row sums: a possible fp16 overflow of some P (sum >= 65504, or not
+    // finite) or underflow (< 2^-8 with keys in range) means the reference did
+    // not suit the row.
     bool bad = false;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const float lt = half_swap_sum(l_run[b]);
       l_run[b] = lt;
-      bad = bad || (has_keys[b] && !(lt >= 0.00390625f && lt <= 3.0e38f));
+      bad = bad || (has_keys[b] && !(lt >= 0.00390625f && lt < 65504.0f));
     }
     if (pass == 1 || __builtin_amdgcn_ballot_w64(bad) == 0) break;
   }
