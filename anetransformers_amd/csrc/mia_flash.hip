@@ -240,6 +240,42 @@ __device__ __forceinline__ h8 read_va(unsigned va_base) {
 __device__ __forceinline__ void mfma_pv(f16v &acc, const h8 &a, const h8 &b) {
   asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
+// S^T += K . Q^T over one k-step, hi part then lo part of Q^T, both read
+// from AGPRs.  Q^T is loop-invariant (128 registers at 64 rows): held in
+// AGPRs, it leaves the VGPR file to the scores, P, the K / V^T operands and
+// the addresses, which otherwise spill into AGPRs and are copied back right
+// before their MFMAs (the A/B operands of an MFMA may be AGPRs).  Inline
+// assembly, so the hazard recognizer does not see that it writes acc: VALU
+// readers of acc come after qk_drain.  An MFMA result read as SrcC by the
+// next MFMA (exactly overlapped, the same opcode) needs no wait states.
+__device__ __forceinline__ void mfma_qk(f16v &acc, const h8 &k, const h8 &qh, const h8 &ql) {
+  asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0\n\t"
+      "v_mfma_f32_32x32x16_f16 %0, %1, %3, %0"
+      : "+v"(acc)
+      : "v"(k), "a"(qh), "a"(ql));
+}
+// The same as the first MFMAs after VALU writes of acc or of the Q^T AGPRs
+// (zeroed scores, the prologue's AGPR writes): the leading wait states cover
+// those writes.
+__device__ __forceinline__ void mfma_qk_first(f16v &acc, const h8 &k, const h8 &qh,
+                                              const h8 &ql) {
+  asm("s_nop 4\n\t"
+      "v_mfma_f32_32x32x16_f16 %0, %1, %2, %0\n\t"
+      "v_mfma_f32_32x32x16_f16 %0, %1, %3, %0"
+      : "+v"(acc)
+      : "v"(k), "a"(qh), "a"(ql));
+}
+// Before VALU reads of scores written by mfma_qk: more wait states than an
+// 8-pass MFMA's result latency, and a data dependence on every score
+// register so that no read is scheduled above it.
+template <int NB>
+__device__ __forceinline__ void qk_drain(f16v (&s)[NB]) {
+  if constexpr (NB == 2)
+    asm volatile("s_nop 7\n\ts_nop 7" : "+v"(s[0]), "+v"(s[1]));
+  else
+    asm volatile("s_nop 7\n\ts_nop 7" : "+v"(s[0]));
+}
+
 // acc = 0 through the MFMA itself (0 x 0 + 0), so the accumulators are only
 // ever written by AGPR-destination MFMAs.  The leading wait states cover a
 // VALU write of z just before (a reload of the zero operand, for instance),
@@ -628,12 +664,11 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) sc[b][i] = 0.f;
+      mfma_qk_first(sc[b], ka[0], qb[b][0], ql[b][0]);
 #pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st], sc[b], 0, 0, 0);
-        sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], ql[b][st], sc[b], 0, 0, 0);
-      }
+      for (int st = 1; st < 8; ++st) mfma_qk(sc[b], ka[st], qb[b][st], ql[b][st]);
     }
+    qk_drain<NB>(sc);
     if (needs_mask(kb)) mask_tile(sc, kb);
   };
 
@@ -685,12 +720,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       asm volatile("" ::"v"(pp0), "v"(pp1), "v"(ls[b]));
     };
     f16v s_next[NB];
-    auto qk = [&](int st, int b) {
-      s_next[b] =
-          __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st & 3], qb[b][st], s_next[b], 0, 0, 0);
-      s_next[b] =
-          __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st & 3], ql[b][st], s_next[b], 0, 0, 0);
-    };
+    auto qk = [&](int st, int b) { mfma_qk(s_next[b], ka[st & 3], qb[b][st], ql[b][st]); };
     // scores of tile it+1: reference k-step, then k-steps 0-3
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -755,6 +785,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       }
       fence();
     }
+    qk_drain<NB>(s_next);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       l_run[b] = ls[b];
@@ -844,10 +875,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       for (int i = 0; i < 16; ++i) z[i] = 0.f;
       s_out[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kx, qx[b], z, 0, 0, 0);
     };
-    auto QK = [&](int st, int b) {
-      s_out[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], qb[b][st], s_out[b], 0, 0, 0);
-      s_out[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], ql[b][st], s_out[b], 0, 0, 0);
-    };
+    auto QK = [&](int st, int b) { mfma_qk(s_out[b], ka[st], qb[b][st], ql[b][st]); };
     auto PVL = [&](int db, int b) {
       if (with_pv) mfma_pv(o[b][db], vlo[db], p_in[b][0]);
     };
@@ -907,7 +935,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     QK(6, 0); fence(); E(5, 2); fence();
     QK(6, 1); fence(); E(5, 3); fence();
     QK(7, 0); fence(); E(6, 0); fence();
-    QK(7, 1); fence(); E(6, 1); fence();
+    QK(7, 1); fence(); E(6, 1); qk_drain<NB>(s_out); fence();
     // slots 27-34: P.V keys 16-31; V(it+1) goes into V(it-1)'s buffer once
     // every LDS read of the step is done
     PVH(0, 0); fence(); E(6, 2); fence();
