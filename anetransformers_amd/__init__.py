@@ -115,6 +115,7 @@ _SIGS = {
     "mia_peak_read_stream": (c_int, [_P, c_size_t, _P]),
     "mia_peak_read_ring": (c_int, [_P, _P, c_int, c_int, c_int, c_int, _P]),
     "mia_peak_mfma_f16": (c_int, [c_int, POINTER(ctypes.c_double), _P]),
+    "mia_peak_empty": (c_int, [c_int, c_int, _P]),
     # hot path
     "mia_rope_f32": (c_int, [_P, _P, c_int, c_int, _P, c_int, c_int, c_int, _P]),
     "mia_kv_write_f32": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, _P]),

@@ -48,10 +48,10 @@ struct DevCtx {
   size_t split_work_bytes = 0;
   // Opt-in kernel timing: an event pair around the main kernel of each call
   // (kind 0 = decode kernel, 1 = flash kernel, 2 = Q4_0 matvec kernel,
-  // 3 = Q4_0 GEMM kernel).
+  // 3 = Q4_0 GEMM kernel, 4 = the empty kernel of mia_peak_empty).
   bool prof_on = false;
-  std::vector<hipEvent_t> prof_ev[4];
-  size_t prof_n[4] = {0, 0, 0, 0};
+  std::vector<hipEvent_t> prof_ev[5];
+  size_t prof_n[5] = {0, 0, 0, 0, 0};
 };
 
 DevCtx g_ctx[kMaxDevices];
@@ -501,13 +501,13 @@ int mia_init(int device) {
 int mia_profile_begin(void) {
   DevCtx *c;
   if (int rc = current_ctx(&c)) return rc;
-  c->prof_n[0] = c->prof_n[1] = c->prof_n[2] = c->prof_n[3] = 0;
+  for (size_t &n : c->prof_n) n = 0;
   c->prof_on = true;
   return MIA_OK;
 }
 
 int mia_profile_end(int kind, int *count, double *total_ms) {
-  if (kind < 0 || kind > 3 || !count || !total_ms) return set_err(MIA_ERR_INVALID, "bad profile query");
+  if (kind < 0 || kind > 4 || !count || !total_ms) return set_err(MIA_ERR_INVALID, "bad profile query");
   DevCtx *c;
   if (int rc = current_ctx(&c)) return rc;
   c->prof_on = false;
@@ -654,6 +654,17 @@ int mia_peak_mfma_f16(int iters, double *flop, void *stream) {
   if (int rc = current_ctx(&c)) return rc;
   if (iters < 1 || !flop) return set_err(MIA_ERR_INVALID, "peak_mfma_f16: iters >= 1 and flop");
   HIP_TRY(mia::launch_peak_mfma_f16(iters, c->num_cus, flop, pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_peak_empty(int workgroups, int threads, void *stream) {
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  if (workgroups < 1 || threads < 1 || threads > 1024)
+    return set_err(MIA_ERR_INVALID, "peak_empty: need workgroups >= 1 and 1 <= threads <= 1024");
+  hipEvent_t ev0, ev1;
+  if (int rc = prof_pair(c, 4, &ev0, &ev1)) return rc;
+  HIP_TRY(mia::launch_peak_empty(workgroups, threads, pick_stream(c, stream), ev0, ev1));
   return MIA_OK;
 }
 

@@ -111,6 +111,10 @@ hipError_t launch_peak_read_stream(const void *buf, size_t bytes, int num_cus, h
 hipError_t launch_peak_read_ring(const _Float16 *kc, const _Float16 *vc, int n_kv, int max_seq,
                                  int L, int start, int nchunk, hipStream_t s);
 hipError_t launch_peak_mfma_f16(int iters, int num_cus, double *flop, hipStream_t s);
+// An empty kernel of the given grid; ev0/ev1 (may be null) stamped at its
+// start and end like the attention kernels' profile events.
+hipError_t launch_peak_empty(int workgroups, int threads, hipStream_t s, hipEvent_t ev0,
+                             hipEvent_t ev1);
 
 // W4A8 projections (mistral/dequant.h).  x [nblocks*32] fp32, 16-byte aligned
 // -> nblocks Q8_0 blocks of 36 bytes.

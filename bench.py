@@ -250,6 +250,13 @@ def measure_peaks(lib, dec: "Decode", reps: int = 10) -> dict:
     iters = 1024
     mf_ms = timed(lib, lambda: check(lib.mia_peak_mfma_f16(iters, ctypes.byref(flop), None)),
                   reps, 2)
+    # the duration floor of a kernel, measured as the attention kernels' are
+    # (dispatch-stamped events): an empty kernel of each of their grids
+    empty = {}
+    for name, wgs, threads in (("decode_grid_us", N_KV * 32, 512), ("flash_grid_us", N_KV * 32, 256)):
+        kernel_avg_ms(lib, lambda: check(lib.mia_peak_empty(wgs, threads, None)), 3, 4)
+        empty[name] = round(1e3 * kernel_avg_ms(
+            lib, lambda: check(lib.mia_peak_empty(wgs, threads, None)), 20, 4), 2)
     return {
         "hbm_read_stream": {
             "value": round(nb / (st_ms * 1e-3) / 1e9, 1), "unit": "GB/s",
@@ -266,6 +273,11 @@ def measure_peaks(lib, dec: "Decode", reps: int = 10) -> dict:
             "workload": f"{iters} rounds of 4 independent v_mfma_f32_32x32x16_f16 chains, "
                         "2 waves per SIMD on every CU",
             "ms_per_launch": round(mf_ms, 4)},
+        "empty_kernel": dict(empty, workload="a kernel with no body on the decode kernel's grid "
+                             "(256 x 512 threads) and the flash kernel's (256 x 256), timed by "
+                             "the same dispatch-stamped events as the kernel averages (rocprof "
+                             "puts the same empty kernel at ~1.5 us: these events add ~2.5 us to "
+                             "a kernel this short, ~0.3 us to the attention kernels)"),
         "published": {"hbm_gbs": HBM_PEAK_GBS, "mfma_f16_tfs": MFMA_F16_PEAK_TFS},
     }
 
@@ -811,7 +823,9 @@ def main() -> int:
             peaks = measure_peaks(lib, dec)
             log(f"peaks: stream {peaks['hbm_read_stream']['value']} GB/s, decode pattern "
                 f"{peaks['hbm_read_decode_pattern']['value']} GB/s, fp16 MFMA "
-                f"{peaks['mfma_f16']['value']} TFLOP/s")
+                f"{peaks['mfma_f16']['value']} TFLOP/s, empty kernel "
+                f"{peaks['empty_kernel']['decode_grid_us']} / "
+                f"{peaks['empty_kernel']['flash_grid_us']} us")
         dd = DropinDecode(lib, dec)
         di_ms = wall_ms(dd.step, args.steps, args.warmup)
         dropin = {"value": round(N_LAYERS * DECODE_BYTES_PER_LAYER / (di_ms * 1e-3) / 1e9, 2),

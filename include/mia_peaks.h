@@ -36,6 +36,13 @@ int mia_peak_read_ring(const uint16_t *k_layer_dev, const uint16_t *v_layer_dev,
  * (32 x 32 x 16 x 2 per instruction). */
 int mia_peak_mfma_f16(int iters, double *flop, void *stream);
 
+/* One empty kernel of `workgroups` x `threads` (1..1024).  Under
+ * mia_profile_begin its dispatch-stamped duration is recorded as profile
+ * kind 4, measured as the attention kernels' durations are: what a kernel
+ * with no body costs (grid dispatch, the cache maintenance at the kernel
+ * boundaries, the completion signal) by that method. */
+int mia_peak_empty(int workgroups, int threads, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,7 +66,8 @@ int mia_event_elapsed_ms(float *ms, void *start, void *stop);
  * mia_gqa_attention / mia_decode_step / mia_attention_step with S=1; kind 1:
  * the S>1 flash kernel; kind 2: the Q4_0 matvec kernel of mia_q4_0_matvec /
  * mia_q4_0_matvec_qkv; kind 3: the Q4_0 GEMM kernel of mia_q4_0_gemm_f32 /
- * mia_prefill_layer); merge, quantize, RMSNorm and RoPE kernels are not timed.
+ * mia_prefill_layer; kind 4: the empty kernel of mia_peak_empty, mia_peaks.h);
+ * merge, quantize, RMSNorm and RoPE kernels are not timed.
  * mia_profile_end stops recording, synchronises and returns the number of
  * timed launches of that kind and their summed duration. */
 int mia_profile_begin(void);
