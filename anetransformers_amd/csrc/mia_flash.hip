@@ -831,16 +831,20 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   // them.  All K and V^T operands of the step are read from LDS at its start.
   // Scores and P live in two register sets that alternate between steps
   // (s_in -> s_out, p_in -> p_out), so nothing is copied at the step's end.
-  auto step2 = [&](int it, auto with_pv, f16v(&s_in)[NB], f16v(&s_out)[NB], h8(&p_in)[NB][2],
-                   h8(&p_out)[NB][2]) {
+  // with_qk is false for a wave's last tile, whose step has no next tile to
+  // score: its slots then hold only the exponentials and the P.V MFMAs.
+  auto step2 = [&](int it, auto with_pv, auto with_qk, f16v(&s_in)[NB], f16v(&s_out)[NB],
+                   h8(&p_in)[NB][2], h8(&p_out)[NB][2]) {
     const unsigned kab = ka_b[(it + 1) & 1];
     const unsigned vab = va_b[(it + 1) & 1];
     // Operands in halves, each read eight slots (~256 cycles) ahead of its
     // first use: K k-steps 0-3 and V^T keys 0-15 now, k-steps 4-7 in slot 11,
     // V^T keys 16-31 in slot 19 (into the registers the first halves free).
     h8 ka[8], vlo[4], vhi[4];
+    if (with_qk) {
 #pragma unroll
-    for (int st = 0; st < 4; ++st) ka[st] = lds_read_h8(kab ^ (unsigned)(st << 5));
+      for (int st = 0; st < 4; ++st) ka[st] = lds_read_h8(kab ^ (unsigned)(st << 5));
+    }
     if (with_pv) {
       vlo[0] = read_va<0, 0>(vab);
       vlo[1] = read_va<0, 1>(vab);
@@ -870,12 +874,15 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       }
     };
     auto REF = [&](int b) {
+      if (!with_qk) return;
       f16v z;
 #pragma unroll
       for (int i = 0; i < 16; ++i) z[i] = 0.f;
       s_out[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kx, qx[b], z, 0, 0, 0);
     };
-    auto QK = [&](int st, int b) { mfma_qk(s_out[b], ka[st], qb[b][st], ql[b][st]); };
+    auto QK = [&](int st, int b) {
+      if (with_qk) mfma_qk(s_out[b], ka[st], qb[b][st], ql[b][st]);
+    };
     auto PVL = [&](int db, int b) {
       if (with_pv) mfma_pv(o[b][db], vlo[db], p_in[b][0]);
     };
@@ -906,8 +913,10 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       if (with_pv) asm volatile("" ::"v"(x));
     };
     // slots 11-18: P.V of tile it-1, keys 0-15
+    if (with_qk) {
 #pragma unroll
-    for (int st = 4; st < 8; ++st) ka[st] = lds_read_h8(kab ^ (unsigned)(st << 5));
+      for (int st = 4; st < 8; ++st) ka[st] = lds_read_h8(kab ^ (unsigned)(st << 5));
+    }
     PVL(0, 0); fence(); E(2, 2); fence();
     PVL(0, 1); fence(); E(2, 3); fence();
     PVL(1, 0); keep(vlo[0]); fence(); E(3, 0); fence();
@@ -935,7 +944,9 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     QK(6, 0); fence(); E(5, 2); fence();
     QK(6, 1); fence(); E(5, 3); fence();
     QK(7, 0); fence(); E(6, 0); fence();
-    QK(7, 1); fence(); E(6, 1); qk_drain<NB>(s_out); fence();
+    QK(7, 1); fence(); E(6, 1);
+    if (with_qk) qk_drain<NB>(s_out);
+    fence();
     // slots 27-34: P.V keys 16-31; V(it+1) goes into V(it-1)'s buffer once
     // every LDS read of the step is done
     PVH(0, 0); fence(); E(6, 2); fence();
@@ -966,8 +977,10 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       p_out[b][1] = __builtin_bit_cast(h8, pw[b][1]);
     }
     // Window mask of tile it+1, only where it crosses a window edge.
-    const int kbn = kb0 + kStride * (it + 1);
-    if (needs_mask(kbn)) mask_tile(s_out, kbn);
+    if (with_qk) {
+      const int kbn = kb0 + kStride * (it + 1);
+      if (needs_mask(kbn)) mask_tile(s_out, kbn);
+    }
   };
   // O += P.V of the wave's last tile (its V in vt[(g_count-1)&1]) from P.
   // The MFMAs are inline assembly, invisible to the compiler's hazard
@@ -1044,22 +1057,37 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     // issues K(it+2), then V(it+1)).  Step it needs K(it+1) and V(it-1): only
     // V(it), the last load issued, may still be pending.
     if constexpr (NB == 2) {
+      // Step it exponentiates tile it and scores tile it+1; the last step
+      // (it = g_count - 1) scores nothing.
+      using T = std::true_type;
+      using F = std::false_type;
       f16v s_alt[NB];
       h8 p_a[NB][2], p_b[NB][2];
       if (g_count > 0) {
         wait_vmcnt<8>();
-        step2(0, std::false_type{}, s_cur, s_alt, p_a, p_b);  // P(0) -> p_b
+        step2(0, F{}, T{}, s_cur, s_alt, p_a, p_b);  // P(0) -> p_b
       }
       int it = 1;
-      for (; it + 1 < g_count; it += 2) {
+      for (; it + 2 < g_count; it += 2) {
         wait_vmcnt<8>();
-        step2(it, std::true_type{}, s_alt, s_cur, p_b, p_a);
+        step2(it, T{}, T{}, s_alt, s_cur, p_b, p_a);
         wait_vmcnt<8>();
-        step2(it + 1, std::true_type{}, s_cur, s_alt, p_a, p_b);
+        step2(it + 1, T{}, T{}, s_cur, s_alt, p_a, p_b);
       }
-      if (it < g_count) {
+      if (it + 1 < g_count) {  // it = g_count - 2: one more scoring step
         wait_vmcnt<8>();
-        step2(it, std::true_type{}, s_alt, s_cur, p_b, p_a);
+        step2(it, T{}, T{}, s_alt, s_cur, p_b, p_a);
+        ++it;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {  // into the registers the last step reads
+          s_alt[b] = s_cur[b];
+          p_b[b][0] = p_a[b][0];
+          p_b[b][1] = p_a[b][1];
+        }
+      }
+      if (it < g_count) {  // it = g_count - 1: the last step
+        wait_vmcnt<8>();
+        step2(it, T{}, F{}, s_alt, s_cur, p_b, p_a);
 #pragma unroll
         for (int b = 0; b < NB; ++b) {  // P of the last tile where last_pv_of reads it
           p_b[b][0] = p_a[b][0];
