@@ -87,10 +87,8 @@ struct Lay {
   static constexpr int kBufBytes = kWaves * 4 * kTileHalfs * 2;  // [wave][K0 K1 V0 V1]
   static constexpr int kQBytes = kRows * HD * 2;               // fp16 Q rows
   static constexpr int kMLBytes = kWaves * kRows * 8;          // (max, sum) per wave, row
-  // After the loop the tile buffers hold the foreign partial outputs:
-  // [NB*4 (block, dim block)][3 source waves][4 chunks][64 lanes][4 floats].
-  static constexpr int kMergeBytes = NB * 4 * 3 * 4 * 64 * 16;
-  static_assert(kMergeBytes <= kBufBytes, "merge area must fit the tile buffers");
+  // After its loop a wave's own tile buffers hold its partial output:
+  // [NB (block)][4 (dim block)][4 chunks][64 lanes][4 floats].
   // Prologue only: (cos, sin) rows of the wave's queries, 2 NB rows of 512 B.
   static constexpr int kCSBytes = kWaves * 2 * NB * 512;
   static constexpr int kBytes = kBufBytes + kQBytes + kMLBytes + kCSBytes;
@@ -1131,8 +1129,14 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
 #undef MIA_LOAD_V_NEXT
 
   // ---- merge of the four key groups ----
+  // Each wave leaves its (max, sum) per row and its unscaled partial output
+  // in its own tile buffers, which are free once its loop is done (its loads
+  // have landed; its reads of them come first in its LDS order): a wave that
+  // finishes early writes without waiting for the others.  After one
+  // barrier, wave w finalises dim block w of every row block from the four
+  // partials, weighted by e_k = 2^(m_k - M): its own from its registers, the
+  // other three from LDS, lane-linear (conflict-free).
   pv_drain<NB>(o);
-  // (max, sum) of every row per wave; the sum covers both key halves.
   lds_float *ml = (lds_float *)(smem + L::kBufBytes + L::kQBytes);  // [wave][RT][2]
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
@@ -1141,9 +1145,25 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     const float mr = !has_keys[b] ? -INFINITY : (m_ref[b] == -INFINITY ? 0.f : m_ref[b]);
     if (half == 0) *(lds_f2 *)(ml + (w * RT + 32 * b + col) * 2) = (f2){mr, l_run[b]};
   }
-  __syncthreads();  // every wave is past its loop: tile buffers are free
+  // wave src's partial of (row block b, dim block db), chunk q of this lane
+  constexpr int kWaveBufBytes = L::kBufBytes / kWaves;
+  static_assert(NB * 4 * 4 * 64 * 16 <= kWaveBufBytes, "a wave's partial must fit its tile buffers");
+  auto mg_at = [&](int src, int b, int db, int q) {
+    return (lds_float *)(smem + src * kWaveBufBytes) + (((b * 4 + db) * 4 + q) * 64 + lane) * 4;
+  };
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      if (db == w) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *(lds_f4 *)mg_at(w, b, db, q) =
+            (f4){o[b][db][4 * q], o[b][db][4 * q + 1], o[b][db][4 * q + 2], o[b][db][4 * q + 3]};
+    }
+  __syncthreads();
 
-  float Mx[NB], Lsum[NB];
+  const size_t tile_id = (size_t)kvh * p.n_rtiles + rtile;
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     f2 mlw[kWaves];
@@ -1153,41 +1173,12 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       mlw[k] = *(lds_f2 *)(ml + (k * RT + 32 * b + col) * 2);
       M = fmaxf(M, mlw[k].x);
     }
-    float Ls = 0.f, e_own = 0.f;
+    float e[kWaves], Ls = 0.f;
 #pragma unroll
     for (int k = 0; k < kWaves; ++k) {
-      const float e = mlw[k].x == -INFINITY ? 0.f : fast_exp2(mlw[k].x - M);
-      Ls = __builtin_fmaf(e, mlw[k].y, Ls);
-      if (k == w) e_own = e;
+      e[k] = mlw[k].x == -INFINITY ? 0.f : fast_exp2(mlw[k].x - M);
+      Ls = __builtin_fmaf(e[k], mlw[k].y, Ls);
     }
-    Mx[b] = M;
-    Lsum[b] = Ls;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[b][db][i] *= e_own;
-  }
-
-  // Wave w finalises dim block db = w of every row block; the other three
-  // dim blocks go to their owners through LDS, lane-linear (conflict-free).
-  lds_float *mg = (lds_float *)smem;
-  auto mg_at = [&](int c, int slot, int q) { return mg + ((((c * 3 + slot) * 4 + q) * 64 + lane) * 4); };
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      if (db == w) continue;
-      const int slot = w < db ? w : w - 1;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *(lds_f4 *)mg_at(b * 4 + db, slot, q) =
-            (f4){o[b][db][4 * q], o[b][db][4 * q + 1], o[b][db][4 * q + 2], o[b][db][4 * q + 3]};
-    }
-  __syncthreads();
-
-  const size_t tile_id = (size_t)kvh * p.n_rtiles + rtile;
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
     const int rl = 32 * b + col;
     const int row = row0 + rl;
     const int t = row >> 2, g = row & 3;
@@ -1197,14 +1188,16 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       f4 acc[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        acc[q] = (f4){o[b][db][4 * q], o[b][db][4 * q + 1], o[b][db][4 * q + 2], o[b][db][4 * q + 3]};
+        acc[q] = (f4){o[b][db][4 * q], o[b][db][4 * q + 1], o[b][db][4 * q + 2], o[b][db][4 * q + 3]} *
+                 e[db];
 #pragma unroll
-        for (int slot = 0; slot < 3; ++slot) acc[q] += *(lds_f4 *)mg_at(b * 4 + db, slot, q);
+        for (int k = 0; k < kWaves; ++k)
+          if (k != db) acc[q] += *(lds_f4 *)mg_at(k, b, db, q) * e[k];
       }
       if (t < p.S) {
         // dims 32*db + 8*q + 4*half .. +4 (the accumulator's dim order)
         if (p.nsplit == 1) {
-          const float inv = 1.0f / Lsum[b];
+          const float inv = 1.0f / Ls;
           float *dst = p.out + (size_t)t * dim_model + (size_t)(kvh * 4 + g) * HD + 32 * db + 4 * half;
 #pragma unroll
           for (int q = 0; q < 4; ++q) *reinterpret_cast<f4 *>(dst + 8 * q) = acc[q] * inv;
@@ -1214,7 +1207,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) *reinterpret_cast<f4 *>(dst + 8 * q) = acc[q];
           if (db == 0 && half == 0)
-            *reinterpret_cast<float2 *>(p.part_ml + pidx * 2) = make_float2(Mx[b], Lsum[b]);
+            *reinterpret_cast<float2 *>(p.part_ml + pidx * 2) = make_float2(M, Ls);
         }
       }
     }
