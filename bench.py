@@ -38,6 +38,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import hashlib
 import json
 import os
 import sys
@@ -767,12 +768,23 @@ def cpu_other_configs():
 
 
 def load_traffic(name: str):
-    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/), or None."""
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/), or None.
+
+    Each entry carries the SHA-256 of the kernel source it was measured on;
+    once that source has changed the figure no longer describes the kernel
+    that runs, and None is reported instead of a stale number."""
     path = os.path.join(REPO, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get(name)
-    except (OSError, ValueError):
+            entry = json.load(f).get(name)
+        src = os.path.join(REPO, entry["kernel_source"])
+        with open(src, "rb") as f:
+            if hashlib.sha256(f.read()).hexdigest() != entry["kernel_source_sha256"]:
+                log(f"roofline.traffic for {name}: {entry['kernel_source']} changed since its "
+                    "counters were measured; reported as null")
+                return None
+        return int(entry["bytes"])
+    except (OSError, ValueError, KeyError, TypeError):
         return None
 
 
