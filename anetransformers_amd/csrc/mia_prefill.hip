@@ -295,6 +295,253 @@ __global__ __launch_bounds__(kGThreads, PF == 3 ? 1 : 2) void q4_gemm_kernel(Gem
   }
 }
 
+// ---- wide-tile GEMM ----
+// Workgroup: 256 threads, 64 tokens x 256 weight rows; wave w owns weight rows
+// 64w .. 64w+63 (two 32-row MFMA tiles) against all 64 tokens (two 32-token
+// tiles), 32 MFMAs per 64-K iteration.  Everything is staged into LDS by
+// direct loads (global_load_lds), kWStages iterations deep, with one
+// barrier per iteration:
+//   - the activations' hi and lo planes, 64 tokens x 64 K each, shared by the
+//     four waves, 16-byte chunk c of token row r at chunk c ^ (r & 7) (the
+//     32 rows an operand read touches then spread over every bank);
+//   - each wave's own 64 weight rows, 36 bytes (two Q4_0 blocks) each, read
+//     back by the wave alone: the B operands are formed from the nibbles in
+//     registers (no dequantised tile written to LDS, no row done twice).
+// Per 32-value block the MFMA partial products are scaled by the block's
+// fp16 scale in fp32 (acc += d * (X . q)), as in q4_gemm_kernel, in the same
+// order: the two kernels' results are identical.
+constexpr int kWN = 256;                          // weight rows per workgroup
+constexpr int kWStages = 3;                       // iterations staged ahead
+constexpr int kWPlane = 64 * kBK * 2;             // one activation plane: 8 KB
+constexpr int kWBRows = 64 * 36;                  // one wave's weight rows: 2304 B
+constexpr int kWStage = 2 * kWPlane + 4 * kWBRows;  // 25,600 B
+
+// 16 (dwordx4) or 4 (dword) bytes per lane from global memory into LDS at
+// byte M0 + lane * size; completion is awaited with vmcnt (the compiler does
+// not track these loads).
+__device__ __forceinline__ void lds_dma16(const void *g, unsigned m) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(m)
+      : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void *g, unsigned m) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(m)
+      : "memory");
+}
+template <int N>
+__device__ __forceinline__ void gemm_wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kGThreads, 2) void q4_gemm_wide_kernel(GemmParams p) {
+#pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5;
+  const int n0 = blockIdx.x * kWN, m0 = blockIdx.y * 64;
+  const int n_all = p.K / kBK;
+  const int it0 = (int)((long)n_all * blockIdx.z / p.ksplit);
+  const int n_it = (int)((long)n_all * (blockIdx.z + 1) / p.ksplit) - it0;
+  const int last = it0 + n_it - 1;
+  const unsigned sbase = __builtin_amdgcn_readfirstlane((unsigned)(__UINTPTR_TYPE__)smem);
+
+  // Activation loads: wave w fills plane w >> 1, token rows 32 (w & 1) .. +32,
+  // four instructions of 8 rows; lane i of instruction j: row
+  // r = 32 (w & 1) + 8 j + i / 8, LDS chunk i % 8 = logical chunk (i % 8) ^ (r & 7).
+  const _Float16 *asrc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 32 * (w & 1) + 8 * j + (lane >> 3);
+    const int c = (lane & 7) ^ (r & 7);
+    asrc[j] = ((w >> 1) ? p.alo : p.ahi) + (size_t)min(m0 + r, p.S - 1) * p.K + 8 * c;
+  }
+  const unsigned a_lds = (unsigned)((w >> 1) * kWPlane + 32 * (w & 1) * (kBK * 2));
+  // Weight loads: the wave's 64 rows x 9 dwords, nine instructions of 64
+  // dwords; lane i of instruction j: dword q = 64 j + i, row q / 9, dword q % 9.
+  const uint8_t *bsrc[9];
+#pragma unroll
+  for (int j = 0; j < 9; ++j) {
+    const int q = 64 * j + lane;
+    const int g = min(n0 + 64 * w + q / 9, p.N - 1);
+    const uint8_t *base = g < p.rows0 ? p.w0 : (g < p.rows01 ? p.w1 : p.w2);
+    const int lr = g < p.rows0 ? g : (g < p.rows01 ? g - p.rows0 : g - p.rows01);
+    bsrc[j] = base + (size_t)lr * (size_t)(p.K / 32) * 18 + 4 * (q % 9);
+  }
+  const unsigned b_lds = (unsigned)(2 * kWPlane + w * kWBRows);
+  // Iteration `it` (absolute) into stage `st`: 4 + 9 loads per wave.
+  auto issue = [&](int st, int it) {
+    const unsigned sb = sbase + (unsigned)(st * kWStage);
+    // (wave-uniform offsets: one scalar multiply, then a 64-bit add per lane)
+    const unsigned aoff = __builtin_amdgcn_readfirstlane((unsigned)it * (unsigned)(kBK * 2));
+    const unsigned boff = __builtin_amdgcn_readfirstlane((unsigned)it * 36u);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      lds_dma16((const char *)asrc[j] + aoff, sb + a_lds + 1024u * j);
+#pragma unroll
+    for (int j = 0; j < 9; ++j) lds_dma4(bsrc[j] + boff, sb + b_lds + 256u * j);
+  };
+  constexpr int kLoadsPerStage = 13;
+
+  f16v acc[2][2];
+#pragma unroll
+  for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[tm][tn][i] = 0.0f;
+
+  typedef __attribute__((address_space(3))) h8 lds_h8;
+  typedef __attribute__((address_space(3))) unsigned lds_u32;
+  unsigned nib_mask = 0x000F000Fu;  // in a VGPR
+  asm volatile("" : "+v"(nib_mask));
+  const unsigned nib_exp = __builtin_amdgcn_readfirstlane(0x64006400u);
+  auto compute = [&](int st) {
+    const unsigned sb = sbase + (unsigned)(st * kWStage);
+    // this lane's weight rows (tn): dwords 2h .. 2h+2 (block 0's nibbles
+    // 8h .. 8h+7 at byte offset 2), dword 0 (scale 0, low half), dword 4
+    // (scale 1, high half), dwords 5+2h, 6+2h (block 1's nibbles 8h .. 8h+7)
+    unsigned nb[2][2][2];  // [tn][block][dword]: 8 nibble bytes
+    float dsc[2][2];       // [tn][block]
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) {
+      const unsigned rb = sb + b_lds + (unsigned)((32 * tn + col) * 36);
+      const lds_u32 *r = (const lds_u32 *)(__UINTPTR_TYPE__)rb;
+      const unsigned x0 = r[2 * half], x1 = r[2 * half + 1], x2 = r[2 * half + 2];
+      const unsigned s0 = r[0], s1 = r[4];
+      nb[tn][0][0] = __builtin_amdgcn_alignbyte(x1, x0, 2);
+      nb[tn][0][1] = __builtin_amdgcn_alignbyte(x2, x1, 2);
+      nb[tn][1][0] = r[5 + 2 * half];
+      nb[tn][1][1] = r[6 + 2 * half];
+      dsc[tn][0] = f16_bits_f32(s0);
+      dsc[tn][1] = f16_bits_f32(s1 >> 16);
+      // converted once here: folded into each FMA, the conversion makes
+      // every scale FMA a mixed-precision one
+      asm volatile("" : "+v"(dsc[tn][0]), "+v"(dsc[tn][1]));
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      // B operands of the block's two k-steps: values 16 ks + 8h .. +8 are
+      // the low (ks 0) or high (ks 1) nibbles of the lane's 8 bytes.  A pair
+      // of consecutive bytes goes to the two halves of a dword with one byte
+      // permute, and one AND-OR leaves their nibbles under the fp16 exponent
+      // of 1024 (0x6400 | n = 1024 + n); subtracting 1032 gives n - 8.
+      h8 bop[2][2];  // [ks][tn]
+#pragma unroll
+      for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const unsigned x0 = ks ? nb[tn][kb][0] >> 4 : nb[tn][kb][0];
+          const unsigned x1 = ks ? nb[tn][kb][1] >> 4 : nb[tn][kb][1];
+          unsigned v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            // bytes 2q, 2q+1 of x1:x0 into bytes 0 and 2 (perm selectors 0-3
+            // pick x0's bytes, 4-7 x1's)
+            const unsigned sel = (unsigned)(2 * q) | ((unsigned)(2 * q + 1) << 16);
+            const unsigned t = __builtin_amdgcn_perm(x1, x0, sel);
+            // (t & mask) | exponent in one instruction (the compiler keeps
+            // both constants as literals, which a VOP3 cannot take; one
+            // scalar operand at most)
+            unsigned e;
+            asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(e) : "v"(t), "v"(nib_mask), "s"(nib_exp));
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            v[q] = __builtin_bit_cast(
+                unsigned, __builtin_bit_cast(h2, e) - (h2){(_Float16)1032.0f, (_Float16)1032.0f});
+          }
+          bop[ks][tn] = __builtin_bit_cast(h8, (u4){v[0], v[1], v[2], v[3]});
+        }
+      f16v blk[2][2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int c = 2 * (2 * kb + ks) + half;  // logical 16-byte chunk
+        h8 ah[2], al[2];
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm) {
+          const int r = 32 * tm + col;
+          const unsigned off = (unsigned)(r * (kBK * 2) + 16 * (c ^ (r & 7)));
+          ah[tm] = *(const lds_h8 *)(__UINTPTR_TYPE__)(sb + off);
+          al[tm] = *(const lds_h8 *)(__UINTPTR_TYPE__)(sb + kWPlane + off);
+        }
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+          for (int tn = 0; tn < 2; ++tn) {
+            if (ks == 0) {
+#pragma unroll
+              for (int i = 0; i < 16; ++i) blk[tm][tn][i] = 0.0f;
+            }
+            blk[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[tm], bop[ks][tn], blk[tm][tn], 0, 0, 0);
+            blk[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[tm], bop[ks][tn], blk[tm][tn], 0, 0, 0);
+          }
+      }
+#pragma unroll
+      for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            acc[tm][tn][i] = __builtin_fmaf(dsc[tn][kb], blk[tm][tn][i], acc[tm][tn][i]);
+    }
+  };
+
+  // Stage s holds iteration it0 + s (mod kWStages).  Loads past the range
+  // repeat its last iteration (in bounds, into a stage nobody reads), so
+  // every iteration issues the same number of loads and the waits are exact.
+  issue(0, it0);
+  issue(1, min(it0 + 1, last));
+  auto step = [&](int it, int st) {
+    gemm_wait_vmcnt<kLoadsPerStage>();  // this wave's loads of stage st are in
+    __syncthreads();                    // everyone's are; stage (it - 1) is read
+    issue((st + 2) % kWStages, min(it0 + it + 2, last));
+    compute(st);
+  };
+  int it = 0;
+  for (; it + kWStages <= n_it; it += kWStages) {
+    step(it, 0);
+    step(it + 1, 1);
+    step(it + 2, 2);
+  }
+  if (it < n_it) step(it, 0);
+  if (it + 1 < n_it) step(it + 1, 1);
+  gemm_wait_vmcnt<0>();  // (the repeated loads past the range)
+
+  // D layout: lane holds column n = col; value i is row 8*(i/4) + 4*half + i%4.
+#pragma unroll
+  for (int tn = 0; tn < 2; ++tn) {
+    const int n = n0 + 64 * w + 32 * tn + col;
+    if (n >= p.N) continue;
+#pragma unroll
+    for (int tm = 0; tm < 2; ++tm) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int m = m0 + 32 * tm + 8 * (i >> 2) + 4 * half + (i & 3);
+        if (m >= p.S) continue;
+        if (p.ksplit > 1)
+          p.part[((size_t)blockIdx.z * p.S + m) * p.N + n] = acc[tm][tn][i];
+        else
+          gemm_epilogue<MODE>(p, m, n, acc[tm][tn][i]);
+      }
+    }
+  }
+}
+
 // Sum of the split partial products in split order, then the epilogue.
 template <int MODE>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
@@ -400,28 +647,47 @@ hipError_t launch_gemm_variant(const GemmParams &p, hipStream_t s, hipEvent_t ev
 // 286 us, QKV 6144 x 4096 106 / 92 / 137, Wo 4096 x 4096 88 / - / 72,
 // W2 4096 x 14336 312 / - / 242.
 template <int MODE>
+hipError_t set_wide_lds_limit() {
+  return hipFuncSetAttribute((const void *)q4_gemm_wide_kernel<MODE>,
+                             hipFuncAttributeMaxDynamicSharedMemorySize, kWStages * kWStage);
+}
+
+template <int MODE>
 hipError_t launch_gemm_mode(const GemmParams &p, int num_cus, hipStream_t s, hipEvent_t ev0,
                             hipEvent_t ev1) {
-  if (p.ksplit > 1 || gemm_tiles(p.N, p.S) > num_cus)
-    return launch_gemm_variant<MODE, 64, 2>(p, s, ev0, ev1);
-  return launch_gemm_variant<MODE, 64, 3>(p, s, ev0, ev1);
+  (void)num_cus;
+  const dim3 grid((p.N + kWN - 1) / kWN, (p.S + 63) / 64, p.ksplit);
+  hipExtLaunchKernelGGL((q4_gemm_wide_kernel<MODE>), grid, dim3(kGThreads), kWStages * kWStage,
+                        s, ev0, ev1, 0, p);
+  if (p.ksplit > 1) {
+    const size_t total = (size_t)p.S * p.N;
+    const unsigned blocks = (unsigned)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+    hipLaunchKernelGGL(gemm_reduce_kernel<MODE>, dim3(blocks), dim3(256), 0, s, p);
+  }
+  return hipGetLastError();
 }
 
 }  // namespace
 
-long gemm_tiles(int N, int S) { return (long)((N + kBN - 1) / kBN) * ((S + 63) / 64); }
+long gemm_tiles(int N, int S) { return (long)((N + kWN - 1) / kWN) * ((S + 63) / 64); }
 
 int gemm_pick_ksplit(int N, int K, int S, int num_cus) {
-  // Grids of at most one workgroup per CU with a long K: two K halves give
-  // two workgroups per CU (the narrow Wo and W2 shapes of a prefill chunk).
-  return gemm_tiles(N, S) <= num_cus && K / kBK >= 16 ? 2 : 1;
+  // Two workgroups fit a CU.  A grid smaller than the CU count splits K
+  // (in two or four, keeping at least 8 iterations per split) toward two
+  // workgroups per CU; the partial products are summed in split order.
+  const long tiles = gemm_tiles(N, S);
+  int ks = 1;
+  while (ks < 4 && tiles * ks * 2 <= 2L * num_cus && K / kBK / (ks * 2) >= 8) ks *= 2;
+  return ks;
 }
 
 hipError_t prepare_gemm() {
   const hipError_t e[] = {
       set_lds_limit<kGemmStore, 64, 2>(),   set_lds_limit<kGemmStore, 64, 3>(),
       set_lds_limit<kGemmAdd, 64, 2>(),     set_lds_limit<kGemmAdd, 64, 3>(),
-      set_lds_limit<kGemmSiluMul, 64, 2>(), set_lds_limit<kGemmSiluMul, 64, 3>()};
+      set_lds_limit<kGemmSiluMul, 64, 2>(), set_lds_limit<kGemmSiluMul, 64, 3>(),
+      set_wide_lds_limit<kGemmStore>(),     set_wide_lds_limit<kGemmAdd>(),
+      set_wide_lds_limit<kGemmSiluMul>()};
   for (hipError_t x : e)
     if (x != hipSuccess) return x;
   return hipSuccess;
