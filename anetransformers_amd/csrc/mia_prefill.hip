@@ -6,18 +6,16 @@
 //
 // GEMM: Y[S][N] = X[S][K] . W[N][K]^T on fp16 MFMA (v_mfma_f32_32x32x16_f16)
 // with fp32 accuracy where it matters:
-//   - X is split into fp16 hi + lo (x = hi + lo to ~2^-22) as it is staged
-//     into LDS, and both halves go through the MFMA;
+//   - X comes as fp16 hi + lo planes (x = hi + lo to ~2^-22, split by its
+//     producer), and both halves go through the MFMA;
 //   - W's 4-bit values q - 8 are exact in fp16; the fp16 block scale d is
 //     applied in fp32 once per 32-value block: acc += d * (X . q) for the
 //     block's partial product, which is what dequantising to fp32 computes.
-// Workgroup: 256 threads, 64 tokens x 128 weight rows, 4 waves of 32 x 64
-// (the kernel also builds for 128-token tiles); each iteration stages 64
-// K values (two Q4_0 blocks, 36 bytes of each row, 4-byte aligned because the
-// blocks per row are even) into one of two LDS stages, with the global loads
-// issued two iterations ahead of their store.
+// Workgroup: 256 threads, 64 tokens x 256 weight rows, 4 waves of 64 x 64;
+// each iteration covers 64 K values (two Q4_0 blocks, 36 bytes of each row,
+// 4-byte aligned because the blocks per row are even), staged three
+// iterations ahead by direct-to-LDS loads (q4_gemm_wide_kernel below).
 #include <algorithm>
-#include <type_traits>
 
 #include "mia_device.h"
 #include "mia_kernels.h"
@@ -26,18 +24,7 @@ namespace mia {
 namespace {
 
 constexpr int kGThreads = 256;
-constexpr int kBN = 128;          // weight rows per workgroup
 constexpr int kBK = 64;           // K values per iteration (two Q4_0 blocks)
-constexpr int kKP = kBK + 8;      // LDS row stride in halves (144 B: conflict-free b128 reads)
-
-// One LDS stage for BM tokens; the kernel keeps two.
-template <int BM>
-struct GemmLds {
-  _Float16 ahi[BM][kKP];
-  _Float16 alo[BM][kKP];
-  _Float16 bq[kBN][kKP];
-  float bd[kBN][2];
-};
 
 __device__ __forceinline__ float f16_bits_f32(unsigned h) {
   return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xFFFFu));
@@ -82,220 +69,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams &p, int m, int n,
   }
 }
 
-// BM = 128 or 64 tokens per workgroup; waves 2 x 2, each BM/2 tokens x 64
-// weight rows (TM x 2 MFMA tiles of 32 x 32).
-// PF: register slots of staged loads, loaded PF - 1 iterations before they
-// are stored.  PF = 2 fits 256 VGPRs (two workgroups per CU); PF = 3 takes
-// about 400 (one workgroup per CU, for grids that have no more workgroups
-// than CUs anyway).
-template <int MODE, int BM, int PF>
-__global__ __launch_bounds__(kGThreads, PF == 3 ? 1 : 2) void q4_gemm_kernel(GemmParams p) {
-#pragma clang fp contract(off)
-  static_assert(PF == 2 || PF == 3, "two or three register slots");
-  constexpr int TM = BM / 64;           // MFMA tiles per wave along the tokens
-  constexpr int ATPR = kGThreads / BM;  // threads per staged token row
-  constexpr int AF4 = kBK / ATPR / 4;   // float4 loads per thread and iteration
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  GemmLds<BM> *const sm = reinterpret_cast<GemmLds<BM> *>(smem);
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * BM;
-
-  // A staging: thread -> token row ar, 4 * AF4 values at column ac of the
-  // hi and lo planes
-  const int ar = tid / ATPR, ac = (tid % ATPR) * 4 * AF4;
-  const size_t aoff = (size_t)min(m0 + ar, p.S - 1) * p.K + ac;
-  const _Float16 *const ahp = p.ahi + aoff, *const alp = p.alo + aoff;
-  // B staging: thread -> weight row br, block bb (0, 1) of the iteration's pair
-  const int br = tid & (kBN - 1), bb = tid / kBN;
-  const uint8_t *bptr;
-  {
-    const int g = min(n0 + br, p.N - 1);
-    const uint8_t *base = g < p.rows0 ? p.w0 : (g < p.rows01 ? p.w1 : p.w2);
-    const int lr = g < p.rows0 ? g : (g < p.rows01 ? g - p.rows0 : g - p.rows01);
-    bptr = base + (size_t)lr * (size_t)(p.K / 32) * 18 + 16 * bb;
-  }
-
-  // Iteration j's rows live in register slot j % PF from their load to their
-  // LDS store.
-  constexpr int kSlots = PF;
-  static_assert(AF4 % 2 == 0, "whole 8-value pieces of A per thread");
-  u4 ahi_s[kSlots][AF4 / 2], alo_s[kSlots][AF4 / 2];
-  unsigned breg_s[kSlots][5];
-  auto load = [&](auto slot, int it) {
-    constexpr int SL = decltype(slot)::value;
-#pragma unroll
-    for (int j = 0; j < AF4 / 2; ++j) {
-      ahi_s[SL][j] = *reinterpret_cast<const u4 *>(ahp + (size_t)it * kBK + 8 * j);
-      alo_s[SL][j] = *reinterpret_cast<const u4 *>(alp + (size_t)it * kBK + 8 * j);
-    }
-    const uint8_t *b = bptr + (size_t)it * 36;
-#pragma unroll
-    for (int j = 0; j < 5; ++j) breg_s[SL][j] = *reinterpret_cast<const unsigned *>(b + 4 * j);
-  };
-  auto store = [&](auto slot, GemmLds<BM> &st) {
-    constexpr int SL = decltype(slot)::value;
-    const unsigned *breg = breg_s[SL];
-#pragma unroll
-    for (int j = 0; j < AF4 / 2; ++j) {
-      *reinterpret_cast<u4 *>(&st.ahi[ar][ac + 8 * j]) = ahi_s[SL][j];
-      *reinterpret_cast<u4 *>(&st.alo[ar][ac + 8 * j]) = alo_s[SL][j];
-    }
-    // bb 0: bytes 0-19 of the pair (scale 0-1, nibbles 2-17);
-    // bb 1: bytes 16-35 (scale 18-19, nibbles 20-35)
-    unsigned q[4];
-    float d;
-    if (bb == 0) {
-      d = f16_bits_f32(breg[0]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) q[i] = __builtin_amdgcn_alignbyte(breg[i + 1], breg[i], 2);
-    } else {
-      d = f16_bits_f32(breg[0] >> 16);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) q[i] = breg[i + 1];
-    }
-    // byte j: low nibble = value j, high nibble = value j + 16
-    unsigned lo8[8], hi8[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const unsigned v = q[i], h = q[i] >> 4;
-      lo8[2 * i] = nib2_to_h2((v & 0xFu) | ((v << 8) & 0xF0000u));
-      lo8[2 * i + 1] = nib2_to_h2(((v >> 16) & 0xFu) | ((v >> 8) & 0xF0000u));
-      hi8[2 * i] = nib2_to_h2((h & 0xFu) | ((h << 8) & 0xF0000u));
-      hi8[2 * i + 1] = nib2_to_h2(((h >> 16) & 0xFu) | ((h >> 8) & 0xF0000u));
-    }
-    _Float16 *dst = &st.bq[br][32 * bb];
-    *reinterpret_cast<u4 *>(dst) = (u4){lo8[0], lo8[1], lo8[2], lo8[3]};
-    *reinterpret_cast<u4 *>(dst + 8) = (u4){lo8[4], lo8[5], lo8[6], lo8[7]};
-    *reinterpret_cast<u4 *>(dst + 16) = (u4){hi8[0], hi8[1], hi8[2], hi8[3]};
-    *reinterpret_cast<u4 *>(dst + 24) = (u4){hi8[4], hi8[5], hi8[6], hi8[7]};
-    st.bd[br][bb] = d;
-  };
-
-  f16v acc[TM][2];
-#pragma unroll
-  for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-    for (int tn = 0; tn < 2; ++tn)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[tm][tn][i] = 0.0f;
-
-  const int col = lane & 31, half = lane >> 5;
-  auto compute = [&](const GemmLds<BM> &st) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      f16v blk[TM][2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int k = 32 * kb + 16 * ks + 8 * half;
-        h8 b[2], ah[TM], al[TM];
-#pragma unroll
-        for (int tn = 0; tn < 2; ++tn)
-          b[tn] = *reinterpret_cast<const h8 *>(&st.bq[64 * wn + 32 * tn + col][k]);
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm) {
-          ah[tm] = *reinterpret_cast<const h8 *>(&st.ahi[(BM / 2) * wm + 32 * tm + col][k]);
-          al[tm] = *reinterpret_cast<const h8 *>(&st.alo[(BM / 2) * wm + 32 * tm + col][k]);
-        }
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-          for (int tn = 0; tn < 2; ++tn) {
-            if (ks == 0) {
-#pragma unroll
-              for (int i = 0; i < 16; ++i) blk[tm][tn][i] = 0.0f;
-            }
-            blk[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[tm], b[tn], blk[tm][tn], 0, 0, 0);
-            blk[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[tm], b[tn], blk[tm][tn], 0, 0, 0);
-          }
-      }
-#pragma unroll
-      for (int tn = 0; tn < 2; ++tn) {
-        const float d = st.bd[64 * wn + 32 * tn + col][kb];
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            acc[tm][tn][i] = __builtin_fmaf(d, blk[tm][tn][i], acc[tm][tn][i]);
-      }
-    }
-  };
-
-  // Two LDS stages: iteration it computes from stage it & 1 and stores the
-  // next iteration's rows into the other stage; one barrier per iteration
-  // orders the stores and reads against the other waves.
-  using S0 = std::integral_constant<int, 0>;
-  // K range of this workgroup: all of it, or split blockIdx.z of p.ksplit
-  // (the partial products then go to p.part and gemm_reduce_kernel sums them)
-  const int n_all = p.K / kBK;
-  const int it0 = (int)((long)n_all * blockIdx.z / p.ksplit);
-  const int n_it = (int)((long)n_all * (blockIdx.z + 1) / p.ksplit) - it0;
-  const int last = it0 + n_it - 1;
-  // Loads past the end repeat the last iteration (in bounds, stored into a
-  // stage nobody reads).  Unrolled by the slot count so that the slots are
-  // registers and the waits exact; the scheduling fence after each step
-  // keeps the steps from being interleaved (which would need more VGPRs
-  // than two workgroups per CU leave).
-  using S1 = std::integral_constant<int, 1>;
-  using S2 = std::integral_constant<int, PF == 3 ? 2 : 0>;
-  load(S0{}, it0);
-  load(S1{}, min(it0 + 1, last));
-  if constexpr (PF == 3) load(S2{}, min(it0 + 2, last));
-  store(S0{}, sm[0]);
-  __syncthreads();
-  // it counts from 0 within the range (stage parity and slot), it0 + it is
-  // the absolute iteration
-  // With two slots the loads of it + 2 go out first: their slot was stored
-  // in the step before, and the store of it + 1 then waits only for loads a
-  // whole step older.  Three slots keep the loads after the store (issued
-  // first they would hold a fourth slot's registers through the compute).
-  auto step = [&](auto slot, auto next, int it) {
-    if constexpr (PF == 2) load(slot, min(it0 + it + kSlots, last));
-    compute(sm[it & 1]);
-    store(next, sm[(it + 1) & 1]);
-    if constexpr (PF == 3) load(slot, min(it0 + it + kSlots, last));
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  int it = 0;
-  if constexpr (PF == 3) {
-    for (; it + kSlots <= n_it; it += kSlots) {
-      step(S0{}, S1{}, it);
-      step(S1{}, S2{}, it + 1);
-      step(S2{}, S0{}, it + 2);
-    }
-    if (it < n_it) step(S0{}, S1{}, it);
-    if (it + 1 < n_it) step(S1{}, S2{}, it + 1);
-  } else {
-    for (; it + kSlots <= n_it; it += kSlots) {
-      step(S0{}, S1{}, it);
-      step(S1{}, S0{}, it + 1);
-    }
-    if (it < n_it) step(S0{}, S1{}, it);
-  }
-
-  // D layout: lane holds column n = col; value i is row 8*(i/4) + 4*half + i%4.
-#pragma unroll
-  for (int tn = 0; tn < 2; ++tn) {
-    const int n = n0 + 64 * wn + 32 * tn + col;
-    if (n >= p.N) continue;
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int m = m0 + (BM / 2) * wm + 32 * tm + 8 * (i >> 2) + 4 * half + (i & 3);
-        if (m >= p.S) continue;
-        if (p.ksplit > 1)
-          p.part[((size_t)blockIdx.z * p.S + m) * p.N + n] = acc[tm][tn][i];
-        else
-          gemm_epilogue<MODE>(p, m, n, acc[tm][tn][i]);
-      }
-    }
-  }
-}
-
-// ---- wide-tile GEMM ----
+// ---- the Q4_0 GEMM ----
 // Workgroup: 256 threads, 64 tokens x 256 weight rows; wave w owns weight rows
 // 64w .. 64w+63 (two 32-row MFMA tiles) against all 64 tokens (two 32-token
 // tiles), 32 MFMAs per 64-K iteration.  Everything is staged into LDS by
@@ -307,9 +81,9 @@ __global__ __launch_bounds__(kGThreads, PF == 3 ? 1 : 2) void q4_gemm_kernel(Gem
 //   - each wave's own 64 weight rows, 36 bytes (two Q4_0 blocks) each, read
 //     back by the wave alone: the B operands are formed from the nibbles in
 //     registers (no dequantised tile written to LDS, no row done twice).
-// Per 32-value block the MFMA partial products are scaled by the block's
-// fp16 scale in fp32 (acc += d * (X . q)), as in q4_gemm_kernel, in the same
-// order: the two kernels' results are identical.
+// Per 32-value block the MFMA partial products (k-steps 0 and 1, hi then lo
+// part of each) are scaled by the block's fp16 scale in fp32:
+// acc += d * (X . q), as dequantising the block to fp32 computes.
 constexpr int kWN = 256;                          // weight rows per workgroup
 constexpr int kWStages = 3;                       // iterations staged ahead
 constexpr int kWPlane = 64 * kBK * 2;             // one activation plane: 8 KB
@@ -620,32 +394,6 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *out, const float *i
   }
 }
 
-template <int MODE, int BM, int PF>
-hipError_t set_lds_limit() {
-  return hipFuncSetAttribute((const void *)q4_gemm_kernel<MODE, BM, PF>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)(2 * sizeof(GemmLds<BM>)));
-}
-
-template <int MODE, int BM, int PF>
-hipError_t launch_gemm_variant(const GemmParams &p, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
-  constexpr size_t kLds = 2 * sizeof(GemmLds<BM>);
-  const dim3 grid((p.N + kBN - 1) / kBN, (p.S + BM - 1) / BM, p.ksplit);
-  hipExtLaunchKernelGGL((q4_gemm_kernel<MODE, BM, PF>), grid, dim3(kGThreads), kLds, s, ev0, ev1,
-                        0, p);
-  if (p.ksplit > 1) {
-    const size_t total = (size_t)p.S * p.N;
-    const unsigned blocks = (unsigned)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
-    hipLaunchKernelGGL(gemm_reduce_kernel<MODE>, dim3(blocks), dim3(256), 0, s, p);
-  }
-  return hipGetLastError();
-}
-
-// 64-token tiles (74 KB of LDS per workgroup).  Grids with more workgroups
-// than CUs keep two per CU with PF = 2; grids of at most one per CU use
-// PF = 3.  Measured at S = 512 (PF 1 / 2 / 3): W1 14336 x 4096 222 / 189 /
-// 286 us, QKV 6144 x 4096 106 / 92 / 137, Wo 4096 x 4096 88 / - / 72,
-// W2 4096 x 14336 312 / - / 242.
 template <int MODE>
 hipError_t set_wide_lds_limit() {
   return hipFuncSetAttribute((const void *)q4_gemm_wide_kernel<MODE>,
@@ -683,10 +431,7 @@ int gemm_pick_ksplit(int N, int K, int S, int num_cus) {
 
 hipError_t prepare_gemm() {
   const hipError_t e[] = {
-      set_lds_limit<kGemmStore, 64, 2>(),   set_lds_limit<kGemmStore, 64, 3>(),
-      set_lds_limit<kGemmAdd, 64, 2>(),     set_lds_limit<kGemmAdd, 64, 3>(),
-      set_lds_limit<kGemmSiluMul, 64, 2>(), set_lds_limit<kGemmSiluMul, 64, 3>(),
-      set_wide_lds_limit<kGemmStore>(),     set_wide_lds_limit<kGemmAdd>(),
+      set_wide_lds_limit<kGemmStore>(), set_wide_lds_limit<kGemmAdd>(),
       set_wide_lds_limit<kGemmSiluMul>()};
   for (hipError_t x : e)
     if (x != hipSuccess) return x;
