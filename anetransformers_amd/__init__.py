@@ -159,7 +159,14 @@ _SIGS = {
     ),
     "mia_rmsnorm_f32": (c_int, [_P, _P, _P, c_int, c_int, c_float, _P]),
     "mia_q4_0_gemm_f32": (c_int, [_P, _P, _P, c_int, c_int, c_int, _P]),
+    "mia_q4_0_pack_gemm": (c_int, [_P, _P, c_int, c_int, _P]),
+    "mia_q4_0_gemm_packed_f32": (c_int, [_P, _P, _P, c_int, c_int, c_int, _P]),
     "mia_prefill_layer": (
+        c_int,
+        [_P, POINTER(LayerWeights), _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,
+         c_int, c_int, _P],
+    ),
+    "mia_prefill_layer_packed": (
         c_int,
         [_P, POINTER(LayerWeights), _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,
          c_int, c_int, _P],

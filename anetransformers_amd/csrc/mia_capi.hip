@@ -393,7 +393,7 @@ int q4_impl(const void *Wq, const void *Wk, const void *Wv, const void *x_q8, co
 int gemm_impl(DevCtx *c, const void *W0, const void *W1, const void *W2, int rows0, int rows1,
               int rows2, const float *X, int K, int S, float *y0, float *y1, float *y2, int mode,
               hipStream_t s, bool reuse_split = false, const _Float16 *planes = nullptr,
-              _Float16 *out_planes = nullptr) {
+              _Float16 *out_planes = nullptr, bool packed = false) {
   // X [S][K] as fp16 hi + lo planes in split_work; reuse_split: the planes of
   // the input are already there (written by the call before on this stream,
   // or by the RMSNorm that produced them), and X is not read.
@@ -428,6 +428,7 @@ int gemm_impl(DevCtx *c, const void *W0, const void *W1, const void *W2, int row
   p.y0 = y0;
   p.y1 = y1;
   p.y2 = y2;
+  p.packed = packed ? 1 : 0;
   p.ksplit = mia::gemm_pick_ksplit(p.N, K, S, c->num_cus);
   if (p.ksplit > 1) {
     if (int rc = ensure_gemm_work(c, (size_t)p.ksplit * S * p.N * sizeof(float))) return rc;
@@ -907,10 +908,41 @@ int mia_q4_0_gemm_f32(const void *W, const float *X, float *Y, int out_dim, int 
                    mia::kGemmStore, pick_stream(c, stream));
 }
 
-int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_inv,
-                      uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden, int n_heads,
-                      int n_kv_heads, float eps, int max_seq, int start_pos, int S,
-                      void *stream) {
+int mia_q4_0_pack_gemm(const void *W, void *Wp, int out_dim, int in_dim, void *stream) {
+  if (!W || !Wp) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (out_dim <= 0 || in_dim <= 0 || out_dim % 64 || in_dim % 64)
+    return set_err(MIA_ERR_INVALID, "out_dim %d and in_dim %d must be positive multiples of 64",
+                   out_dim, in_dim);
+  if ((uintptr_t)W & 3) return set_err(MIA_ERR_INVALID, "W must be 4-byte aligned");
+  if ((uintptr_t)Wp & 15) return set_err(MIA_ERR_INVALID, "Wp must be 16-byte aligned");
+  const uintptr_t bytes = (uintptr_t)out_dim * (uintptr_t)(in_dim / 32) * 18;
+  const uintptr_t a = (uintptr_t)W, b = (uintptr_t)Wp;
+  if (a < b + bytes && b < a + bytes) return set_err(MIA_ERR_INVALID, "W and Wp overlap");
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  HIP_TRY(mia::launch_q4_pack(W, Wp, out_dim, in_dim, pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_q4_0_gemm_packed_f32(const void *Wp, const float *X, float *Y, int out_dim, int in_dim,
+                             int S, void *stream) {
+  if (!Wp || !X || !Y) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (int rc = check_gemm_dims(out_dim, in_dim, S)) return rc;
+  if (out_dim % 64) return set_err(MIA_ERR_INVALID, "out_dim %d must be a multiple of 64", out_dim);
+  if ((uintptr_t)Wp & 15) return set_err(MIA_ERR_INVALID, "Wp must be 16-byte aligned");
+  if (int rc = check_align16(X, Y, nullptr, nullptr)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  return gemm_impl(c, Wp, nullptr, nullptr, out_dim, 0, 0, X, in_dim, S, Y, nullptr, nullptr,
+                   mia::kGemmStore, pick_stream(c, stream), false, nullptr, nullptr, true);
+}
+
+// (every row count, dim, kv_dim and hidden, is a multiple of 64 here, as the
+// tile layout needs)
+static int prefill_layer_impl(float *X, const mia_layer_weights *lw, const float *theta_inv,
+                       uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden, int n_heads,
+                       int n_kv_heads, float eps, int max_seq, int start_pos, int S, void *stream,
+                       bool packed) {
   if (!X || !lw || !theta_inv || !k_layer || !v_layer) return set_err(MIA_ERR_INVALID, "NULL pointer");
   if (!lw->wq || !lw->wk || !lw->wv || !lw->wo || !lw->w1 || !lw->w2 || !lw->w3 || !lw->rms_att ||
       !lw->rms_ffn)
@@ -924,7 +956,8 @@ int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_
   const uintptr_t wb = (uintptr_t)lw->wq | (uintptr_t)lw->wk | (uintptr_t)lw->wv |
                        (uintptr_t)lw->wo | (uintptr_t)lw->w1 | (uintptr_t)lw->w2 |
                        (uintptr_t)lw->w3;
-  if (wb & 3) return set_err(MIA_ERR_INVALID, "weights must be 4-byte aligned");
+  if (wb & (packed ? 15 : 3))
+    return set_err(MIA_ERR_INVALID, "weights must be %d-byte aligned", packed ? 16 : 4);
   if (int rc = check_align16(X, lw->rms_att, lw->rms_ffn, k_layer)) return rc;
   if (int rc = check_align16(v_layer, nullptr, nullptr, nullptr)) return rc;
   DevCtx *c;
@@ -952,7 +985,7 @@ int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_
   // mistral_ane_prefill.h:1092-1110
   HIP_TRY(mia::launch_rmsnorm_split(xn_hi, xn_lo, X, lw->rms_att, dim, S, eps, s));
   if (int rc = gemm_impl(c, lw->wq, lw->wk, lw->wv, dim, kv_dim, kv_dim, nullptr, dim, S, Q, K,
-                         V, mia::kGemmStore, s, /*reuse_split=*/true))
+                         V, mia::kGemmStore, s, /*reuse_split=*/true, nullptr, nullptr, packed))
     return rc;
   // apply_rope_batch, kv_write_batch, attention_batch (:1097-1098): every
   // token's K/V go into the ring first and each query attends the ring as
@@ -967,17 +1000,35 @@ int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_
                           start_pos, S, s))
     return rc;
   if (int rc = gemm_impl(c, lw->wo, nullptr, nullptr, dim, 0, 0, A, dim, S, X, nullptr, nullptr,
-                         mia::kGemmAdd, s))
+                         mia::kGemmAdd, s, false, nullptr, nullptr, packed))
     return rc;
   HIP_TRY(mia::launch_rmsnorm_split(xn_hi, xn_lo, X, lw->rms_ffn, dim, S, eps, s));
   if (int rc = gemm_impl(c, lw->w1, nullptr, nullptr, hidden, 0, 0, nullptr, dim, S, G, nullptr,
-                         nullptr, mia::kGemmStore, s, /*reuse_split=*/true))
+                         nullptr, mia::kGemmStore, s, /*reuse_split=*/true, nullptr, nullptr,
+                         packed))
     return rc;
   if (int rc = gemm_impl(c, lw->w3, nullptr, nullptr, hidden, 0, 0, nullptr, dim, S, G, nullptr,
-                         nullptr, mia::kGemmSiluMul, s, /*reuse_split=*/true, nullptr, h_planes))
+                         nullptr, mia::kGemmSiluMul, s, /*reuse_split=*/true, nullptr, h_planes,
+                         packed))
     return rc;
   return gemm_impl(c, lw->w2, nullptr, nullptr, dim, 0, 0, nullptr, hidden, S, X, nullptr,
-                   nullptr, mia::kGemmAdd, s, false, h_planes);
+                   nullptr, mia::kGemmAdd, s, false, h_planes, nullptr, packed);
+}
+
+int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_inv,
+                      uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden, int n_heads,
+                      int n_kv_heads, float eps, int max_seq, int start_pos, int S,
+                      void *stream) {
+  return prefill_layer_impl(X, lw, theta_inv, k_layer, v_layer, dim, hidden, n_heads, n_kv_heads,
+                            eps, max_seq, start_pos, S, stream, false);
+}
+
+int mia_prefill_layer_packed(float *X, const mia_layer_weights *lw, const float *theta_inv,
+                             uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden,
+                             int n_heads, int n_kv_heads, float eps, int max_seq, int start_pos,
+                             int S, void *stream) {
+  return prefill_layer_impl(X, lw, theta_inv, k_layer, v_layer, dim, hidden, n_heads, n_kv_heads,
+                            eps, max_seq, start_pos, S, stream, true);
 }
 
 int mia_quantize_q8_0(const float *x, void *out_q8, int n, void *stream) {

@@ -162,8 +162,14 @@ struct GemmParams {
   // [S][N] (the next GEMM's input, launch_split_hilo's split) instead of
   // into y0.
   _Float16 *ohi, *olo;
+  // w0, w1, w2 in the GEMM tile layout of launch_q4_pack (row counts and K
+  // multiples of 64) instead of the GGUF layout
+  int packed;
 };
 long gemm_tiles(int N, int S);
+// Q4_0 [N][K / 32] in the GGUF layout -> the GEMM tile layout (same size;
+// N and K multiples of 64, src 4-byte and dst 16-byte aligned, no overlap).
+hipError_t launch_q4_pack(const void *src, void *dst, int N, int K, hipStream_t s);
 int gemm_pick_ksplit(int N, int K, int S, int num_cus);
 hipError_t launch_q4_gemm(const GemmParams &p, int mode, int num_cus, hipStream_t s,
                           hipEvent_t ev0, hipEvent_t ev1);

@@ -15,6 +15,9 @@
 // each iteration covers 64 K values (two Q4_0 blocks, 36 bytes of each row,
 // 4-byte aligned because the blocks per row are even), staged three
 // iterations ahead by direct-to-LDS loads (q4_gemm_wide_kernel below).
+// The weights are read either in the GGUF layout (rows of blocks) or in the
+// GEMM tile layout of q4_pack_kernel (the same bytes regrouped once, so that
+// a wave's 64 rows x 2 blocks are one contiguous 2,304-byte tile).
 #include <algorithm>
 
 #include "mia_device.h"
@@ -76,8 +79,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams &p, int m, int n,
 // direct loads (global_load_lds), kWStages iterations deep, with one
 // barrier per iteration:
 //   - the activations' hi and lo planes, 64 tokens x 64 K each, shared by the
-//     four waves, 16-byte chunk c of token row r at chunk c ^ (r & 7) (the
-//     32 rows an operand read touches then spread over every bank);
+//     four waves, 16-byte chunk c of token row r at chunk c ^ aswz(r) (any 8
+//     consecutive rows of an operand read then cover 128 bytes of banks and
+//     any 16 rows 256 bytes);
 //   - each wave's own 64 weight rows, 36 bytes (two Q4_0 blocks) each, read
 //     back by the wave alone: the B operands are formed from the nibbles in
 //     registers (no dequantised tile written to LDS, no row done twice).
@@ -89,6 +93,25 @@ constexpr int kWStages = 3;                       // iterations staged ahead
 constexpr int kWPlane = 64 * kBK * 2;             // one activation plane: 8 KB
 constexpr int kWBRows = 64 * 36;                  // one wave's weight rows: 2304 B
 constexpr int kWStage = 2 * kWPlane + 4 * kWBRows;  // 25,600 B
+
+// The GEMM tile layout of a Q4_0 matrix [N][K / 32 blocks], N and K multiples
+// of 64: tile (s, i) holds rows 64 s .. 64 s + 63 and blocks 2 i, 2 i + 1 at
+// byte (s * (K / 64) + i) * 2304:
+//   - bytes h * 1024 + rr * 16 + 8 * bb + j (half h, row rr, block bb, j < 8):
+//     byte 8 h + kPackOrder[j] of the block's 16 quant bytes;
+//   - bytes 2048 + rr * 4 + 2 * bb: the block's fp16 scale.
+// A wave stages its tile with two 16-byte and one 4-byte direct load per
+// lane, and a lane (row rr, half h) reads its 16 quant bytes in one 16-byte
+// LDS read.  In each 4 bytes the order 0, 2, 1, 3 puts the quant bytes of a
+// value pair (2t, 2t + 1) in bytes 0 and 2 (t even) or 1 and 3 (t odd), so a
+// shift and a mask give both values' nibbles under the fp16 exponent.
+constexpr int kPackTile = 2304;
+__device__ constexpr int kPackOrder[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+
+// Chunk swizzle of a 128-byte activation row r: rows r and r + 8 (same bank
+// half, same r & 7) get different chunks, so 16 rows read together hit 16
+// different 16-byte bank groups, 8 rows 8 different ones.
+__device__ __forceinline__ int aswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // 16 (dwordx4) or 4 (dword) bytes per lane from global memory into LDS at
 // byte M0 + lane * size; completion is awaited with vmcnt (the compiler does
@@ -122,7 +145,7 @@ __device__ __forceinline__ void gemm_wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int MODE>
+template <int MODE, bool PK>
 __global__ __launch_bounds__(kGThreads, 2) void q4_gemm_wide_kernel(GemmParams p) {
 #pragma clang fp contract(off)
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -138,40 +161,64 @@ __global__ __launch_bounds__(kGThreads, 2) void q4_gemm_wide_kernel(GemmParams p
 
   // Activation loads: wave w fills plane w >> 1, token rows 32 (w & 1) .. +32,
   // four instructions of 8 rows; lane i of instruction j: row
-  // r = 32 (w & 1) + 8 j + i / 8, LDS chunk i % 8 = logical chunk (i % 8) ^ (r & 7).
+  // r = 32 (w & 1) + 8 j + i / 8, LDS chunk i % 8 = logical chunk (i % 8) ^ aswz(r).
   const _Float16 *asrc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = 32 * (w & 1) + 8 * j + (lane >> 3);
-    const int c = (lane & 7) ^ (r & 7);
+    const int c = (lane & 7) ^ aswz(r);
     asrc[j] = ((w >> 1) ? p.alo : p.ahi) + (size_t)min(m0 + r, p.S - 1) * p.K + 8 * c;
   }
   const unsigned a_lds = (unsigned)((w >> 1) * kWPlane + 32 * (w & 1) * (kBK * 2));
-  // Weight loads: the wave's 64 rows x 9 dwords, nine instructions of 64
-  // dwords; lane i of instruction j: dword q = 64 j + i, row q / 9, dword q % 9.
-  const uint8_t *bsrc[9];
-#pragma unroll
-  for (int j = 0; j < 9; ++j) {
-    const int q = 64 * j + lane;
-    const int g = min(n0 + 64 * w + q / 9, p.N - 1);
+  // Weight loads.  GGUF layout: the wave's 64 rows x 9 dwords, nine
+  // instructions of 64 dwords; lane i of instruction j: dword q = 64 j + i,
+  // row q / 9, dword q % 9.  Tile layout: the wave's tile, two 16-byte loads
+  // and one 4-byte load per lane, in order.
+  constexpr int kBLoads = PK ? 3 : 9;
+  const uint8_t *bsrc[kBLoads];
+  if constexpr (PK) {
+    // every wave's rows lie in one matrix (its row counts are multiples of
+    // 64); a wave past N loads the last tile of rows (its results are not
+    // written)
+    const int g = min(n0 + 64 * w, p.N - 64);
     const uint8_t *base = g < p.rows0 ? p.w0 : (g < p.rows01 ? p.w1 : p.w2);
     const int lr = g < p.rows0 ? g : (g < p.rows01 ? g - p.rows0 : g - p.rows01);
-    bsrc[j] = base + (size_t)lr * (size_t)(p.K / 32) * 18 + 4 * (q % 9);
+    const uint8_t *tile = base + (size_t)(lr / 64) * (size_t)(p.K / kBK) * kPackTile;
+    bsrc[0] = tile + 16 * lane;
+    bsrc[1] = tile + 1024 + 16 * lane;
+    bsrc[2] = tile + 2048 + 4 * lane;
+  } else {
+#pragma unroll
+    for (int j = 0; j < kBLoads; ++j) {
+      const int q = 64 * j + lane;
+      const int g = min(n0 + 64 * w + q / 9, p.N - 1);
+      const uint8_t *base = g < p.rows0 ? p.w0 : (g < p.rows01 ? p.w1 : p.w2);
+      const int lr = g < p.rows0 ? g : (g < p.rows01 ? g - p.rows0 : g - p.rows01);
+      bsrc[j] = base + (size_t)lr * (size_t)(p.K / 32) * 18 + 4 * (q % 9);
+    }
   }
   const unsigned b_lds = (unsigned)(2 * kWPlane + w * kWBRows);
-  // Iteration `it` (absolute) into stage `st`: 4 + 9 loads per wave.
+  // Iteration `it` (absolute) into stage `st`: 4 + 9 (GGUF) or 4 + 3 (tile)
+  // loads per wave.
   auto issue = [&](int st, int it) {
     const unsigned sb = sbase + (unsigned)(st * kWStage);
     // (wave-uniform offsets: one scalar multiply, then a 64-bit add per lane)
     const unsigned aoff = __builtin_amdgcn_readfirstlane((unsigned)it * (unsigned)(kBK * 2));
-    const unsigned boff = __builtin_amdgcn_readfirstlane((unsigned)it * 36u);
+    const unsigned boff =
+        __builtin_amdgcn_readfirstlane((unsigned)it * (PK ? (unsigned)kPackTile : 36u));
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       lds_dma16((const char *)asrc[j] + aoff, sb + a_lds + 1024u * j);
+    if constexpr (PK) {
+      lds_dma16(bsrc[0] + boff, sb + b_lds);
+      lds_dma16(bsrc[1] + boff, sb + b_lds + 1024u);
+      lds_dma4(bsrc[2] + boff, sb + b_lds + 2048u);
+    } else {
 #pragma unroll
-    for (int j = 0; j < 9; ++j) lds_dma4(bsrc[j] + boff, sb + b_lds + 256u * j);
+      for (int j = 0; j < kBLoads; ++j) lds_dma4(bsrc[j] + boff, sb + b_lds + 256u * j);
+    }
   };
-  constexpr int kLoadsPerStage = 13;
+  constexpr int kLoadsPerStage = 4 + kBLoads;
 
   f16v acc[2][2];
 #pragma unroll
@@ -191,18 +238,34 @@ __global__ __launch_bounds__(kGThreads, 2) void q4_gemm_wide_kernel(GemmParams p
     // this lane's weight rows (tn): dwords 2h .. 2h+2 (block 0's nibbles
     // 8h .. 8h+7 at byte offset 2), dword 0 (scale 0, low half), dword 4
     // (scale 1, high half), dwords 5+2h, 6+2h (block 1's nibbles 8h .. 8h+7)
+    // (tile layout: the lane's 16 quant bytes and the row's two scales)
     unsigned nb[2][2][2];  // [tn][block][dword]: 8 nibble bytes
     float dsc[2][2];       // [tn][block]
 #pragma unroll
     for (int tn = 0; tn < 2; ++tn) {
-      const unsigned rb = sb + b_lds + (unsigned)((32 * tn + col) * 36);
-      const lds_u32 *r = (const lds_u32 *)(__UINTPTR_TYPE__)rb;
-      const unsigned x0 = r[2 * half], x1 = r[2 * half + 1], x2 = r[2 * half + 2];
-      const unsigned s0 = r[0], s1 = r[4];
-      nb[tn][0][0] = __builtin_amdgcn_alignbyte(x1, x0, 2);
-      nb[tn][0][1] = __builtin_amdgcn_alignbyte(x2, x1, 2);
-      nb[tn][1][0] = r[5 + 2 * half];
-      nb[tn][1][1] = r[6 + 2 * half];
+      unsigned s0, s1;
+      if constexpr (PK) {
+        typedef __attribute__((address_space(3))) u4 lds_u4;
+        const int rr = 32 * tn + col;
+        const u4 qv = *(const lds_u4 *)(__UINTPTR_TYPE__)(sb + b_lds +
+                                                          (unsigned)(half * 1024 + rr * 16));
+        s0 = *(const lds_u32 *)(__UINTPTR_TYPE__)(sb + b_lds + (unsigned)(2048 + rr * 4));
+        s1 = s0;
+        nb[tn][0][0] = qv[0];
+        nb[tn][0][1] = qv[1];
+        nb[tn][1][0] = qv[2];
+        nb[tn][1][1] = qv[3];
+      } else {
+        const unsigned rb = sb + b_lds + (unsigned)((32 * tn + col) * 36);
+        const lds_u32 *r = (const lds_u32 *)(__UINTPTR_TYPE__)rb;
+        const unsigned x0 = r[2 * half], x1 = r[2 * half + 1], x2 = r[2 * half + 2];
+        s0 = r[0];
+        s1 = r[4];
+        nb[tn][0][0] = __builtin_amdgcn_alignbyte(x1, x0, 2);
+        nb[tn][0][1] = __builtin_amdgcn_alignbyte(x2, x1, 2);
+        nb[tn][1][0] = r[5 + 2 * half];
+        nb[tn][1][1] = r[6 + 2 * half];
+      }
       dsc[tn][0] = f16_bits_f32(s0);
       dsc[tn][1] = f16_bits_f32(s1 >> 16);
       // converted once here: folded into each FMA, the conversion makes
@@ -213,23 +276,30 @@ __global__ __launch_bounds__(kGThreads, 2) void q4_gemm_wide_kernel(GemmParams p
     for (int kb = 0; kb < 2; ++kb) {
       // B operands of the block's two k-steps: values 16 ks + 8h .. +8 are
       // the low (ks 0) or high (ks 1) nibbles of the lane's 8 bytes.  A pair
-      // of consecutive bytes goes to the two halves of a dword with one byte
-      // permute, and one AND-OR leaves their nibbles under the fp16 exponent
-      // of 1024 (0x6400 | n = 1024 + n); subtracting 1032 gives n - 8.
+      // of consecutive bytes goes to the two halves of a dword (GGUF layout:
+      // one byte permute; tile layout: a shift, the pair being in bytes 0
+      // and 2 or 1 and 3 already), and one AND-OR leaves their nibbles under
+      // the fp16 exponent of 1024 (0x6400 | n = 1024 + n); subtracting 1032
+      // gives n - 8.
       h8 bop[2][2];  // [ks][tn]
 #pragma unroll
       for (int tn = 0; tn < 2; ++tn)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const unsigned x0 = ks ? nb[tn][kb][0] >> 4 : nb[tn][kb][0];
-          const unsigned x1 = ks ? nb[tn][kb][1] >> 4 : nb[tn][kb][1];
+          const unsigned x0 = ks && !PK ? nb[tn][kb][0] >> 4 : nb[tn][kb][0];
+          const unsigned x1 = ks && !PK ? nb[tn][kb][1] >> 4 : nb[tn][kb][1];
           unsigned v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            // bytes 2q, 2q+1 of x1:x0 into bytes 0 and 2 (perm selectors 0-3
-            // pick x0's bytes, 4-7 x1's)
-            const unsigned sel = (unsigned)(2 * q) | ((unsigned)(2 * q + 1) << 16);
-            const unsigned t = __builtin_amdgcn_perm(x1, x0, sel);
+            unsigned t;
+            if constexpr (PK) {
+              t = (q < 2 ? x0 : x1) >> (8 * (q & 1) + 4 * ks);
+            } else {
+              // bytes 2q, 2q+1 of x1:x0 into bytes 0 and 2 (perm selectors
+              // 0-3 pick x0's bytes, 4-7 x1's)
+              const unsigned sel = (unsigned)(2 * q) | ((unsigned)(2 * q + 1) << 16);
+              t = __builtin_amdgcn_perm(x1, x0, sel);
+            }
             // (t & mask) | exponent in one instruction (the compiler keeps
             // both constants as literals, which a VOP3 cannot take; one
             // scalar operand at most)
@@ -249,7 +319,7 @@ __global__ __launch_bounds__(kGThreads, 2) void q4_gemm_wide_kernel(GemmParams p
 #pragma unroll
         for (int tm = 0; tm < 2; ++tm) {
           const int r = 32 * tm + col;
-          const unsigned off = (unsigned)(r * (kBK * 2) + 16 * (c ^ (r & 7)));
+          const unsigned off = (unsigned)(r * (kBK * 2) + 16 * (c ^ aswz(r)));
           ah[tm] = *(const lds_h8 *)(__UINTPTR_TYPE__)(sb + off);
           al[tm] = *(const lds_h8 *)(__UINTPTR_TYPE__)(sb + kWPlane + off);
         }
@@ -327,6 +397,39 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
   }
 }
 
+// GGUF layout -> GEMM tile layout (above): one thread per (row, block pair),
+// 36 bytes in, the same 36 bytes out at their tile places.
+__global__ __launch_bounds__(256) void q4_pack_kernel(const uint8_t *__restrict__ src,
+                                                      uint8_t *__restrict__ dst, int N, int K) {
+  const int steps = K / kBK;
+  const long e = (long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (long)N * steps) return;
+  const int row = (int)(e / steps), i = (int)(e % steps);
+  const unsigned *in = reinterpret_cast<const unsigned *>(src + ((size_t)row * steps + i) * 36);
+  unsigned x[9];
+#pragma unroll
+  for (int j = 0; j < 9; ++j) x[j] = in[j];
+  auto byte = [&](int b) { return (x[b >> 2] >> (8 * (b & 3))) & 0xFFu; };
+  uint8_t *tile = dst + ((size_t)(row / 64) * steps + i) * kPackTile;
+  const int rr = row % 64;
+  // block bb: scale at bytes 18 bb, 18 bb + 1; quant bytes at 18 bb + 2 ..
+  *reinterpret_cast<unsigned *>(tile + 2048 + 4 * rr) = byte(0) | byte(1) << 8 |
+                                                        byte(18) << 16 | byte(19) << 24;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    unsigned o[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const int bb = d >> 1, j0 = 4 * (d & 1);
+      unsigned v = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v |= byte(18 * bb + 2 + 8 * h + kPackOrder[j0 + j]) << (8 * j);
+      o[d] = v;
+    }
+    *reinterpret_cast<u4 *>(tile + h * 1024 + rr * 16) = (u4){o[0], o[1], o[2], o[3]};
+  }
+}
+
 // One workgroup per token row: ss = sum(x^2), scale = 1 / sqrt(ss / dim + eps),
 // out = (x * scale) * w, the reference's two roundings (vsmul then vmul).
 // The GEMM's fp32 activations as fp16 hi + lo planes (x = hi + lo to ~2^-22:
@@ -396,7 +499,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *out, const float *i
 
 template <int MODE>
 hipError_t set_wide_lds_limit() {
-  return hipFuncSetAttribute((const void *)q4_gemm_wide_kernel<MODE>,
+  const hipError_t e = hipFuncSetAttribute((const void *)q4_gemm_wide_kernel<MODE, false>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           kWStages * kWStage);
+  if (e != hipSuccess) return e;
+  return hipFuncSetAttribute((const void *)q4_gemm_wide_kernel<MODE, true>,
                              hipFuncAttributeMaxDynamicSharedMemorySize, kWStages * kWStage);
 }
 
@@ -405,8 +512,12 @@ hipError_t launch_gemm_mode(const GemmParams &p, int num_cus, hipStream_t s, hip
                             hipEvent_t ev1) {
   (void)num_cus;
   const dim3 grid((p.N + kWN - 1) / kWN, (p.S + 63) / 64, p.ksplit);
-  hipExtLaunchKernelGGL((q4_gemm_wide_kernel<MODE>), grid, dim3(kGThreads), kWStages * kWStage,
-                        s, ev0, ev1, 0, p);
+  if (p.packed)
+    hipExtLaunchKernelGGL((q4_gemm_wide_kernel<MODE, true>), grid, dim3(kGThreads),
+                          kWStages * kWStage, s, ev0, ev1, 0, p);
+  else
+    hipExtLaunchKernelGGL((q4_gemm_wide_kernel<MODE, false>), grid, dim3(kGThreads),
+                          kWStages * kWStage, s, ev0, ev1, 0, p);
   if (p.ksplit > 1) {
     const size_t total = (size_t)p.S * p.N;
     const unsigned blocks = (unsigned)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
@@ -443,6 +554,14 @@ hipError_t launch_q4_gemm(const GemmParams &p, int mode, int num_cus, hipStream_
   if (mode == kGemmStore) return launch_gemm_mode<kGemmStore>(p, num_cus, s, ev0, ev1);
   if (mode == kGemmAdd) return launch_gemm_mode<kGemmAdd>(p, num_cus, s, ev0, ev1);
   return launch_gemm_mode<kGemmSiluMul>(p, num_cus, s, ev0, ev1);
+}
+
+hipError_t launch_q4_pack(const void *src, void *dst, int N, int K, hipStream_t s) {
+  const long n = (long)N * (K / kBK);
+  hipLaunchKernelGGL(q4_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                     reinterpret_cast<const uint8_t *>(src), reinterpret_cast<uint8_t *>(dst), N,
+                     K);
+  return hipGetLastError();
 }
 
 hipError_t launch_split_hilo(const float *x, long n, _Float16 *hi, _Float16 *lo, int num_cus,

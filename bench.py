@@ -588,12 +588,15 @@ def q4_bytes(rows: int, cols: int) -> int:
 
 
 class PrefillLayers:
-    """The whole prefill layer on the GPU (mia_prefill_layer), 32 layers with
-    their own Q4_0 weights (3.9 GB), S = 512 new tokens after 1536 cached
-    positions, the residual stream X carried from layer to layer."""
+    """The whole prefill layer on the GPU (mia_prefill_layer_packed), 32 layers
+    with their own Q4_0 weights (3.9 GB, regrouped once into the GEMM tile
+    layout by mia_q4_0_pack_gemm at set-up, as a loader would), S = 512 new
+    tokens after 1536 cached positions, the residual stream X carried from
+    layer to layer.  packed=False: mia_prefill_layer on the GGUF layout."""
 
-    def __init__(self, lib, seed: int = 51):
+    def __init__(self, lib, seed: int = 51, packed: bool = True):
         self.lib = lib
+        self.packed = packed
         g = np.random.default_rng(seed)
         self.sizes = [("wq", DIM, DIM), ("wk", KV_DIM, DIM), ("wv", KV_DIM, DIM), ("wo", DIM, DIM),
                       ("w1", HIDDEN, DIM), ("w2", DIM, HIDDEN), ("w3", HIDDEN, DIM)]
@@ -603,6 +606,15 @@ class PrefillLayers:
         # x 2^-12 keeps the block scales near 2.4e-4: the residual stream stays O(1)
         check(lib.mia_scale_rows_f16(self.w.ptr, N_LAYERS * self.lw_bytes // 2048, 1024, 1, 0,
                                      1.0 / 4096, None))
+        if packed:
+            wp = DeviceBuffer(N_LAYERS * self.lw_bytes)
+            off = 0
+            for _ in range(N_LAYERS):
+                for _, r, c in self.sizes:
+                    check(lib.mia_q4_0_pack_gemm(self.w.ptr + off, wp.ptr + off, r, c, None))
+                    off += q4_bytes(r, c)
+            check(lib.mia_device_sync())
+            self.w = wp                              # (the GGUF-layout copy is freed)
         self.norms = DeviceBuffer.from_array(
             (1.0 + 0.1 * g.standard_normal((N_LAYERS, 2, DIM))).astype(np.float32))
         lay = PF_M * KV_DIM
@@ -628,11 +640,11 @@ class PrefillLayers:
 
     def step(self) -> None:
         lay = PF_M * KV_DIM * 2
+        fn = self.lib.mia_prefill_layer_packed if self.packed else self.lib.mia_prefill_layer
         for l in range(N_LAYERS):
-            check(self.lib.mia_prefill_layer(self.X.ptr, ctypes.byref(self.lws[l]), self.th.ptr,
-                                             self.kc.ptr + l * lay, self.vc.ptr + l * lay, DIM,
-                                             HIDDEN, N_HEADS, N_KV, 1e-5, PF_M, PF_START, PF_S,
-                                             None), "prefill_layer")
+            check(fn(self.X.ptr, ctypes.byref(self.lws[l]), self.th.ptr, self.kc.ptr + l * lay,
+                     self.vc.ptr + l * lay, DIM, HIDDEN, N_HEADS, N_KV, 1e-5, PF_M, PF_START, PF_S,
+                     None), "prefill_layer")
 
 
 def cpu_baseline_prefill_layer():

@@ -255,6 +255,21 @@ int mia_rmsnorm_f32(float *out, const float *in, const float *w, int dim, int S,
 int mia_q4_0_gemm_f32(const void *W, const float *X, float *Y, int out_dim, int in_dim, int S,
                       void *stream);
 
+/* The same weights regrouped once, at load time, for the GEMM (no reference
+ * counterpart: the reference dequantises the GGUF blocks per 128-row tile,
+ * mistral/mistral_ane_prefill.h:1018-1042; the values are unchanged).  Wp
+ * (dev, 16-byte aligned, not overlapping W) receives the out_dim x in_dim / 32
+ * blocks of W (dev, 4-byte aligned) in the GEMM tile layout: for each 64 rows
+ * and 64 columns one contiguous 2,304-byte tile, the rows' quant bytes first,
+ * their fp16 scales after.  out_dim and in_dim multiples of 64. */
+int mia_q4_0_pack_gemm(const void *W, void *Wp, int out_dim, int in_dim, void *stream);
+
+/* mia_q4_0_gemm_f32 on weights in the tile layout of mia_q4_0_pack_gemm:
+ * bit-identical results, fewer and contiguous weight loads.  out_dim a
+ * multiple of 64, Wp 16-byte aligned. */
+int mia_q4_0_gemm_packed_f32(const void *Wp, const float *X, float *Y, int out_dim, int in_dim,
+                             int S, void *stream);
+
 /* One layer's Q4_0 weights on the device (GGUF layout) and RMSNorm weights. */
 typedef struct {
     const void *wq, *wk, *wv, *wo; /* attention projections */
@@ -278,6 +293,14 @@ int mia_prefill_layer(float *X, const mia_layer_weights *lw, const float *theta_
                       uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden, int n_heads,
                       int n_kv_heads, float eps, int max_seq, int start_pos, int S,
                       void *stream);
+
+/* mia_prefill_layer with the seven Q4_0 matrices of lw in the tile layout of
+ * mia_q4_0_pack_gemm (16-byte aligned; the RMSNorm weights as before):
+ * bit-identical results. */
+int mia_prefill_layer_packed(float *X, const mia_layer_weights *lw, const float *theta_inv,
+                             uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden,
+                             int n_heads, int n_kv_heads, float eps, int max_seq, int start_pos,
+                             int S, void *stream);
 
 #ifdef __cplusplus
 }

@@ -203,6 +203,22 @@ def test_prefill_argument_errors_without_device_work():
     lw.w2 = None
     assert lib.mia_prefill_layer(p, ctypes.byref(lw), p, p, p, 512, 1024, 4, 1, 1e-5, 64, 0, 4,
                                  None) == mia.MIA_ERR_INVALID
+    # the tile layout: multiples of 64, 16-byte aligned destination, no overlap
+    big = np.zeros(64 * 128 // 32 * 18 // 4 + 8, np.float32)
+    q = (big.ctypes.data + 15) // 16 * 16
+    n = 64 * 128 // 32 * 18
+    assert lib.mia_q4_0_pack_gemm(p, q, 100, 128, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_q4_0_pack_gemm(p, q, 64, 96, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_q4_0_pack_gemm(p, q + 4, 64, 128, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_q4_0_pack_gemm(q, q + n - 16, 64, 128, None) == mia.MIA_ERR_INVALID
+    assert b"overlap" in lib.mia_last_error()
+    assert lib.mia_q4_0_gemm_packed_f32(q, p, p, 96, 128, 4, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_q4_0_gemm_packed_f32(q + 4, p, p, 64, 128, 4, None) == mia.MIA_ERR_INVALID
+    lw = mia.LayerWeights(*([q] * 9))
+    lw.wo = q + 4
+    assert lib.mia_prefill_layer_packed(p, ctypes.byref(lw), p, p, p, 512, 1024, 4, 1, 1e-5, 64,
+                                        0, 4, None) == mia.MIA_ERR_INVALID
+    assert b"16-byte" in lib.mia_last_error()
 
 
 def test_q4_argument_errors_without_device_work():
