@@ -4,8 +4,9 @@ and prefill layer on packed weights.
 The layout has no reference counterpart: the reference dequantises the GGUF
 blocks per 128-row tile (mistral/mistral_ane_prefill.h:1018-1042).  So:
   - the packed bytes are checked against the layout as the header states it,
-    restated here with numpy index arithmetic (every byte of the input lands
-    exactly once, which a permutation check confirms);
+    restated with numpy index arithmetic in tests/_gemm_layout.py (every byte
+    of the input lands exactly once, which a permutation check confirms; the
+    CPU tests of test_gemm_layout.py pin the restatement);
   - the GEMM and the layer on packed weights must be bit-identical to the
     same calls on the GGUF-layout weights, which test_gpu_prefill.py holds to
     the oracle; the small GEMM shapes are also held to the oracle's bound
@@ -17,6 +18,7 @@ import numpy as np
 import pytest
 
 import _data as D
+import _gemm_layout as GL
 import _gpu as G
 import _oracle as O
 import anetransformers_amd as mia
@@ -24,24 +26,6 @@ from anetransformers_amd import DeviceBuffer as DB
 from anetransformers_amd import check
 
 pytestmark = pytest.mark.gpu
-
-ORDER = np.array([0, 2, 1, 3, 4, 6, 5, 7])
-
-
-def pack_layout(W, N, K):
-    """The tile layout of include/miattn.h (mia_q4_0_pack_gemm), in numpy."""
-    rows = W.reshape(N // 64, 64, K // 64, 36)               # [slab][row][step][2 blocks]
-    out = np.zeros((N // 64, K // 64, 2304), W.dtype)
-    rr = np.arange(64)
-    for bb in range(2):
-        for e in range(2):                                    # the fp16 scale's two bytes
-            out[:, :, 2048 + rr * 4 + 2 * bb + e] = rows[:, :, :, 18 * bb + e].transpose(0, 2, 1)
-        for h in range(2):
-            for j in range(8):
-                src = 18 * bb + 2 + 8 * h + ORDER[j]
-                out[:, :, h * 1024 + rr * 16 + 8 * bb + j] = rows[:, :, :, src].transpose(0, 2, 1)
-    return out.reshape(-1)
-
 
 def gpu_pack(dw, N, K):
     L = G.lib()
@@ -67,10 +51,10 @@ def test_pack_layout(N, K):
     dp = gpu_pack(DB.from_array(W), N, K)
     check(G.lib().mia_stream_sync(None), "sync")
     got = dp.download((W.size,), np.uint8)
-    want = pack_layout(W, N, K)
+    want = GL.pack_layout(W, N, K)
     assert np.array_equal(got, want)
     # every input byte lands exactly once: the layout is a permutation
-    perm = pack_layout(np.arange(W.size, dtype=np.int64), N, K)
+    perm = GL.pack_layout(np.arange(W.size, dtype=np.int64), N, K)
     assert np.array_equal(np.sort(perm), np.arange(W.size))
 
 
