@@ -43,7 +43,11 @@ namespace {
 constexpr int kWaves = 8;         // waves per workgroup, all on one kv head
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 16;        // keys per wave tile
-constexpr int kDepth = 2;        // register tile buffers per wave
+// Register tile buffers per wave.  One: the buffer is refilled while it is
+// consumed (K once staged to LDS, V after the P.V MFMAs), so one tile per wave
+// is in flight while the current one is processed.  Two buffers kept more
+// loads in flight and read the window ~4 % slower.
+constexpr int kDepth = 1;
 constexpr int kMaxChunks = 256;  // merge capacity per kv head
 constexpr int G = 4;             // query heads per kv head
 // Bytes per staged K row: 16 B of padding put the 16 rows of a column read
@@ -348,7 +352,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
   };
 
   // Ring of kDepth register buffers: buffer b is refilled with the next tile
-  // of the stream while it is consumed, so kDepth-1 tiles stay in flight.
+  // of the stream while it is consumed (K once staged, V after the P.V
+  // MFMAs).
   // Tiles come in stream order, so the first empty buffer ends the loop.
   for (bool more = tix[0] >= 0; more;) {
 #pragma unroll
