@@ -73,18 +73,15 @@ __global__ void __launch_bounds__(512, 1) read_ring_kernel(const _Float16 *__res
     }
   };
   if (count == 0) return;
-  u4 b0[8], b1[8];
+  // one register buffer, refilled as soon as it is consumed, as the decode
+  // kernel's (one tile per wave in flight)
+  u4 b0[8];
   u4 acc = {0u, 0u, 0u, 0u};
   issue(b0, 0);
-  issue(b1, 1);
-  for (int i = 0; i < count; i += 2) {
+  for (int i = 0; i < count; ++i) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) acc ^= b0[s];
-    issue(b0, i + 2);
-    if (i + 1 >= count) break;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) acc ^= b1[s];
-    issue(b1, i + 3);
+    if (i + 1 < count) issue(b0, i + 1);
   }
   const unsigned r = acc.x ^ acc.y ^ acc.z ^ acc.w;
   if (r == kNever) g_peak_sink[lane] = r;
