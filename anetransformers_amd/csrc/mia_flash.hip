@@ -23,12 +23,12 @@
 //   online softmax    one row per lane (the D column): running max and sum
 //                     stay lane-local; the two key halves of a row meet via
 //                     a lane exchange; the fp32 exponentials are summed in
-//                     fp32 and rounded to fp16 for P.V with v_cvt_pk (a
-//                     v_dot2 of the fp16 pairs would hold up the next MFMA's
-//                     issue by ~17 cycles; fp16 P then differs from the
-//                     summed weights by at most 2^-12 relative)
-//   O^T += V^T . P^T  P^T straight from the S^T accumulator layout, V^T via
-//                     the transposing LDS read ds_read_b64_tr_b16
+//                     fp32 and split into fp16 hi + lo parts for P.V
+//                     (p = hi + lo to ~2^-22: a single fp16 P would err by
+//                     up to 2^-11 of each weight, 2^-11 |v| in a peaked row)
+//   O^T += V^T . P^T  P^T straight from the S^T accumulator layout, hi then
+//                     lo part (two MFMAs per k-step), V^T via the
+//                     transposing LDS read ds_read_b64_tr_b16
 // The scores of tile i+1 are computed on MFMA while the exponentials of tile
 // i are formed.  Each row's softmax reference is fixed for the whole key
 // range (its first tile's max, subtracted inside the score MFMA by one extra
@@ -237,6 +237,26 @@ __device__ __forceinline__ h8 read_va(unsigned va_base) {
 // recognizer does not look inside inline assembly).
 __device__ __forceinline__ void mfma_pv(f16v &acc, const h8 &a, const h8 &b) {
   asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// The same with P^T as two fp16 parts, hi then lo (p = hi + lo to ~2^-22):
+// the P.V product then carries the fp32 weights' accuracy, where one fp16 P
+// errs by up to 2^-11 of each weight (2^-11 |v| in a peaked row).  The second
+// MFMA reads the first one's result as SrcC (the same opcode, exactly
+// overlapped): no wait states between them.
+__device__ __forceinline__ void mfma_pv2(f16v &acc, const h8 &a, const h8 &bh, const h8 &bl) {
+  asm("s_nop 1\n\t"
+      "v_mfma_f32_32x32x16_f16 %0, %1, %2, %0\n\t"
+      "v_mfma_f32_32x32x16_f16 %0, %1, %3, %0"
+      : "+a"(acc)
+      : "v"(a), "v"(bh), "v"(bl));
+}
+// fp32 pair -> fp16 hi pair and the fp16 pair of what the hi parts miss.
+__device__ __forceinline__ void split_pair(float x0, float x1, unsigned &hi, unsigned &lo) {
+  const f2 x = {x0, x1};
+  const h2 h = __builtin_convertvector(x, h2);
+  const h2 l = __builtin_convertvector(x - __builtin_convertvector(h, f2), h2);
+  hi = __builtin_bit_cast(unsigned, h);
+  lo = __builtin_bit_cast(unsigned, l);
 }
 // S^T += K . Q^T over one k-step, hi part then lo part of Q^T, both read
 // from AGPRs.  Q^T is loop-invariant (128 registers at 64 rows): held in
@@ -563,14 +583,16 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   // the max of the row's scores in its first tile (p <= 1 there), rounded to
   // fp16 and subtracted inside the score MFMA by one extra k-step (a ones
   // column in K against -m_ref in Q), so the loop neither subtracts nor
-  // tracks maxima and never rescales the accumulators.  P is fp16, so a later
-  // score more than ~16 (log2 units) above the reference overflows, and a row
-  // whose scores all sit far below an unset reference underflows: both show in
-  // the fp32 row sum of the unrounded P at the end of the pass (a P that
-  // rounds to fp16 infinity, >= 65520, makes the sum at least that; an
-  // underflowing row sums below 2^-8).  Such a wave sweeps its tiles for the
-  // exact row maxima and runs once more with them as the reference (a row
-  // whose sum is merely large, >= 65504 with no P overflowing, reruns too).
+  // tracks maxima and never rescales the accumulators.  P's hi part is fp16,
+  // so a later score more than ~16 (log2 units) above the reference
+  // overflows it, and a row whose scores all sit far below an unset reference
+  // underflows.  An underflowing row sums below 2^-8 (the fp32 row sum of the
+  // unrounded P).  A P that rounds to fp16 infinity (>= 65520) makes the row
+  // sum at least that and the row's accumulators non-finite (inf - inf from
+  // its hi and lo parts); the accumulators are only inspected when the sum
+  // is that large, so a long flat row with a large but finite sum costs one
+  // look at them, not a second pass.  A wave with such a row sweeps its tiles
+  // for the exact row maxima and runs once more with them as the reference.
   f16v o[NB][4];
   float m_ref[NB], l_run[NB];
   f16v s_cur[NB];
@@ -673,14 +695,15 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   // One tile step, with P.V one tile behind the scores: P of tile it from
   // s_cur (already shifted by the reference) into pb_next, shifted scores of
   // tile it+1 into s_cur, and (from it = 1 on) O += P.V of tile it-1 from
-  // pb.  The 34 MFMAs of a step (scores of it+1, P.V of it-1) are then
+  // pb.  The MFMAs of a step (scores of it+1, P.V of it-1) are then
   // independent of the step's exponentials, which fill the issue slots
   // between them.  K(it+1) is in kt[(it+1)&1], V(it-1) in vt[(it+1)&1]; the
   // step refills kt[it&1] with K(it+2) at its start (K(it) was consumed by
   // the previous step) and vt[(it+1)&1] with V(it+1) after its P.V reads.
   // The K and V operands are streamed in halves (k-steps 0-3 / 4-7, keys
   // 0-15 / 16-31) to keep the register footprint within one wave per SIMD.
-  h8 pb[NB][2];
+  // P^T of a tile as fp16 hi parts (keys 0-15, 16-31), then the lo parts.
+  h8 pb[NB][4];
   // A single wave per SIMD issues everything in program order, so the step
   // is written in its issue order and fenced (sched_barrier) into small
   // groups: one or two MFMAs, then a slice of the exponentials, which then
@@ -700,7 +723,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     }
     fence();
     // Exponential slice j (0 .. 4 NB - 1): scores 4(j%4) .. +3 of row block j/4.
-    u4 pw[NB][2];
+    u4 pw[NB][4];  // hi parts (keys 0-15, 16-31), then lo parts
     float ls[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) ls[b] = l_run[b];
@@ -708,14 +731,17 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       const int b = j >> 2, i = 4 * (j & 3);
       const float p0 = fast_exp2(s_cur[b][i]), p1 = fast_exp2(s_cur[b][i + 1]);
       const float p2 = fast_exp2(s_cur[b][i + 2]), p3 = fast_exp2(s_cur[b][i + 3]);
-      const h2 pp0 = __builtin_convertvector((f2){p0, p1}, h2);
-      const h2 pp1 = __builtin_convertvector((f2){p2, p3}, h2);
+      unsigned h0, l0, h1, l1;
+      split_pair(p0, p1, h0, l0);
+      split_pair(p2, p3, h1, l1);
       ls[b] = ((ls[b] + p0) + p1) + (p2 + p3);
-      pw[b][i >> 3][(i & 7) >> 1] = __builtin_bit_cast(unsigned, pp0);
-      pw[b][i >> 3][((i & 7) >> 1) + 1] = __builtin_bit_cast(unsigned, pp1);
+      pw[b][i >> 3][(i & 7) >> 1] = h0;
+      pw[b][i >> 3][((i & 7) >> 1) + 1] = h1;
+      pw[b][2 + (i >> 3)][(i & 7) >> 1] = l0;
+      pw[b][2 + (i >> 3)][((i & 7) >> 1) + 1] = l1;
       // used only by the next step: pinned here so that the work is not
       // sunk to the end of the step
-      asm volatile("" ::"v"(pp0), "v"(pp1), "v"(ls[b]));
+      asm volatile("" ::"v"(h0), "v"(h1), "v"(l0), "v"(l1), "v"(ls[b]));
     };
     f16v s_next[NB];
     auto qk = [&](int st, int b) { mfma_qk(s_next[b], ka[st & 3], qb[b][st], ql[b][st]); };
@@ -758,7 +784,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     for (int db = 0; db < 4; ++db) {
       if (with_pv) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pb[b][0]);
+        for (int b = 0; b < NB; ++b) mfma_pv2(o[b][db], va[db], pb[b][0], pb[b][2]);
       }
       fence();
       if (sl < 4 * NB) exp_slice(sl);  // NB = 1 has four slices only
@@ -779,7 +805,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       for (int b = 0; b < NB; ++b) qk(st, b);
       if (with_pv) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) mfma_pv(o[b][st - 4], va[st - 4], pb[b][1]);
+        for (int b = 0; b < NB; ++b) mfma_pv2(o[b][st - 4], va[st - 4], pb[b][1], pb[b][3]);
       }
       fence();
     }
@@ -787,8 +813,8 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       l_run[b] = ls[b];
-      pb[b][0] = __builtin_bit_cast(h8, pw[b][0]);
-      pb[b][1] = __builtin_bit_cast(h8, pw[b][1]);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) pb[b][h] = __builtin_bit_cast(h8, pw[b][h]);
     }
     if (it + 1 < g_count) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // V(it-1) reads done
@@ -811,7 +837,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pb[b][0]);
+      for (int b = 0; b < NB; ++b) mfma_pv2(o[b][db], va[db], pb[b][0], pb[b][2]);
     va[0] = read_va<1, 0>(vab);
     va[1] = read_va<1, 1>(vab);
     va[2] = read_va<1, 2>(vab);
@@ -819,20 +845,21 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pb[b][1]);
+      for (int b = 0; b < NB; ++b) mfma_pv2(o[b][db], va[db], pb[b][1], pb[b][3]);
   };
 
-  // NB = 2 (prefill): the same step as one MFMA per slot, 34 slots, each
-  // followed by one exponential of tile it (with its fp16 packing and row-sum
-  // work every second slot), so a 16-cycle transcendental issue sits under
-  // every 32-cycle MFMA instead of the exponentials queueing behind half of
-  // them.  All K and V^T operands of the step are read from LDS at its start.
+  // NB = 2 (prefill): the same step as 34 slots of one score k-step (hi and
+  // lo q) or one P.V k-step (hi and lo P), i.e. two MFMAs, except the two
+  // reference k-steps; each slot is followed by one exponential of tile it
+  // (with its hi + lo split and row-sum work every second slot), so the
+  // transcendental issue sits under the MFMAs instead of the exponentials
+  // queueing behind half of them.
   // Scores and P live in two register sets that alternate between steps
   // (s_in -> s_out, p_in -> p_out), so nothing is copied at the step's end.
   // with_qk is false for a wave's last tile, whose step has no next tile to
   // score: its slots then hold only the exponentials and the P.V MFMAs.
   auto step2 = [&](int it, auto with_pv, auto with_qk, f16v(&s_in)[NB], f16v(&s_out)[NB],
-                   h8(&p_in)[NB][2], h8(&p_out)[NB][2]) {
+                   h8(&p_in)[NB][4], h8(&p_out)[NB][4]) {
     const unsigned kab = ka_b[(it + 1) & 1];
     const unsigned vab = va_b[(it + 1) & 1];
     // Operands in halves, each read eight slots (~256 cycles) ahead of its
@@ -853,10 +880,11 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     float ls[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) ls[b] = l_run[b];
-    u4 pw[NB][2];
+    u4 pw[NB][4];  // hi parts (keys 0-15, 16-31), then lo parts
     float ex[4];
     // Element k of exponential slice j: score e = 4 (j % 4) + k of row block
-    // j / 4; odd k packs the pair (e-1, e) into fp16 and adds it to the sum.
+    // j / 4; odd k splits the pair (e-1, e) into fp16 hi and lo parts and
+    // adds it to the sum.
     // (The results are pinned where they are formed: they are only read at
     // the step's end, and would otherwise be sunk there, behind the MFMAs.)
     auto E = [&](int j, int k) {
@@ -864,9 +892,11 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       ex[k] = fast_exp2(s_in[b][e]);
       ls[b] += ex[k];
       if (k & 1) {
-        const h2 pp = __builtin_convertvector((f2){ex[k - 1], ex[k]}, h2);
-        pw[b][e >> 3][((e - 1) & 7) >> 1] = __builtin_bit_cast(unsigned, pp);
-        asm volatile("" ::"v"(pp), "v"(ls[b]));
+        unsigned hi, lo;
+        split_pair(ex[k - 1], ex[k], hi, lo);
+        pw[b][e >> 3][((e - 1) & 7) >> 1] = hi;
+        pw[b][2 + (e >> 3)][((e - 1) & 7) >> 1] = lo;
+        asm volatile("" ::"v"(hi), "v"(lo), "v"(ls[b]));
       } else {
         asm volatile("" ::"v"(ex[k]), "v"(ls[b]));
       }
@@ -882,10 +912,10 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       if (with_qk) mfma_qk(s_out[b], ka[st], qb[b][st], ql[b][st]);
     };
     auto PVL = [&](int db, int b) {
-      if (with_pv) mfma_pv(o[b][db], vlo[db], p_in[b][0]);
+      if (with_pv) mfma_pv2(o[b][db], vlo[db], p_in[b][0], p_in[b][2]);
     };
     auto PVH = [&](int db, int b) {
-      if (with_pv) mfma_pv(o[b][db], vhi[db], p_in[b][1]);
+      if (with_pv) mfma_pv2(o[b][db], vhi[db], p_in[b][1], p_in[b][3]);
     };
     // slots 1-10: reference k-steps and k-steps 0-3; exponential slices 0-2
     REF(0); fence(); E(0, 0); fence();
@@ -928,6 +958,8 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
     keep(vlo[3]);
     keep(p_in[0][0]);
     keep(p_in[1][0]);
+    keep(p_in[0][2]);
+    keep(p_in[1][2]);
     fence();
     if (with_pv) {
       vhi[0] = read_va<1, 0>(vab);
@@ -971,8 +1003,8 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       l_run[b] = ls[b];
-      p_out[b][0] = __builtin_bit_cast(h8, pw[b][0]);
-      p_out[b][1] = __builtin_bit_cast(h8, pw[b][1]);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) p_out[b][h] = __builtin_bit_cast(h8, pw[b][h]);
     }
     // Window mask of tile it+1, only where it crosses a window edge.
     if (with_qk) {
@@ -984,7 +1016,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
   // The MFMAs are inline assembly, invisible to the compiler's hazard
   // checks: the leading wait states keep them from reading P registers the
   // step just wrote.
-  auto last_pv_of = [&](h8(&pl)[NB][2]) {
+  auto last_pv_of = [&](h8(&pl)[NB][4]) {
     asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
     const unsigned vab = va_b[(g_count - 1) & 1];
     h8 va[4];
@@ -995,7 +1027,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pl[b][0]);
+      for (int b = 0; b < NB; ++b) mfma_pv2(o[b][db], va[db], pl[b][0], pl[b][2]);
     va[0] = read_va<1, 0>(vab);
     va[1] = read_va<1, 1>(vab);
     va[2] = read_va<1, 2>(vab);
@@ -1003,7 +1035,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int b = 0; b < NB; ++b) mfma_pv(o[b][db], va[db], pl[b][1]);
+      for (int b = 0; b < NB; ++b) mfma_pv2(o[b][db], va[db], pl[b][1], pl[b][3]);
     pv_drain_all(o);
   };
 
@@ -1060,7 +1092,7 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
       using T = std::true_type;
       using F = std::false_type;
       f16v s_alt[NB];
-      h8 p_a[NB][2], p_b[NB][2];
+      h8 p_a[NB][4], p_b[NB][4];
       if (g_count > 0) {
         wait_vmcnt<8>();
         step2(0, F{}, T{}, s_cur, s_alt, p_a, p_b);  // P(0) -> p_b
@@ -1079,8 +1111,8 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {  // into the registers the last step reads
           s_alt[b] = s_cur[b];
-          p_b[b][0] = p_a[b][0];
-          p_b[b][1] = p_a[b][1];
+#pragma unroll
+          for (int h = 0; h < 4; ++h) p_b[b][h] = p_a[b][h];
         }
       }
       if (it < g_count) {  // it = g_count - 1: the last step
@@ -1088,8 +1120,8 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
         step2(it, T{}, F{}, s_alt, s_cur, p_b, p_a);
 #pragma unroll
         for (int b = 0; b < NB; ++b) {  // P of the last tile where last_pv_of reads it
-          p_b[b][0] = p_a[b][0];
-          p_b[b][1] = p_a[b][1];
+#pragma unroll
+          for (int h = 0; h < 4; ++h) p_b[b][h] = p_a[b][h];
         }
       }
       if (g_count > 0) {
@@ -1110,15 +1142,34 @@ __global__ void __launch_bounds__(256) flash_kernel(FlashParams p) {
         last_pv();
       }
     }
-    // Row sums: a possible fp16 overflow of some P (sum >= 65504, or not
-    // finite) or underflow (< 2^-8 with keys in range) means the reference did
-    // not suit the row.
-    bool bad = false;
+    // Row sums: an underflow (< 2^-8 with keys in range, or not finite) means
+    // the reference did not suit the row; so does an fp16 overflow of some P,
+    // possible only where the sum reaches 65504 and then visible as a
+    // non-finite accumulator of the row.
+    bool bad = false, large = false;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const float lt = half_swap_sum(l_run[b]);
       l_run[b] = lt;
-      bad = bad || (has_keys[b] && !(lt >= 0.00390625f && lt < 65504.0f));
+      bad = bad || (has_keys[b] && !(lt >= 0.00390625f));
+      large = large || (has_keys[b] && !(lt < 65504.0f));
+    }
+    if (pass == 0 && __builtin_amdgcn_ballot_w64(large) != 0) {
+      pv_drain<NB>(o);
+      bool nonfinite = false;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        // a sum of the row's accumulators is non-finite iff one of them is
+        // (at magnitudes far below fp32's range)
+        float t = 0.f;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) t += o[b][db][i];
+        t = half_swap_sum(t);
+        nonfinite = nonfinite || (has_keys[b] && !__builtin_isfinite(t));
+      }
+      bad = bad || nonfinite;
     }
     if (pass == 1 || __builtin_amdgcn_ballot_w64(bad) == 0) break;
   }

@@ -157,3 +157,91 @@ def test_verify_causal_among_drafts_index_revealing():
         sel = ids[: t + 1]
         assert np.allclose(out[t, :, 0::2], (sel // 64).mean(), atol=2e-2), t
         assert np.allclose(out[t, :, 1::2], (sel % 64).mean(), atol=2e-2), t
+
+
+def _peaked_large_v(g, M, filled, sigma=2.0, vscale=8.0):
+    """Ring with K ~ sigma N(0,1) (scores ~ sigma^2 N(0,1) in units of
+    1/sqrt(128): a handful of keys carry each row's weight) and V ~ vscale
+    N(0,1) (|v| up to ~5 vscale)."""
+    kc = np.zeros((M, 1024), np.uint16)
+    vc = np.zeros((M, 1024), np.uint16)
+    n = min(filled, M)
+    kc[:n] = D.to_f16_bits(sigma * D.normal(g, (n, 1024)))
+    vc[:n] = D.to_f16_bits(vscale * D.normal(g, (n, 1024)))
+    return kc, vc
+
+
+def _batch_f64(Q, kc, vc, start, S):
+    """float64 causal attention of queries start..start+S-1 over an unwrapped
+    ring (slot = position), Q already rotated."""
+    n = start + S
+    Kf = D.f16_bits_to_f32(kc[:n]).astype(np.float64).reshape(n, 8, 128)
+    Vf = D.f16_bits_to_f32(vc[:n]).astype(np.float64).reshape(n, 8, 128)
+    Qh = Q.astype(np.float64).reshape(S, 32, 128)
+    future = np.arange(n)[None, :] > (start + np.arange(S))[:, None]
+    out = np.empty((S, 32, 128))
+    for h in range(32):
+        s = Qh[:, h] @ Kf[:, h // 4].T / np.sqrt(128.0)
+        s[future] = -np.inf
+        s -= s.max(axis=1, keepdims=True)
+        p = np.exp(s)
+        out[:, h] = (p / p.sum(axis=1, keepdims=True)) @ Vf[:, h // 4]
+    return out.reshape(S, 4096)
+
+
+def _check_vs_exact_and_oracle(out, exact, ref, what):
+    """The stated bar against the exact (float64) attention; against the
+    oracle, the bar plus the oracle's own distance from the exact result
+    (the reference's fp32 sums of scores near 20 natural-log units and of
+    |v| ~ 40 values err by up to ~3e-3 themselves)."""
+    D.check_close(out, exact, what=what + " vs float64")
+    slack = np.abs(np.asarray(ref, np.float64) - exact)
+    err = np.abs(np.asarray(out, np.float64) - ref)
+    assert np.all(err <= D.ATOL + slack), f"{what}: vs oracle {float((err - slack).max()):.3e}"
+
+
+@pytest.mark.parametrize("start,S", [(1536, 512), (1536, 64), (100, 9)])
+def test_attention_batch_peaked_large_v(start, S):
+    # Peaked rows over values of magnitude up to ~40: an fp16 P would err
+    # by up to 2^-11 |v| per output (2e-2 here); P carried as hi + lo keeps
+    # the output within the stated tolerance at any |v|.
+    G.say(f"attention_batch peaked rows, V ~ 8 N(0,1): start={start} S={S}")
+    g = D.rng(90 + S)
+    M = 4096
+    kc, vc = _peaked_large_v(g, M, start + S)
+    Q = (2.0 * D.normal(g, (S, 4096))).astype(np.float32)
+    out = G.attention_batch(Q, kc, vc, M, start, S)
+    ref = O.attention_batch_parallel(Q, kc, vc, 32, 8, 128, M, start, S)
+    exact = _batch_f64(Q, kc, vc, start, S)
+    assert np.abs(exact).max() > 16.0  # the case reaches the large values
+    _check_vs_exact_and_oracle(out, exact, ref, f"peaked large V start={start} S={S}")
+
+
+def test_verify_step_65536_peaked_large_v():
+    # The wrapped 65536-slot ring of the verify workload (drafts at 70000..)
+    # with peaked rows and V ~ 8 N(0,1): the key range is split over
+    # workgroups here, so the split merge is covered at large |v| too.
+    G.say("attention_step verify M=65536 start=70000 S=8, peaked rows, V ~ 8 N(0,1)")
+    g = D.rng(7)
+    M, start, S = 65536, 70000, 8
+    kc, vc = _peaked_large_v(g, M, M)
+    Q = (2.0 * D.normal(g, (S, 4096))).astype(np.float32)
+    K = (2.0 * D.normal(g, (S, 1024))).astype(np.float32)
+    V = (8.0 * D.normal(g, (S, 1024))).astype(np.float32)
+    out, kc_g, vc_g = G.attention_step(kc, vc, Q, K, V, TH, M, start, S)
+    kc_o, vc_o = kc.copy(), vc.copy()
+    ref = O.verify_steps(kc_o, vc_o, Q, K, V, start, S, TH, 32, 8, 128, M)
+    pos = np.arange(start, start + S)
+    D.check_ring(kc_g, kc_o, vc_g, vc_o, pos % M, K, pos, TH, "verify ring")
+    # exact: token t over the ring with drafts 0..t written (sequential
+    # verify), q and the drafts' keys as the oracle rotated them
+    Qr = Q.copy()
+    O.load().ora_apply_rope_batch(Qr.ctypes.data, None, start, TH.ctypes.data, 32, 8, 128, S)
+    exact = np.empty((S, 4096))
+    rk, rv = kc.copy(), vc.copy()
+    for t in range(S):
+        rk[(start + t) % M] = kc_o[(start + t) % M]
+        rv[(start + t) % M] = vc_o[(start + t) % M]
+        exact[t] = D.gqa_decode_f64(Qr[t], rk, rv, 32, 8, 128, M, start + t)
+    assert np.abs(exact).max() > 16.0
+    _check_vs_exact_and_oracle(out, exact, ref, "verify 65536 peaked large V")

@@ -88,14 +88,6 @@ def _layer(g, dim, hidden, nh, nkv):
             "rms_ffn": (1.0 + 0.1 * g.standard_normal(dim)).astype(np.float32)}
 
 
-def _scale_q4_0(Wq, f):
-    """The same Q4_0 rows with every block scale times f (a power of two: exact)."""
-    B = Wq.reshape(Wq.shape[0], -1, 18).copy()
-    d = B[:, :, 0:2].copy().view(np.float16) * np.float16(f)
-    B[:, :, 0:2] = d.view(np.uint8).reshape(B.shape[0], B.shape[1], 2)
-    return B.reshape(Wq.shape)
-
-
 def _zero_scales(Wq):
     B = Wq.reshape(Wq.shape[0], -1, 18).copy()
     B[:, :, 0:2] = 0                          # d = 0: every weight of the matrix is 0
@@ -165,17 +157,13 @@ def test_prefill_layer_attention_output(dim, hidden, nh, nkv, M, start, S):
     # ring check of test_prefill_layer_matches_oracle bounds that at one ulp,
     # and through a peaked softmax one V ulp alone moves an output by up to
     # 2e-3 once |v| >= 2, so the oracle's own ring is not the reference here.)
-    # The projections have Mistral-7B's weight scale (Q4_0 scales 1/4 of
-    # _layer's: weight std ~0.02, q/k/v elements ~1.5): the flash kernel
-    # rounds P to fp16, an output error of ~2^-12 |v| (within 1e-2 relative
-    # at any scale, within 2e-3 absolute for |v| up to ~4; at _layer's own
-    # scale v reaches ~6 and the output errs by 2.6e-3).
+    # The projections keep _layer's weight scale, so v reaches ~6: the flash
+    # kernel carries P as fp16 hi + lo, and the output meets the absolute
+    # bar at that scale (a single fp16 P erred by 2.6e-3 here).
     G.say(f"prefill: layer attention output dim={dim} M={M} start={start} S={S}")
     L = G.lib()
     g = np.random.default_rng(7 * S + start)
     W = _layer(g, dim, hidden, nh, nkv)
-    for n in ("wq", "wk", "wv"):
-        W[n] = _scale_q4_0(W[n], 0.25)
     W["wo"] = _identity_q4_0(dim)
     W["w2"] = _zero_scales(W["w2"])
     kvd = dim // nh * nkv
