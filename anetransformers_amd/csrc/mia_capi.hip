@@ -28,6 +28,10 @@ constexpr int kMaxDevices = 16;
 constexpr int kG = 4;
 constexpr int kHD = 128;
 constexpr int kMaxSeq = 1 << 22;  // ring capacity limit; in-layer offsets are 64-bit in every kernel
+// mia_attention_chunk: up to this many tokens, each finds out whether a later
+// token takes its slot by scanning them (S^2 / 2 reads); longer chunks use a
+// per-slot area instead (one more launch, linear in S).
+constexpr int kChunkScanMax = 64;
 
 struct DevCtx {
   bool ready = false;
@@ -46,6 +50,8 @@ struct DevCtx {
   size_t gemm_work_bytes = 0;
   void *split_work = nullptr;  // the Q4_0 GEMM's activations as fp16 hi and lo planes
   size_t split_work_bytes = 0;
+  int *owner = nullptr;  // long chunks of mia_attention_chunk: last token per ring slot, -1 at rest
+  int owner_slots = 0;
   // Opt-in kernel timing: an event pair around the main kernel of each call
   // (kind 0 = decode kernel, 1 = flash kernel, 2 = Q4_0 matvec kernel,
   // 3 = Q4_0 GEMM kernel, 4 = the empty kernel of mia_peak_empty).
@@ -113,6 +119,19 @@ int ensure_work(DevCtx *c, size_t bytes) {
     c->work_bytes = 0;
     HIP_TRY(hipMalloc(&c->work, bytes));
     c->work_bytes = bytes;
+  }
+  return MIA_OK;
+}
+
+int ensure_owner(DevCtx *c, int slots) {
+  if (slots > c->owner_slots) {
+    HIP_TRY(hipDeviceSynchronize());
+    if (c->owner) HIP_TRY(hipFree(c->owner));
+    c->owner = nullptr;
+    c->owner_slots = 0;
+    HIP_TRY(hipMalloc((void **)&c->owner, (size_t)slots * sizeof(int)));
+    HIP_TRY(hipMemset(c->owner, 0xFF, (size_t)slots * sizeof(int)));  // -1 everywhere
+    c->owner_slots = slots;
   }
   return MIA_OK;
 }
@@ -784,10 +803,18 @@ int mia_attention_chunk(const float *Q, const float *K, const float *V, const in
   if (int rc = current_ctx(&c)) return rc;
   hipStream_t s = pick_stream(c, stream);
   // phase 1 (mistral_model.h:935-955), then phase 2 (:961-1044) with Q
-  // rotated in the attention kernel
+  // rotated in the attention kernel.  Which token of a slot writes last: a
+  // scan of the later tokens for short chunks (the reference's are 32,
+  // mistral_model.h:902), one linear pass through a per-slot area beyond.
+  int *owner = nullptr;
+  if (S > kChunkScanMax) {
+    if (int rc = ensure_owner(c, max_seq)) return rc;
+    owner = c->owner;
+  }
   HIP_TRY(mia::launch_rope_kv_positions(K, V, theta_inv, positions, S, n_kv_heads,
                                         reinterpret_cast<_Float16 *>(k_layer),
-                                        reinterpret_cast<_Float16 *>(v_layer), max_seq, s));
+                                        reinterpret_cast<_Float16 *>(v_layer), max_seq, owner,
+                                        s));
   return positions_impl(c, Q, theta_inv, positions, k_layer, v_layer, out, n_kv_heads, max_seq, S,
                         s);
 }

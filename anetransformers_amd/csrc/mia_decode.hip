@@ -98,7 +98,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(DecodeParams p) {
     const int tok = blockIdx.y;
     pos = p.positions[tok];
     // mistral_model.h:964-967; a negative position has an empty window
-    win_L = pos < 0 ? 0 : (pos + 1 < p.max_seq ? pos + 1 : p.max_seq);
+    // (pos + 1 is not formed: it would overflow at INT_MAX)
+    win_L = pos < 0 ? 0 : (pos < p.max_seq - 1 ? pos + 1 : p.max_seq);
     win_start = pos < 0 ? 0 : (int)(((long)pos + 1 - win_L) % p.max_seq);
     const size_t rows = (size_t)p.n_kv * G;  // query heads
     q_in += (size_t)tok * rows * HD;

@@ -104,16 +104,31 @@ __global__ void __launch_bounds__(128)
   }
 }
 
+// Long chunks: the last token of each slot, found in one linear pass.
+// owner[slot] holds -1 between calls; every token claims its slot with an
+// atomic max of its index, and rope_kv_positions_kernel resets the slot
+// after reading it.
+__global__ void slot_claim_kernel(const int *positions, int S, int max_seq, int *owner) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= S) return;
+  const int pos = positions[t];
+  if (pos >= 0) atomicMax(owner + pos % max_seq, t);
+}
+
 // Phase 1 of the chunked prefill for K / V (mistral/mistral_model.h:935-955):
 // one workgroup of 128 threads per token t.  k is rotated at positions[t]
 // (angles fl32(theta_inv[i] * pos), mistral_model.h:87-105), k and v are
 // rounded to fp16 and written to slot positions[t] % max_seq -- unless a
 // later token of the chunk takes the same slot: the reference writes the
-// tokens in order, so that later token is what the slot keeps.
+// tokens in order, so that later token is what the slot keeps.  Without
+// `owner` each token looks for such a later token among positions[t+1..S)
+// (short chunks); with it, the slot_claim_kernel launch before this one has
+// left the slot's last token there: the token that finds itself writes and
+// puts -1 back (a token that reads -1 there is not the last either).
 __global__ void __launch_bounds__(128)
     rope_kv_positions_kernel(const float *K, const float *V, const float *theta_inv,
                              const int *positions, int S, int n_kv, _Float16 *kc, _Float16 *vc,
-                             int max_seq) {
+                             int max_seq, int *owner) {
   __shared__ float2 cs[HD / 2];
   __shared__ int overwritten;
   const int t = blockIdx.x;
@@ -121,11 +136,19 @@ __global__ void __launch_bounds__(128)
   const int pos = positions[t];
   if (pos < 0) return;  // no slot (the attention gives such a token a zero row)
   const int slot = pos % max_seq;
-  if (tid == 0) overwritten = 0;
-  __syncthreads();
-  for (int u = t + 1 + tid; u < S; u += blockDim.x) {
-    const int pu = positions[u];
-    if (pu >= 0 && pu % max_seq == slot) overwritten = 1;
+  if (owner != nullptr) {
+    if (tid == 0) {
+      const int last = owner[slot];
+      overwritten = last != t;
+      if (last == t) owner[slot] = -1;
+    }
+  } else {
+    if (tid == 0) overwritten = 0;
+    __syncthreads();
+    for (int u = t + 1 + tid; u < S; u += blockDim.x) {
+      const int pu = positions[u];
+      if (pu >= 0 && pu % max_seq == slot) overwritten = 1;
+    }
   }
   if (tid < HD / 2) {
     const float ang = theta_inv[tid] * (float)pos;
@@ -267,10 +290,16 @@ hipError_t launch_kv_write(_Float16 *kc, _Float16 *vc, const float *K, const flo
 
 hipError_t launch_rope_kv_positions(const float *K, const float *V, const float *theta_inv,
                                     const int *positions, int S, int n_kv, _Float16 *kc,
-                                    _Float16 *vc, int max_seq, hipStream_t s) {
+                                    _Float16 *vc, int max_seq, int *owner, hipStream_t s) {
   if (S <= 0) return hipSuccess;
+  if (owner != nullptr) {
+    hipLaunchKernelGGL(slot_claim_kernel, dim3((S + 255) / 256), dim3(256), 0, s, positions, S,
+                       max_seq, owner);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   hipLaunchKernelGGL(rope_kv_positions_kernel, dim3(S), dim3(128), 0, s, K, V, theta_inv,
-                     positions, S, n_kv, kc, vc, max_seq);
+                     positions, S, n_kv, kc, vc, max_seq, owner);
   return hipGetLastError();
 }
 

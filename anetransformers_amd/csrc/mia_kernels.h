@@ -96,9 +96,11 @@ hipError_t launch_kv_write(_Float16 *kc, _Float16 *vc, const float *K, const flo
 // token t's k rotated at positions[t] (device int32), k and v rounded to fp16
 // and written to slot positions[t] % max_seq unless a later token of the
 // chunk takes the same slot (the reference's in-order writes leave the last).
+// owner: null (each token scans the later ones, O(S^2) reads: short chunks)
+// or an int32 [max_seq] area holding -1 everywhere, left so (linear in S).
 hipError_t launch_rope_kv_positions(const float *K, const float *V, const float *theta_inv,
                                     const int *positions, int S, int n_kv, _Float16 *kc,
-                                    _Float16 *vc, int max_seq, hipStream_t s);
+                                    _Float16 *vc, int max_seq, int *owner, hipStream_t s);
 // Staged rows 0..S-1 -> ring slots (start_pos + t) % max_seq, for n_layers
 // layers ring_stride / stage_stride elements apart.
 hipError_t launch_commit(_Float16 *kc, _Float16 *vc, const _Float16 *kst, const _Float16 *vst,

@@ -27,6 +27,13 @@ CASES = [
     (48, [1000, 999, 998, 997]),                        # descending on a wrapped ring
     (65536, [70000 + 3 * i for i in range(16)]),        # strided on the wrapped 65536 ring
     (65536, [70000, 66536, 131000, 5, 65535, 131071]),  # scattered over the whole ring
+    # chunks longer than 64 tokens find each slot's last writer through the
+    # per-slot area: every slot taken 2-3 times, then (the area must be back
+    # at rest after the first) an unsorted chunk with collisions on a larger
+    # ring
+    (64, list(range(200, 330))),
+    (4096, [int(x) for x in np.random.default_rng(5).permutation(np.arange(5000, 5100))]
+     + [5003 + 4096, 5050 + 8192, 5099 - 4096]),
 ]
 
 
@@ -106,6 +113,28 @@ def test_attention_positions_negative_position_gives_zero_row():
     for t in (0, 2):
         ref = O.gqa_attention(Q[t], kc, vc, 32, 4, 128, M, int(positions[t]))
         D.check_close(out[t], ref, what=f"t={t}")
+
+
+def test_attention_positions_largest_positions():
+    # positions up to INT_MAX: the window is the whole ring (its length is
+    # formed without pos + 1), checked against the float64 brute force
+    G.say("attention_positions with positions up to INT_MAX")
+    lib = G.lib()
+    g = D.rng(823)
+    M = 1024
+    kc, vc = D.ring(g, M)
+    positions = np.array([2**31 - 1, 2**31 - 2, M - 1, M], np.int32)
+    S = len(positions)
+    Q = D.normal(g, (S, 4096))
+    dkc, dvc, dq, dp = DB.from_array(kc), DB.from_array(vc), DB.from_array(Q), DB.from_array(positions)
+    dout = DB(S * 4096 * 4)
+    check(lib.mia_attention_positions(dq.ptr, dout.ptr, dkc.ptr, dvc.ptr, dp.ptr, 32, 8, 128, M,
+                                      S, None), "attention_positions")
+    check(lib.mia_stream_sync(None), "sync")
+    out = dout.download((S, 4096), np.float32)
+    for t, p in enumerate(positions):
+        ref = D.gqa_decode_f64(Q[t], kc, vc, 32, 8, 128, M, int(p))
+        D.check_close(out[t], ref, what=f"t={t} pos={p}")
 
 
 def test_dropin_prefill_chunk_attention_two_layers():

@@ -4,7 +4,11 @@ C ABI: two calls in a row, the second with a smaller input, then a shape with
 16 kv heads.  Outputs must match to the parity bar (the two entry points share
 their kernels and, at these shapes, their chunk plan, so they are expected to
 be bit-identical), and the rings bit-exactly; the oracle checks the decode
-step itself."""
+step itself.  A call is also captured into a HIP graph in global capture
+mode, where allocating or synchronising the device is refused: the capture
+succeeds only if the entry point does neither."""
+
+import ctypes
 
 import numpy as np
 import pytest
@@ -65,3 +69,61 @@ def test_noalloc_sixteen_kv_heads():
     kc_o, vc_o = kc.copy(), vc.copy()
     ref = O.decode_step(kc_o, vc_o, q, k, v, pos, TH, n_heads, n_kv, 128, M)
     D.check_close(out_n, ref, what="noalloc 16 kv heads vs oracle")
+
+
+def _hip():
+    h = ctypes.CDLL("libamdhip64.so")
+    v = ctypes.c_void_p
+    for name, args in (("hipStreamBeginCapture", [v, ctypes.c_int]),
+                       ("hipStreamEndCapture", [v, ctypes.POINTER(v)]),
+                       ("hipGraphInstantiate", [ctypes.POINTER(v), v, v, v, ctypes.c_size_t]),
+                       ("hipGraphLaunch", [v, v]),
+                       ("hipGraphExecDestroy", [v]),
+                       ("hipGraphDestroy", [v])):
+        getattr(h, name).argtypes = args
+        getattr(h, name).restype = ctypes.c_int
+    return h
+
+
+def test_noalloc_captured_in_graph():
+    # Global capture mode: hipMalloc / hipFree / hipDeviceSynchronize from
+    # any thread during the capture make it fail.  A 32K window takes 32
+    # chunks, so the split-K partials are in use.  The graph is replayed
+    # three times with eager work and synchronisations in between, each
+    # replay checked against the eager mia_decode_step.
+    lib = G.lib()
+    hip = _hip()
+    g = D.rng(902)
+    M, pos = 32768, 40000
+    G.say(f"decode_step_noalloc captured in a HIP graph M={M} pos={pos}")
+    kc, vc = D.ring(g, M, spike_every=1024)
+    q, k, v = D.normal(g, 4096), D.normal(g, 1024), D.normal(g, 1024)
+    (_, out_r), _ = _both(lib, kc, vc, q, k, v, 32, 8, M, pos)
+    dth = DB.from_array(TH)
+    dq, dk, dv = DB.from_array(q), DB.from_array(k), DB.from_array(v)
+    dkc, dvc = DB.from_array(kc), DB.from_array(vc)
+    dout = DB(4096 * 4)
+    stream = ctypes.c_void_p()
+    check(lib.mia_stream_create(ctypes.byref(stream)), "stream")
+    graph, gexec = ctypes.c_void_p(), ctypes.c_void_p()
+    try:
+        assert hip.hipStreamBeginCapture(stream, 0) == 0  # hipStreamCaptureModeGlobal
+        rc = lib.mia_decode_step_noalloc(dq.ptr, dk.ptr, dv.ptr, dth.ptr, dkc.ptr, dvc.ptr,
+                                         dout.ptr, 32, 8, 128, M, pos, stream)
+        end = hip.hipStreamEndCapture(stream, ctypes.byref(graph))
+        assert rc == 0, lib.mia_last_error().decode()
+        assert end == 0, f"capture ended with hipError {end}"
+        assert hip.hipGraphInstantiate(ctypes.byref(gexec), graph, None, None, 0) == 0
+        for rep in range(3):
+            check(lib.mia_memset(dout.ptr, 0, 4096 * 4), "clear")
+            check(lib.mia_device_sync(), "sync")
+            assert hip.hipGraphLaunch(gexec, stream) == 0
+            check(lib.mia_stream_sync(stream), "sync")
+            got = dout.download(4096, np.float32)
+            assert np.array_equal(got, out_r), f"replay {rep}"
+    finally:
+        if gexec.value:
+            hip.hipGraphExecDestroy(gexec)
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+        lib.mia_stream_destroy(stream)
