@@ -251,12 +251,16 @@ __device__ __forceinline__ void mfma_pv2(f16v &acc, const h8 &a, const h8 &bh, c
       : "v"(a), "v"(bh), "v"(bl));
 }
 // fp32 pair -> fp16 hi pair and the fp16 pair of what the hi parts miss.
+// x - hi is formed by v_fma_mix_f32 straight from the packed fp16 hi (hi *
+// -1 + x, one rounding of an exact difference: the same value as converting
+// hi back and subtracting, in one instruction instead of two).
 __device__ __forceinline__ void split_pair(float x0, float x1, unsigned &hi, unsigned &lo) {
-  const f2 x = {x0, x1};
-  const h2 h = __builtin_convertvector(x, h2);
-  const h2 l = __builtin_convertvector(x - __builtin_convertvector(h, f2), h2);
+  const h2 h = __builtin_convertvector((f2){x0, x1}, h2);
   hi = __builtin_bit_cast(unsigned, h);
-  lo = __builtin_bit_cast(unsigned, l);
+  float r0, r1;
+  asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r0) : "v"(hi), "v"(x0));
+  asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r1) : "v"(hi), "v"(x1));
+  lo = __builtin_bit_cast(unsigned, __builtin_convertvector((f2){r0, r1}, h2));
 }
 // S^T += K . Q^T over one k-step, hi part then lo part of Q^T, both read
 // from AGPRs.  Q^T is loop-invariant (128 registers at 64 rows): held in
