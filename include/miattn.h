@@ -154,7 +154,9 @@ int mia_attention_positions(const float *Q, float *out, const uint16_t *k_layer,
  * a later token in the same slot wins), then mia_attention_positions over the
  * ring so written, with q rotated at positions[t].  Q [S][n_heads*128], K, V
  * [S][n_kv_heads*128] raw fp32 dev (not modified); theta_inv [64] dev.  The
- * caller keeps the len bookkeeping (mistral_model.h:952). */
+ * caller keeps the len bookkeeping (mistral_model.h:952).  Chunks of more
+ * than 64 tokens use a per-device int32 [max_seq] area (allocated on first
+ * use) to find each slot's last token in one pass. */
 int mia_attention_chunk(const float *Q, const float *K, const float *V, const int *positions,
                         const float *theta_inv, uint16_t *k_layer, uint16_t *v_layer, float *out,
                         int n_heads, int n_kv_heads, int hd, int max_seq, int S, void *stream);
