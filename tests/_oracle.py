@@ -82,6 +82,11 @@ _SIGS = {
         [_P, POINTER(OraKV), _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P,
          c_int],
     ),
+    "ora_typed_row_bytes": (ctypes.c_long, [c_int, c_int]),
+    "ora_dequant_typed_rows": (c_int, [_P, c_int, _P, c_int, c_int]),
+    "ora_typed_matvec": (c_int, [_P, c_int, _P, _P, c_int, c_int]),
+    "ora_typed_matvec_q8": (c_int, [_P, c_int, _P, _P, c_int, c_int]),
+    "ora_typed_gemm": (c_int, [_P, c_int, c_int, c_int, _P, c_int, _P, c_int]),
 }
 
 
@@ -369,3 +374,78 @@ def prefill_layer(W, X, kc, vc, start_pos, S, dim, hidden, n_heads, n_kv, th, ep
                              hidden, n_heads, n_kv, eps, _p(np.ascontiguousarray(th, np.float32)),
                              threads)
     return Xo
+
+
+# ---- weight types other than Q4_0 (oracle/kquant_oracle.c) -----------------
+
+TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 2, 12, 14
+
+
+def typed_row_bytes(t: int, cols: int) -> int:
+    return int(load().ora_typed_row_bytes(t, cols))
+
+
+def make_q4_k(g: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    """Random Q4_K rows: small positive fp16 d / dmin, random 6-bit scales and
+    mins (all 12 bytes random), random nibbles."""
+    nb = cols // 256
+    B = np.empty((rows, nb, 144), np.uint8)
+    d = (np.abs(g.standard_normal((rows, nb))) * 0.002 + 1e-4).astype(np.float16)
+    dm = (np.abs(g.standard_normal((rows, nb))) * 0.002 + 1e-4).astype(np.float16)
+    B[:, :, 0:2] = d.view(np.uint8).reshape(rows, nb, 2)
+    B[:, :, 2:4] = dm.view(np.uint8).reshape(rows, nb, 2)
+    B[:, :, 4:] = g.integers(0, 256, (rows, nb, 140), dtype=np.uint8)
+    return B.reshape(rows, nb * 144)
+
+
+def make_q6_k(g: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    """Random Q6_K rows: random ql / qh bits, int8 scales, small fp16 d."""
+    nb = cols // 256
+    B = np.empty((rows, nb, 210), np.uint8)
+    B[:, :, :208] = g.integers(0, 256, (rows, nb, 208), dtype=np.uint8)
+    d = (np.abs(g.standard_normal((rows, nb))) * 0.0005 + 1e-5).astype(np.float16)
+    B[:, :, 208:210] = d.view(np.uint8).reshape(rows, nb, 2)
+    return B.reshape(rows, nb * 210)
+
+
+def make_typed(g: np.random.Generator, t: int, rows: int, cols: int) -> np.ndarray:
+    if t == TYPE_Q4_K:
+        return make_q4_k(g, rows, cols)
+    if t == TYPE_Q6_K:
+        return make_q6_k(g, rows, cols)
+    if t == TYPE_Q4_0:
+        return make_q4_0(g, rows, cols)
+    w = (g.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    if t == TYPE_F16:
+        return w.astype(np.float16).view(np.uint8).reshape(rows, cols * 2)
+    return w.view(np.uint8).reshape(rows, cols * 4)
+
+
+def dequant_typed(W, t: int, rows: int, cols: int) -> np.ndarray:
+    out = np.empty((rows, cols), np.float32)
+    assert load().ora_dequant_typed_rows(_p(np.ascontiguousarray(W, np.uint8)), t, _p(out), rows,
+                                         cols) == 0
+    return out
+
+
+def typed_matvec(W, t: int, x, out_dim: int, in_dim: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(out_dim, np.float32)
+    assert load().ora_typed_matvec(_p(np.ascontiguousarray(W, np.uint8)), t, _p(x), _p(y),
+                                   out_dim, in_dim) == 0
+    return y
+
+
+def typed_matvec_q8(W, t: int, xq, out_dim: int, in_dim: int) -> np.ndarray:
+    y = np.empty(out_dim, np.float32)
+    assert load().ora_typed_matvec_q8(_p(np.ascontiguousarray(W, np.uint8)), t, xq.ctypes.data,
+                                      _p(y), out_dim, in_dim) == 0
+    return y
+
+
+def typed_gemm(W, t: int, out_dim: int, in_dim: int, X, threads: int = 0) -> np.ndarray:
+    X = np.ascontiguousarray(X, np.float32)
+    Y = np.empty((X.shape[0], out_dim), np.float32)
+    assert load().ora_typed_gemm(_p(np.ascontiguousarray(W, np.uint8)), t, out_dim, in_dim, _p(X),
+                                 X.shape[0], _p(Y), threads) == 0
+    return Y
