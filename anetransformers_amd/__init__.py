@@ -86,6 +86,17 @@ class LayerWeights(ctypes.Structure):
                                          "rms_ffn")]
 
 
+class LayerWeightsTyped(ctypes.Structure):
+    """mia_layer_weights_typed (include/miattn.h): device pointers and GGML
+    type ids of one layer."""
+
+    _fields_ = ([(n, c_void_p) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3")]
+                + [(n + "_type", c_int) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3")]
+                + [("rms_att", c_void_p), ("rms_ffn", c_void_p)])
+
+
+TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 2, 12, 14
+
 _P = c_void_p
 _SIGS = {
     # runtime plumbing
@@ -169,6 +180,17 @@ _SIGS = {
     "mia_prefill_layer_packed": (
         c_int,
         [_P, POINTER(LayerWeights), _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,
+         c_int, c_int, _P],
+    ),
+    # weight types other than Q4_0
+    "mia_weight_row_bytes": (c_long, [c_int, c_int]),
+    "mia_dequant_f32": (c_int, [_P, c_int, _P, c_int, c_int, _P]),
+    "mia_matvec_f32": (c_int, [_P, c_int, _P, _P, c_int, c_int, _P]),
+    "mia_matvec_q8": (c_int, [_P, c_int, _P, _P, c_int, c_int, _P]),
+    "mia_gemm_f32": (c_int, [_P, c_int, _P, _P, c_int, c_int, c_int, _P]),
+    "mia_prefill_layer_typed": (
+        c_int,
+        [_P, POINTER(LayerWeightsTyped), _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,
          c_int, c_int, _P],
     ),
     # GGUF weight files (include/mia_gguf.h); the config struct is MistralConfig's layout

@@ -2,6 +2,7 @@
 // Host code only: validation, per-device context (stream, split-K scratch,
 // work buffers) and launch planning.
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
 
 #include <climits>
 #include <cstdarg>
@@ -52,12 +53,18 @@ struct DevCtx {
   size_t split_work_bytes = 0;
   int *owner = nullptr;  // long chunks of mia_attention_chunk: last token per ring slot, -1 at rest
   int owner_slots = 0;
+  // Weight types other than Q4_0 in the GEMM: the dequantised fp32 matrix,
+  // multiplied by rocBLAS sgemm (handle created on first use).
+  float *wbuf = nullptr;
+  size_t wbuf_bytes = 0;
+  rocblas_handle blas = nullptr;
   // Opt-in kernel timing: an event pair around the main kernel of each call
   // (kind 0 = decode kernel, 1 = flash kernel, 2 = Q4_0 matvec kernel,
-  // 3 = Q4_0 GEMM kernel, 4 = the empty kernel of mia_peak_empty).
+  // 3 = Q4_0 GEMM kernel, 4 = the empty kernel of mia_peak_empty, 5 = the
+  // matvec kernel of the other weight types).
   bool prof_on = false;
-  std::vector<hipEvent_t> prof_ev[5];
-  size_t prof_n[5] = {0, 0, 0, 0, 0};
+  std::vector<hipEvent_t> prof_ev[6];
+  size_t prof_n[6] = {0, 0, 0, 0, 0, 0};
 };
 
 DevCtx g_ctx[kMaxDevices];
@@ -168,6 +175,29 @@ int ensure_gemm_work(DevCtx *c, size_t bytes) {
     c->gemm_work_bytes = 0;
     HIP_TRY(hipMalloc(&c->gemm_work, bytes));
     c->gemm_work_bytes = bytes;
+  }
+  return MIA_OK;
+}
+
+int ensure_wbuf(DevCtx *c, size_t bytes) {
+  if (bytes > c->wbuf_bytes) {
+    HIP_TRY(hipDeviceSynchronize());
+    if (c->wbuf) HIP_TRY(hipFree(c->wbuf));
+    c->wbuf = nullptr;
+    c->wbuf_bytes = 0;
+    HIP_TRY(hipMalloc((void **)&c->wbuf, bytes));
+    c->wbuf_bytes = bytes;
+  }
+  return MIA_OK;
+}
+
+int ensure_blas(DevCtx *c) {
+  if (c->blas == nullptr) {
+    rocblas_handle h = nullptr;
+    const rocblas_status st = rocblas_create_handle(&h);
+    if (st != rocblas_status_success)
+      return set_err(MIA_ERR_HIP, "rocblas_create_handle: %s", rocblas_status_to_string(st));
+    c->blas = h;
   }
   return MIA_OK;
 }
@@ -527,7 +557,7 @@ int mia_profile_begin(void) {
 }
 
 int mia_profile_end(int kind, int *count, double *total_ms) {
-  if (kind < 0 || kind > 4 || !count || !total_ms) return set_err(MIA_ERR_INVALID, "bad profile query");
+  if (kind < 0 || kind > 5 || !count || !total_ms) return set_err(MIA_ERR_INVALID, "bad profile query");
   DevCtx *c;
   if (int rc = current_ctx(&c)) return rc;
   c->prof_on = false;
@@ -1056,6 +1086,175 @@ int mia_prefill_layer_packed(float *X, const mia_layer_weights *lw, const float 
                              int S, void *stream) {
   return prefill_layer_impl(X, lw, theta_inv, k_layer, v_layer, dim, hidden, n_heads, n_kv_heads,
                             eps, max_seq, start_pos, S, stream, true);
+}
+
+// ---- weight types other than Q4_0 ------------------------------------------
+
+static int check_typed(int type, int in_dim, const void *W) {
+  if (mia::typed_row_bytes(type, in_dim) == 0)
+    return set_err(MIA_ERR_UNSUPPORTED,
+                   "weight type %d with in_dim %d: types 0, 1, 2, 12, 14 with in_dim a multiple "
+                   "of 32 (of 256 for 12 and 14)",
+                   type, in_dim);
+  const uintptr_t need = (type == MIA_TYPE_Q4_0 || type == MIA_TYPE_Q6_K) ? 2 : 16;
+  if ((uintptr_t)W & (need - 1))
+    return set_err(MIA_ERR_INVALID, "W of type %d must be %d-byte aligned", type, (int)need);
+  return MIA_OK;
+}
+
+// Y [S][N] (+)= X [S][K] . W^T for a weight type other than Q4_0: the fp32
+// weights into wbuf, then sgemm.  rocBLAS is column-major: Y^T [N][S] =
+// (W^T [K][N])^T . X^T [K][S], so W is the transposed A operand with lda K.
+static int typed_gemm_impl(DevCtx *c, const void *W, int type, const float *X, float *Y, int N,
+                           int K, int S, bool add, hipStream_t s) {
+  if (type == MIA_TYPE_Q4_0)
+    return gemm_impl(c, W, nullptr, nullptr, N, 0, 0, X, K, S, Y, nullptr, nullptr,
+                     add ? mia::kGemmAdd : mia::kGemmStore, s);
+  if (int rc = ensure_wbuf(c, (size_t)N * K * sizeof(float))) return rc;
+  if (int rc = ensure_blas(c)) return rc;
+  HIP_TRY(mia::launch_typed_dequant(W, type, c->wbuf, N, K, s));
+  const float one = 1.0f, beta = add ? 1.0f : 0.0f;
+  rocblas_status st = rocblas_set_stream(c->blas, s);
+  if (st == rocblas_status_success)
+    st = rocblas_sgemm(c->blas, rocblas_operation_transpose, rocblas_operation_none, N, S, K, &one,
+                       c->wbuf, K, X, K, &beta, Y, N);
+  if (st != rocblas_status_success)
+    return set_err(MIA_ERR_HIP, "rocblas_sgemm: %s", rocblas_status_to_string(st));
+  return MIA_OK;
+}
+
+long mia_weight_row_bytes(int type, int in_dim) { return mia::typed_row_bytes(type, in_dim); }
+
+int mia_dequant_f32(const void *W, int type, float *out, int rows, int cols, void *stream) {
+  if (!W || !out) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (rows <= 0 || cols <= 0) return set_err(MIA_ERR_INVALID, "bad sizes (rows=%d cols=%d)", rows, cols);
+  if (int rc = check_typed(type, cols, W)) return rc;
+  if ((uintptr_t)out & 15) return set_err(MIA_ERR_INVALID, "out must be 16-byte aligned");
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  HIP_TRY(mia::launch_typed_dequant(W, type, out, rows, cols, pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+static int typed_matvec_impl(const void *W, int type, const void *x, bool xq8, float *y,
+                             int out_dim, int in_dim, void *stream) {
+  if (!W || !x || !y) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (out_dim <= 0 || in_dim <= 0)
+    return set_err(MIA_ERR_INVALID, "bad sizes (out_dim=%d in_dim=%d)", out_dim, in_dim);
+  if (int rc = check_typed(type, in_dim, W)) return rc;
+  if ((uintptr_t)x & (xq8 ? 3 : 15))
+    return set_err(MIA_ERR_INVALID, "x must be %d-byte aligned", xq8 ? 4 : 16);
+  if ((uintptr_t)y & 3) return set_err(MIA_ERR_INVALID, "y must be 4-byte aligned");
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  hipEvent_t ev0, ev1;
+  if (int rc = prof_pair(c, 5, &ev0, &ev1)) return rc;
+  HIP_TRY(mia::launch_typed_matvec(W, type, x, xq8, y, out_dim, in_dim, pick_stream(c, stream),
+                                   ev0, ev1));
+  return MIA_OK;
+}
+
+int mia_matvec_f32(const void *W, int type, const float *x, float *y, int out_dim, int in_dim,
+                   void *stream) {
+  return typed_matvec_impl(W, type, x, false, y, out_dim, in_dim, stream);
+}
+
+int mia_matvec_q8(const void *W, int type, const void *x_q8, float *y, int out_dim, int in_dim,
+                  void *stream) {
+  if (type == MIA_TYPE_Q4_0) return mia_q4_0_matvec(W, x_q8, y, out_dim, in_dim, stream);
+  return typed_matvec_impl(W, type, x_q8, true, y, out_dim, in_dim, stream);
+}
+
+int mia_gemm_f32(const void *W, int type, const float *X, float *Y, int out_dim, int in_dim,
+                 int S, void *stream) {
+  if (type == MIA_TYPE_Q4_0) return mia_q4_0_gemm_f32(W, X, Y, out_dim, in_dim, S, stream);
+  if (!W || !X || !Y) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (out_dim <= 0 || in_dim <= 0 || S <= 0)
+    return set_err(MIA_ERR_INVALID, "bad sizes (out_dim=%d in_dim=%d S=%d)", out_dim, in_dim, S);
+  if (int rc = check_typed(type, in_dim, W)) return rc;
+  if ((long)S * in_dim > INT_MAX || (long)S * out_dim > INT_MAX)
+    return set_err(MIA_ERR_UNSUPPORTED, "S x dim above 2^31");
+  if (int rc = check_align16(X, Y, nullptr, nullptr)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  return typed_gemm_impl(c, W, type, X, Y, out_dim, in_dim, S, false, pick_stream(c, stream));
+}
+
+int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const float *theta_inv,
+                            uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden,
+                            int n_heads, int n_kv_heads, float eps, int max_seq, int start_pos,
+                            int S, void *stream) {
+  if (!lw) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  const int types[7] = {lw->wq_type, lw->wk_type, lw->wv_type, lw->wo_type,
+                        lw->w1_type, lw->w2_type, lw->w3_type};
+  bool all_q4_0 = true;
+  for (int t : types) all_q4_0 = all_q4_0 && t == MIA_TYPE_Q4_0;
+  if (all_q4_0) {
+    const mia_layer_weights q{lw->wq, lw->wk, lw->wv, lw->wo, lw->w1,
+                              lw->w2, lw->w3, lw->rms_att, lw->rms_ffn};
+    return prefill_layer_impl(X, &q, theta_inv, k_layer, v_layer, dim, hidden, n_heads,
+                              n_kv_heads, eps, max_seq, start_pos, S, stream, false);
+  }
+  if (!X || !theta_inv || !k_layer || !v_layer) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (!lw->wq || !lw->wk || !lw->wv || !lw->wo || !lw->w1 || !lw->w2 || !lw->w3 || !lw->rms_att ||
+      !lw->rms_ffn)
+    return set_err(MIA_ERR_INVALID, "NULL weight pointer");
+  if (n_heads <= 0 || dim != n_heads * kHD)
+    return set_err(MIA_ERR_UNSUPPORTED, "dim %d must be n_heads x 128", dim);
+  if (int rc = check_shape(n_heads, n_kv_heads, kHD, max_seq)) return rc;
+  if (int rc = check_pos(start_pos, S)) return rc;
+  const int kv_dim = n_kv_heads * kHD;
+  const void *const ws[7] = {lw->wq, lw->wk, lw->wv, lw->wo, lw->w1, lw->w2, lw->w3};
+  const int in_dims[7] = {dim, dim, dim, dim, dim, hidden, dim};
+  for (int i = 0; i < 7; ++i) {
+    if (int rc = check_typed(types[i], in_dims[i], ws[i])) return rc;
+    // Q4_0 matrices take the fp16-MFMA GEMM (4-byte aligned, in_dim a multiple of 64)
+    if (types[i] == MIA_TYPE_Q4_0) {
+      if (in_dims[i] % 64) return set_err(MIA_ERR_UNSUPPORTED, "Q4_0 GEMM needs in_dim %% 64 == 0");
+      if ((uintptr_t)ws[i] & 3) return set_err(MIA_ERR_INVALID, "Q4_0 weights must be 4-byte aligned");
+    }
+  }
+  if (hidden <= 0 || (long)S * hidden > INT_MAX || (long)S * dim > INT_MAX)
+    return set_err(MIA_ERR_UNSUPPORTED, "bad hidden %d or S x dim above 2^31", hidden);
+  if (int rc = check_align16(X, lw->rms_att, lw->rms_ffn, k_layer)) return rc;
+  if (int rc = check_align16(v_layer, nullptr, nullptr, nullptr)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  hipStream_t s = pick_stream(c, stream);
+  // XN, Q, A [S][dim] | K, V [S][kv_dim] | G, U [S][hidden], all fp32
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  const size_t bd = al((size_t)S * dim * 4), bk = al((size_t)S * kv_dim * 4),
+               bh = al((size_t)S * hidden * 4);
+  if (int rc = ensure_layer_work(c, 3 * bd + 2 * bk + 2 * bh)) return rc;
+  char *w = reinterpret_cast<char *>(c->layer_work);
+  float *XN = reinterpret_cast<float *>(w);
+  float *Q = reinterpret_cast<float *>(w + bd);
+  float *A = reinterpret_cast<float *>(w + 2 * bd);
+  float *K = reinterpret_cast<float *>(w + 3 * bd);
+  float *V = reinterpret_cast<float *>(w + 3 * bd + bk);
+  float *G = reinterpret_cast<float *>(w + 3 * bd + 2 * bk);
+  float *U = reinterpret_cast<float *>(w + 3 * bd + 2 * bk + bh);
+  // mistral_ane_prefill.h:1092-1110
+  HIP_TRY(mia::launch_rmsnorm(XN, X, lw->rms_att, dim, S, eps, s));
+  if (int rc = typed_gemm_impl(c, lw->wq, lw->wq_type, XN, Q, dim, dim, S, false, s)) return rc;
+  if (int rc = typed_gemm_impl(c, lw->wk, lw->wk_type, XN, K, kv_dim, dim, S, false, s)) return rc;
+  if (int rc = typed_gemm_impl(c, lw->wv, lw->wv_type, XN, V, kv_dim, dim, S, false, s)) return rc;
+  // apply_rope_batch, kv_write_batch, attention_batch, as mia_prefill_layer
+  if (int rc = ensure_work(c, (size_t)S * kHD * sizeof(float))) return rc;
+  float *cs = reinterpret_cast<float *>(c->work);
+  HIP_TRY(mia::launch_rope_to_ring(K, V, theta_inv, S, start_pos, n_kv_heads,
+                                   reinterpret_cast<_Float16 *>(k_layer),
+                                   reinterpret_cast<_Float16 *>(v_layer), max_seq, cs, s));
+  if (int rc = flash_impl(c, Q, cs, nullptr, nullptr, k_layer, v_layer, A, n_kv_heads, max_seq,
+                          start_pos, S, s))
+    return rc;
+  // X + A . Wo^T (vDSP_vadd after the GEMM: the sum rounded once more)
+  if (int rc = typed_gemm_impl(c, lw->wo, lw->wo_type, A, X, dim, dim, S, true, s)) return rc;
+  HIP_TRY(mia::launch_rmsnorm(XN, X, lw->rms_ffn, dim, S, eps, s));
+  if (int rc = typed_gemm_impl(c, lw->w1, lw->w1_type, XN, G, hidden, dim, S, false, s)) return rc;
+  if (int rc = typed_gemm_impl(c, lw->w3, lw->w3_type, XN, U, hidden, dim, S, false, s)) return rc;
+  HIP_TRY(mia::launch_silu_mul(G, U, (long)S * hidden, s));
+  return typed_gemm_impl(c, lw->w2, lw->w2_type, G, X, dim, hidden, S, true, s);
 }
 
 int mia_quantize_q8_0(const float *x, void *out_q8, int n, void *stream) {

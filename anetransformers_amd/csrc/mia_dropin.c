@@ -387,13 +387,28 @@ void mia_dropin_q4_matvec_sdot_parallel_fused_qkv(const void *Wq, const void *Wk
 
 void mia_dropin_q4_matvec_sdot_parallel(const void *W, uint32_t type, const mia_block_q8_0 *x_q8,
                                         float *y, int out_dim, int in_dim) {
+    const char *what = "q4_matvec_sdot_parallel";
     g_status = 0;
-    if (type != MIA_GGML_TYPE_Q4_0) {
-        fail(MIA_ERR_UNSUPPORTED, "q4_matvec_sdot_parallel (only Q4_0 weights)");
+    if (type == MIA_GGML_TYPE_Q4_0) {
+        mia_dropin_q4_matvec_sdot_parallel_fused_qkv(W, NULL, NULL, x_q8, y, NULL, NULL, out_dim,
+                                                     0, in_dim);
         return;
     }
-    mia_dropin_q4_matvec_sdot_parallel_fused_qkv(W, NULL, NULL, x_q8, y, NULL, NULL, out_dim, 0,
-                                                 in_dim);
+    /* every other type: the Q8_0 values d * q against the type's weights
+     * (mistral_model.h:656-670) */
+    if (out_dim <= 0 || in_dim <= 0 || in_dim % 32) {
+        fail(MIA_ERR_INVALID, "q4_matvec (bad sizes)");
+        return;
+    }
+    size_t xb = (size_t)(in_dim / 32) * sizeof(mia_block_q8_0);
+    size_t yb = (size_t)out_dim * sizeof(float);
+    TRY(what, dbuf(align256(xb) + align256(yb)));
+    void *dx = g_dbuf;
+    float *dy = (float *)(g_dbuf + align256(xb));
+    TRY(what, mia_memcpy_h2d(dx, x_q8, xb));
+    TRY(what, mia_matvec_q8(W, (int)type, dx, dy, out_dim, in_dim, NULL));
+    TRY(what, mia_stream_sync(NULL));
+    TRY(what, mia_memcpy_d2h(y, dy, yb));
 }
 
 void mia_dropin_verify_stage(KVCache *kv, int layer, const float *Q, const float *K, const float *V,

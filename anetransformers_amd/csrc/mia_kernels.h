@@ -184,4 +184,18 @@ hipError_t launch_rmsnorm_split(_Float16 *hi, _Float16 *lo, const float *in, con
 hipError_t launch_rmsnorm(float *out, const float *in, const float *w, int dim, int S, float eps,
                           hipStream_t s);
 
+// Weight types by GGML id (mia_kquant.hip).  Rows of `cols` weights, cols a
+// multiple of 32 (256 for Q4_K / Q6_K); W 16-byte aligned for F32 / F16 /
+// Q4_K, 2-byte for Q4_0 / Q6_K; fp32 x 16-byte aligned, Q8_0 x 4-byte.
+enum { kTypeF32 = 0, kTypeF16 = 1, kTypeQ40 = 2, kTypeQ4K = 12, kTypeQ6K = 14 };
+long typed_row_bytes(int type, int cols);  // 0: type or cols not supported
+// y [rows] = W . x with x fp32 [cols] or (x_q8) Q8_0 blocks [cols / 32].
+hipError_t launch_typed_matvec(const void *W, int type, const void *x, bool x_q8, float *y,
+                               int rows, int cols, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
+// out [rows][cols] fp32 = the weights the reference multiplies.
+hipError_t launch_typed_dequant(const void *W, int type, float *out, int rows, int cols,
+                                hipStream_t s);
+// gate [n] = gate * sigmoid(gate) * up (the SwiGLU product).
+hipError_t launch_silu_mul(float *gate, const float *up, long n, hipStream_t s);
+
 }  // namespace mia

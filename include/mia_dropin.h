@@ -143,7 +143,9 @@ void mia_dropin_verify_commit(KVCache *kv, int start_pos, int n_accepted);
  * way, mistral/metal_matvec.h:185-192, 314); x, x_q8 and y are host buffers. */
 /* mistral/dequant.h:545-612 */
 void mia_dropin_quantize_q8_0(const float *x, mia_block_q8_0 *out, int n);
-/* mistral/mistral_model.h:649-668 for type Q4_0 (other types: MIA_ERR_UNSUPPORTED) */
+/* mistral/mistral_model.h:649-670: Q4_0 on the W4A8 kernel; Q4_K, Q6_K, F16
+ * and F32 weights against the Q8_0 values (mia_matvec_q8; other types:
+ * MIA_ERR_UNSUPPORTED) */
 void mia_dropin_q4_matvec_sdot_parallel(const void *W, uint32_t type, const mia_block_q8_0 *x_q8,
                                         float *y, int out_dim, int in_dim);
 /* mistral/mistral_model.h:676-745 */

@@ -66,7 +66,9 @@ int mia_event_elapsed_ms(float *ms, void *start, void *stop);
  * mia_gqa_attention / mia_decode_step / mia_attention_step with S=1; kind 1:
  * the S>1 flash kernel; kind 2: the Q4_0 matvec kernel of mia_q4_0_matvec /
  * mia_q4_0_matvec_qkv; kind 3: the Q4_0 GEMM kernel of mia_q4_0_gemm_f32 /
- * mia_prefill_layer; kind 4: the empty kernel of mia_peak_empty, mia_peaks.h);
+ * mia_prefill_layer; kind 4: the empty kernel of mia_peak_empty, mia_peaks.h;
+ * kind 5: the matvec kernel of mia_matvec_f32 / mia_matvec_q8 for types
+ * other than Q4_0);
  * merge, quantize, RMSNorm and RoPE kernels are not timed.
  * mia_profile_end stops recording, synchronises and returns the number of
  * timed launches of that kind and their summed duration. */
@@ -303,6 +305,77 @@ int mia_prefill_layer_packed(float *X, const mia_layer_weights *lw, const float 
                              uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden,
                              int n_heads, int n_kv_heads, float eps, int max_seq, int start_pos,
                              int S, void *stream);
+
+/* ---- weight types: Q4_K, Q6_K, F16, F32 beside Q4_0 ----------------------- */
+/* GGML type ids (mistral/gguf_loader.h:32-38).  Q4_K = 144 bytes per 256
+ * weights (fp16 d, fp16 dmin, 12 bytes of 6-bit sub-block scales and mins,
+ * 128 bytes of nibbles; mistral/dequant.h:23-29); Q6_K = 210 bytes per 256
+ * weights (ql[128], qh[64], int8 scales[16], fp16 d; dequant.h:283-289).  A
+ * matrix [out_dim][in_dim] is out_dim rows of in_dim / 32 (Q4_0) or in_dim /
+ * 256 (Q4_K, Q6_K) blocks, or of in_dim values, as GGUF stores it.  in_dim
+ * must be a multiple of 32 (256 for the K-quants); W is device memory,
+ * 16-byte aligned for F32 / F16 / Q4_K, 2-byte aligned for Q4_0 / Q6_K. */
+enum {
+    MIA_TYPE_F32 = 0,
+    MIA_TYPE_F16 = 1,
+    MIA_TYPE_Q4_0 = 2,
+    MIA_TYPE_Q4_K = 12,
+    MIA_TYPE_Q6_K = 14
+};
+
+/* Bytes of one row of in_dim weights of the type; 0 for a type or in_dim
+ * the library does not take (q_row_bytes, mistral/mistral_ane_prefill.h:
+ * 1008-1015). */
+long mia_weight_row_bytes(int type, int in_dim);
+
+/* out [rows][cols] fp32 dev (16-byte aligned) = the weights the reference
+ * multiplies, bit for bit (dequant_weight_to_fp32_buf, mistral/
+ * mistral_ane_prefill.h:907-1000): Q4_K through the fp16 arithmetic of
+ * dequant_q4_K_block_neon (dequant.h:68-125), Q6_K as dequant_q6_K_block
+ * (dequant.h:291-307), Q4_0 as d * (q - 8) in fp32. */
+int mia_dequant_f32(const void *W, int type, float *out, int rows, int cols, void *stream);
+
+/* y [out_dim] = W . x with fp32 x (dev, 16-byte aligned): q4_matvec /
+ * q4_matvec_parallel (mistral/mistral_model.h:211-243, 581-644) for every
+ * type.  The weights are those of mia_dequant_f32, multiplied and summed in
+ * fp32 (the reference's sgemv / NEON lane sums, in another order). */
+int mia_matvec_f32(const void *W, int type, const float *x, float *y, int out_dim, int in_dim,
+                   void *stream);
+
+/* q4_matvec_sdot_parallel for every type (mistral/mistral_model.h:649-670):
+ * Q4_0 is mia_q4_0_matvec (in_dim a multiple of 64); the other types take
+ * x as the Q8_0 blocks' values d * q in fp32, as the reference does, and
+ * multiply as mia_matvec_f32. */
+int mia_matvec_q8(const void *W, int type, const void *x_q8, float *y, int out_dim, int in_dim,
+                  void *stream);
+
+/* tiled_q4_gemm for every type (mistral/mistral_ane_prefill.h:1018-1042):
+ * Y[S][out_dim] = X[S][in_dim] . W^T, fp32 X and Y (dev, 16-byte aligned).
+ * Q4_0 is mia_q4_0_gemm_f32.  The other types are dequantised into a
+ * per-device fp32 area of out_dim * in_dim * 4 bytes and multiplied by
+ * rocBLAS sgemm in fp32, as the reference hands them to cblas_sgemm. */
+int mia_gemm_f32(const void *W, int type, const float *X, float *Y, int out_dim, int in_dim,
+                 int S, void *stream);
+
+/* One layer's weights with their types (LayerWeights, mistral/
+ * mistral_model.h:16-28). */
+typedef struct {
+    const void *wq, *wk, *wv, *wo, *w1, *w2, *w3;
+    int wq_type, wk_type, wv_type, wo_type, w1_type, w2_type, w3_type;
+    const float *rms_att, *rms_ffn;
+} mia_layer_weights_typed;
+
+/* blas_prefill_layer (mistral/mistral_ane_prefill.h:1081-1110) with each
+ * matrix of its own type, as mia_prefill_layer otherwise (same arguments,
+ * attention step and ring semantics).  A layer whose seven matrices are all
+ * Q4_0 is mia_prefill_layer; any other mix multiplies every matrix as
+ * mia_gemm_f32, with the activations in fp32 and the SwiGLU product
+ * gate * (1 / (1 + exp(-gate))) * up (silu_mul_neon, mistral_model.h:
+ * 174-199) in between. */
+int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const float *theta_inv,
+                            uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden,
+                            int n_heads, int n_kv_heads, float eps, int max_seq, int start_pos,
+                            int S, void *stream);
 
 #ifdef __cplusplus
 }

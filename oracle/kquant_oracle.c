@@ -13,9 +13,10 @@
 #include "kquant_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
-#include "miattn_oracle.h"
+#include "prefill_oracle.h"
 #ifdef _OPENMP
 #include <omp.h>
 #endif
@@ -156,13 +157,22 @@ int ora_dequant_typed_rows(const void *W, int type, float *dst, int rows, int co
 }
 
 int ora_typed_matvec(const void *W, int type, const float *x, float *y, int out_dim, int in_dim) {
-    if (type == ORA_TYPE_Q4_0) return -1;
     const long rb = ora_typed_row_bytes(type, in_dim);
     if (rb == 0) return -1;
     float tmp[QK_K];
     for (int r = 0; r < out_dim; r++) {
         const uint8_t *row = (const uint8_t *)W + (size_t)r * rb;
-        if (type == ORA_TYPE_Q6_K) {
+        if (type == ORA_TYPE_Q4_0) {
+            /* q4_0_matvec_f32 (dequant.h:142-278): w = (q - 8) * d in fp32,
+             * lane l of four accumulating values 4k + l with fma; vaddvq */
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int b = 0; b < in_dim / 32; b++) {
+                ora_dequant_typed_rows(row + 18 * b, ORA_TYPE_Q4_0, tmp, 1, 32);
+                for (int i = 0; i < 32; i++)
+                    acc[i & 3] = fmaf(tmp[i], x[32 * b + i], acc[i & 3]);
+            }
+            y[r] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        } else if (type == ORA_TYPE_Q6_K) {
             /* dequant.h:365-521: lane l accumulates values 4k + l of the row
              * with fma, sub-block after sub-block; then vaddvq */
             float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -225,5 +235,41 @@ int ora_typed_gemm(const void *W, int type, int out_dim, int in_dim, const float
             Y[(size_t)t * out_dim + n] = sum;
         }
     }
+    return bad ? -1 : 0;
+}
+
+int ora_prefill_layer_typed(const OraLayerWeightsTyped *lw, OraKV *kv, float *X, int layer,
+                            int start_pos, int S, int dim, int hidden, int n_heads,
+                            int n_kv_heads, float eps, const float *theta_inv, int threads) {
+    const int hd = dim / n_heads;
+    const int kv_dim = n_kv_heads * hd;
+    const size_t sd = (size_t)S * dim, sk = (size_t)S * kv_dim, sh = (size_t)S * hidden;
+    float *Xn = (float *)malloc(sd * sizeof(float));
+    float *Q = (float *)malloc(sd * sizeof(float));
+    float *K = (float *)malloc(sk * sizeof(float));
+    float *V = (float *)malloc(sk * sizeof(float));
+    float *A = (float *)malloc(sd * sizeof(float));
+    float *G = (float *)malloc(sh * sizeof(float));
+    float *U = (float *)malloc(sh * sizeof(float));
+    float *att = (float *)malloc((size_t)n_heads * kv->max_seq * sizeof(float));
+    if (!Xn || !Q || !K || !V || !A || !G || !U || !att) abort();
+    int bad = 0;
+    /* mistral_ane_prefill.h:1092-1110 */
+    ora_rmsnorm_batch(Xn, X, lw->rms_att, dim, S, eps);
+    bad |= ora_typed_gemm(lw->wq, lw->wq_type, dim, dim, Xn, S, Q, threads);
+    bad |= ora_typed_gemm(lw->wk, lw->wk_type, kv_dim, dim, Xn, S, K, threads);
+    bad |= ora_typed_gemm(lw->wv, lw->wv_type, kv_dim, dim, Xn, S, V, threads);
+    ora_apply_rope_batch(Q, K, start_pos, theta_inv, n_heads, n_kv_heads, hd, S);
+    ora_kv_write_batch(kv, layer, start_pos, K, V, kv_dim, S);
+    ora_attention_batch(Q, A, kv, layer, start_pos, n_heads, n_kv_heads, hd, S, att);
+    bad |= ora_typed_gemm(lw->wo, lw->wo_type, dim, dim, A, S, Xn, threads);
+    for (size_t i = 0; i < sd; i++) X[i] = X[i] + Xn[i];
+    ora_rmsnorm_batch(Xn, X, lw->rms_ffn, dim, S, eps);
+    bad |= ora_typed_gemm(lw->w1, lw->w1_type, hidden, dim, Xn, S, G, threads);
+    bad |= ora_typed_gemm(lw->w3, lw->w3_type, hidden, dim, Xn, S, U, threads);
+    ora_silu_mul(G, U, (int)sh);
+    bad |= ora_typed_gemm(lw->w2, lw->w2_type, dim, hidden, G, S, Xn, threads);
+    for (size_t i = 0; i < sd; i++) X[i] = X[i] + Xn[i];
+    free(Xn); free(Q); free(K); free(V); free(A); free(G); free(U); free(att);
     return bad ? -1 : 0;
 }

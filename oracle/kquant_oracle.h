@@ -26,13 +26,18 @@
  *                           unpinned at the ulp level); Q6_K follows the
  *                           reference's four-lane fma order        pinned
  *   ora_typed_matvec_q8     == ora_typed_matvec on the Q8_0 values  pinned
- *   ora_typed_gemm          float64 matmul of the dequantised rows  pinned
+ *   ora_typed_gemm          float64 matmul of the dequantised rows; the
+ *                           Q4_0 branch equals prefill_oracle's GEMM  pinned
+ *   ora_prefill_layer_typed all-Q4_0 weights reproduce ora_prefill_layer
+ *                           bit for bit; its other steps are that
+ *                           function's (prefill_oracle.h)            pinned
  */
 #ifndef KQUANT_ORACLE_H
 #define KQUANT_ORACLE_H
 
 #include <stdint.h>
 
+#include "miattn_oracle.h"
 #include "q4_oracle.h"
 
 #ifdef __cplusplus
@@ -57,8 +62,9 @@ int ora_dequant_typed_rows(const void *W, int type, float *dst, int rows, int co
 /* y = W . x, the reference's fp32-activation matvec for the type
  * (q4_matvec / q4_matvec_parallel, mistral_model.h:211-243, 581-644):
  * Q4_K, F16, F32 as dequantised rows dotted in k order (sgemv), Q6_K in the
- * four-lane fma order of q6_K_matvec_f32_neon (dequant.h:365-521).  Q4_0
- * is not taken here (the decode path quantises x for it: q4_oracle.h). */
+ * four-lane fma order of q6_K_matvec_f32_neon (dequant.h:365-521), Q4_0 in
+ * that of q4_0_matvec_f32 (dequant.h:142-278; the decode layer's W4A8 path
+ * for Q4_0 is q4_oracle.h's). */
 int ora_typed_matvec(const void *W, int type, const float *x, float *y, int out_dim, int in_dim);
 
 /* The non-Q4_0 branch of q4_matvec_sdot_parallel (mistral_model.h:656-670):
@@ -71,6 +77,19 @@ int ora_typed_matvec_q8(const void *W, int type, const OraQ8Block *xq, float *y,
  * when threads != 1. */
 int ora_typed_gemm(const void *W, int type, int out_dim, int in_dim, const float *X, int S,
                    float *Y, int threads);
+
+typedef struct {
+    const void *wq, *wk, *wv, *wo, *w1, *w2, *w3; /* [out][in] rows of their type */
+    int wq_type, wk_type, wv_type, wo_type, w1_type, w2_type, w3_type;
+    const float *rms_att, *rms_ffn;               /* [dim] */
+} OraLayerWeightsTyped;
+
+/* blas_prefill_layer (mistral/mistral_ane_prefill.h:1081-1110) with each
+ * matrix multiplied by ora_typed_gemm for its own type; otherwise the steps
+ * of ora_prefill_layer.  0 on success, -1 for a type it does not know. */
+int ora_prefill_layer_typed(const OraLayerWeightsTyped *lw, OraKV *kv, float *X, int layer,
+                            int start_pos, int S, int dim, int hidden, int n_heads,
+                            int n_kv_heads, float eps, const float *theta_inv, int threads);
 
 #ifdef __cplusplus
 }

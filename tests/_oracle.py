@@ -87,12 +87,24 @@ _SIGS = {
     "ora_typed_matvec": (c_int, [_P, c_int, _P, _P, c_int, c_int]),
     "ora_typed_matvec_q8": (c_int, [_P, c_int, _P, _P, c_int, c_int]),
     "ora_typed_gemm": (c_int, [_P, c_int, c_int, c_int, _P, c_int, _P, c_int]),
+    "ora_prefill_layer_typed": (
+        c_int,
+        [_P, POINTER(OraKV), _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P,
+         c_int],
+    ),
 }
 
 
 class OraLayerWeights(ctypes.Structure):
     _fields_ = [(n, c_void_p) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "rms_att",
                                          "rms_ffn")]
+
+
+class OraLayerWeightsTyped(ctypes.Structure):
+    _fields_ = ([(n, c_void_p) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3")]
+                + [(n + "_type", c_int) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3")]
+                + [("rms_att", c_void_p), ("rms_ffn", c_void_p)])
+
 
 _libs: dict = {}
 
@@ -385,34 +397,38 @@ def typed_row_bytes(t: int, cols: int) -> int:
     return int(load().ora_typed_row_bytes(t, cols))
 
 
-def make_q4_k(g: np.random.Generator, rows: int, cols: int) -> np.ndarray:
-    """Random Q4_K rows: small positive fp16 d / dmin, random 6-bit scales and
-    mins (all 12 bytes random), random nibbles."""
+def make_q4_k(g: np.random.Generator, rows: int, cols: int, d_scale: float = 1.0) -> np.ndarray:
+    """Random Q4_K rows: small positive fp16 d / dmin (times d_scale), random
+    6-bit scales and mins (all 12 bytes random), random nibbles."""
     nb = cols // 256
     B = np.empty((rows, nb, 144), np.uint8)
-    d = (np.abs(g.standard_normal((rows, nb))) * 0.002 + 1e-4).astype(np.float16)
-    dm = (np.abs(g.standard_normal((rows, nb))) * 0.002 + 1e-4).astype(np.float16)
+    d = ((np.abs(g.standard_normal((rows, nb))) * 0.002 + 1e-4) * d_scale).astype(np.float16)
+    dm = ((np.abs(g.standard_normal((rows, nb))) * 0.002 + 1e-4) * d_scale).astype(np.float16)
     B[:, :, 0:2] = d.view(np.uint8).reshape(rows, nb, 2)
     B[:, :, 2:4] = dm.view(np.uint8).reshape(rows, nb, 2)
     B[:, :, 4:] = g.integers(0, 256, (rows, nb, 140), dtype=np.uint8)
     return B.reshape(rows, nb * 144)
 
 
-def make_q6_k(g: np.random.Generator, rows: int, cols: int) -> np.ndarray:
-    """Random Q6_K rows: random ql / qh bits, int8 scales, small fp16 d."""
+def make_q6_k(g: np.random.Generator, rows: int, cols: int, d_scale: float = 1.0) -> np.ndarray:
+    """Random Q6_K rows: random ql / qh bits, int8 scales, small fp16 d (times
+    d_scale)."""
     nb = cols // 256
     B = np.empty((rows, nb, 210), np.uint8)
     B[:, :, :208] = g.integers(0, 256, (rows, nb, 208), dtype=np.uint8)
-    d = (np.abs(g.standard_normal((rows, nb))) * 0.0005 + 1e-5).astype(np.float16)
+    d = ((np.abs(g.standard_normal((rows, nb))) * 0.0005 + 1e-5) * d_scale).astype(np.float16)
     B[:, :, 208:210] = d.view(np.uint8).reshape(rows, nb, 2)
     return B.reshape(rows, nb * 210)
 
 
-def make_typed(g: np.random.Generator, t: int, rows: int, cols: int) -> np.ndarray:
+def make_typed(g: np.random.Generator, t: int, rows: int, cols: int,
+               d_scale: float = 1.0) -> np.ndarray:
+    """Random rows of type t; d_scale shrinks the K-quants' block scales
+    (0.07 gives weights of a few hundredths, as a model's)."""
     if t == TYPE_Q4_K:
-        return make_q4_k(g, rows, cols)
+        return make_q4_k(g, rows, cols, d_scale)
     if t == TYPE_Q6_K:
-        return make_q6_k(g, rows, cols)
+        return make_q6_k(g, rows, cols, d_scale)
     if t == TYPE_Q4_0:
         return make_q4_0(g, rows, cols)
     w = (g.standard_normal((rows, cols)) * 0.02).astype(np.float32)
@@ -449,3 +465,23 @@ def typed_gemm(W, t: int, out_dim: int, in_dim: int, X, threads: int = 0) -> np.
     assert load().ora_typed_gemm(_p(np.ascontiguousarray(W, np.uint8)), t, out_dim, in_dim, _p(X),
                                  X.shape[0], _p(Y), threads) == 0
     return Y
+
+
+MATS = ("wq", "wk", "wv", "wo", "w1", "w2", "w3")
+
+
+def prefill_layer_typed(W, types, X, kc, vc, start_pos, S, dim, hidden, n_heads, n_kv, th,
+                        eps=1e-5, threads=0):
+    """ora_prefill_layer_typed on copies: returns X'; kc/vc (one layer) updated.
+    W: dict of the seven matrices (uint8 rows of their type) and rms_att,
+    rms_ffn; types: dict of the seven GGML type ids."""
+    hd = dim // n_heads
+    kv = make_kv(kc, vc, n_kv, hd, kc.shape[0])
+    arrs = {k: np.ascontiguousarray(v) for k, v in W.items()}
+    lw = OraLayerWeightsTyped(*[_p(arrs[n]) for n in MATS], *[types[n] for n in MATS],
+                              _p(arrs["rms_att"]), _p(arrs["rms_ffn"]))
+    Xo = np.array(X, np.float32, copy=True)
+    assert load().ora_prefill_layer_typed(ctypes.byref(lw), ctypes.byref(kv), _p(Xo), 0,
+                                          start_pos, S, dim, hidden, n_heads, n_kv, eps,
+                                          _p(np.ascontiguousarray(th, np.float32)), threads) == 0
+    return Xo

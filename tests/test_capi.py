@@ -221,6 +221,51 @@ def test_prefill_argument_errors_without_device_work():
     assert b"16-byte" in lib.mia_last_error()
 
 
+def test_typed_weight_entry_points_without_device_work(tmp_path):
+    import _oracle as O
+    lib = mia.load()
+    for t in (mia.TYPE_F32, mia.TYPE_F16, mia.TYPE_Q4_0, mia.TYPE_Q4_K, mia.TYPE_Q6_K, 3, 8):
+        for n in (32, 96, 256, 4096, 14336, 100):
+            # the reference's sizes, where the library takes the shape (rows of
+            # whole 32-value groups)
+            want = O.typed_row_bytes(t, n) if t in (0, 1, 2, 12, 14) and n % 32 == 0 else 0
+            assert lib.mia_weight_row_bytes(t, n) == want, (t, n)
+    buf = np.zeros(64, np.float32)
+    p = (buf.ctypes.data + 15) // 16 * 16
+    assert lib.mia_matvec_f32(p, 3, p, p, 8, 256, None) == mia.MIA_ERR_UNSUPPORTED   # Q4_1
+    assert lib.mia_matvec_f32(p, mia.TYPE_Q4_K, p, p, 8, 128, None) == mia.MIA_ERR_UNSUPPORTED
+    assert lib.mia_matvec_f32(p + 2, mia.TYPE_Q4_K, p, p, 8, 256, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_matvec_f32(p + 2, mia.TYPE_Q6_K, p + 4, p, 8, 256, None) == mia.MIA_ERR_INVALID
+    assert b"x must be 16-byte" in lib.mia_last_error()
+    assert lib.mia_matvec_q8(p, mia.TYPE_Q6_K, p + 2, p, 8, 256, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_matvec_q8(p, mia.TYPE_Q4_0, p, p, 8, 96, None) == mia.MIA_ERR_UNSUPPORTED
+    assert lib.mia_dequant_f32(p, mia.TYPE_F16, p + 4, 8, 64, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_dequant_f32(p, mia.TYPE_F16, p, 0, 64, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_gemm_f32(p, mia.TYPE_Q6_K, p, p, 8, 200, 4, None) == mia.MIA_ERR_UNSUPPORTED
+    assert lib.mia_gemm_f32(p, mia.TYPE_F32, p, p + 4, 8, 64, 4, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_gemm_f32(p, mia.TYPE_Q4_0, p, p, 8, 96, 4, None) == mia.MIA_ERR_UNSUPPORTED
+    lw = mia.LayerWeightsTyped(*([p] * 7), *([mia.TYPE_Q4_K] * 7), p, p)
+    lw.w2_type = 5                                                            # Q5_0
+    assert lib.mia_prefill_layer_typed(p, ctypes.byref(lw), p, p, p, 512, 1024, 4, 1, 1e-5, 64,
+                                       0, 4, None) == mia.MIA_ERR_UNSUPPORTED
+    lw.w2_type, lw.w1 = mia.TYPE_Q6_K, None
+    assert lib.mia_prefill_layer_typed(p, ctypes.byref(lw), p, p, p, 512, 1024, 4, 1, 1e-5, 64,
+                                       0, 4, None) == mia.MIA_ERR_INVALID
+    # the C struct and the binding agree
+    if os.path.exists(CLANG):
+        src = tmp_path / "lw.c"
+        src.write_text(r'''
+#include <stddef.h>
+#include "miattn.h"
+_Static_assert(offsetof(mia_layer_weights_typed, wq_type) == %d, "types");
+_Static_assert(offsetof(mia_layer_weights_typed, w3_type) == %d, "types");
+_Static_assert(offsetof(mia_layer_weights_typed, rms_att) == %d, "rms");
+_Static_assert(sizeof(mia_layer_weights_typed) == %d, "size");
+''' % (mia.LayerWeightsTyped.wq_type.offset, mia.LayerWeightsTyped.w3_type.offset,
+       mia.LayerWeightsTyped.rms_att.offset, ctypes.sizeof(mia.LayerWeightsTyped)))
+        subprocess.run([CLANG, "-std=c11", "-fsyntax-only", "-I", INCLUDE, str(src)], check=True)
+
+
 def test_q4_argument_errors_without_device_work():
     lib = mia.load()
     buf = np.zeros(64, np.float32)

@@ -7,7 +7,9 @@ float64, not by restating its loops."""
 import numpy as np
 import pytest
 
+import _data as D
 import _oracle as O
+import test_oracle_prefill as P
 
 
 def _pack_q4_k_scales(sc, m):
@@ -136,7 +138,7 @@ def test_f16_f32_and_q4_0_rows_exact():
     assert np.array_equal(O.dequant_typed(W, O.TYPE_Q4_0, 8, 96), O.dequant_q4_0(W, 8, 96))
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K, O.TYPE_F16, O.TYPE_F32])
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K, O.TYPE_F16, O.TYPE_F32, O.TYPE_Q4_0])
 def test_typed_matvec_against_float64(t):
     g = np.random.default_rng(10 + t)
     rows, cols = 37, 1024
@@ -181,3 +183,92 @@ def test_row_bytes():
     assert O.typed_row_bytes(O.TYPE_Q4_0, 4096) == 128 * 18
     assert O.typed_row_bytes(O.TYPE_Q4_K, 100) == 0
     assert O.typed_row_bytes(7, 256) == 0
+
+
+def _ones_row(t, cols):
+    """A row of weights all exactly 1.0 in type t (d = 1, q at its offset + 1)."""
+    if t == O.TYPE_Q4_0:
+        blk = np.zeros(18, np.uint8)
+        blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+        blk[2:] = 9 | (9 << 4)                                  # q - 8 = 1
+        return np.tile(blk, cols // 32)[None]
+    ql, qh = _q6_k_encode(np.full(256, 33))                     # q - 32 = 1
+    blk = np.concatenate([ql, qh, np.ones(16, np.int8).view(np.uint8),
+                          np.frombuffer(np.float16(1.0).tobytes(), np.uint8)])
+    return np.tile(blk, cols // 256)[None]
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q4_0, O.TYPE_Q6_K])
+def test_typed_matvec_four_lane_order(t):
+    # q4_0_matvec_f32 / q6_K_matvec_f32_neon keep four fp32 lane sums (value
+    # i in lane i % 4) and add them at the end: with x0 = 2^24 and x1 = x5 = 1
+    # lane 1 holds 2 and the row sums to 2^24 + 2 exactly, where a sum in k
+    # order rounds 2^24 + 1 back to 2^24 twice
+    cols = 256
+    x = np.zeros(cols, np.float32)
+    x[0], x[1], x[5] = 2.0 ** 24, 1.0, 1.0
+    W = _ones_row(t, cols)
+    assert np.array_equal(O.dequant_typed(W, t, 1, cols), np.ones((1, cols), np.float32))
+    assert O.typed_matvec(W, t, x, 1, cols)[0] == 2.0 ** 24 + 2
+    # the F32 path (sgemv, k order) on the same values
+    Wf = np.ones((1, cols), np.float32).view(np.uint8)
+    assert O.typed_matvec(Wf, O.TYPE_F32, x, 1, cols)[0] == 2.0 ** 24
+
+
+# Q4_K_M's mix (the reference's target files, mistral/gguf_loader.h:1-2): Q4_K
+# matrices with Q6_K for the value and down projections
+Q4_K_M = {"wq": O.TYPE_Q4_K, "wk": O.TYPE_Q4_K, "wv": O.TYPE_Q6_K, "wo": O.TYPE_Q4_K,
+          "w1": O.TYPE_Q4_K, "w3": O.TYPE_Q4_K, "w2": O.TYPE_Q6_K}
+
+
+def make_layer_typed(g, types, dim, hidden, nh, nkv):
+    kvd = dim // nh * nkv
+    shapes = {"wq": (dim, dim), "wk": (kvd, dim), "wv": (kvd, dim), "wo": (dim, dim),
+              "w1": (hidden, dim), "w3": (hidden, dim), "w2": (dim, hidden)}
+    W = {k: O.make_typed(g, types[k], *shapes[k]) for k in O.MATS}
+    W["rms_att"] = (1.0 + 0.1 * g.standard_normal(dim)).astype(np.float32)
+    W["rms_ffn"] = (1.0 + 0.1 * g.standard_normal(dim)).astype(np.float32)
+    return W
+
+
+def _ring(g, M, kvd, start):
+    kc = np.zeros((M, kvd), np.uint16)
+    vc = np.zeros((M, kvd), np.uint16)
+    kc[:start] = D.to_f16_bits(g.standard_normal((start, kvd)).astype(np.float32))
+    vc[:start] = D.to_f16_bits(g.standard_normal((start, kvd)).astype(np.float32))
+    return kc, vc
+
+
+def test_prefill_layer_typed_all_q4_0_is_prefill_layer():
+    g = np.random.default_rng(41)
+    dim, hidden, nh, nkv, M, start, S = 256, 512, 4, 1, 32, 3, 6
+    W = P.make_layer(g, dim, hidden, nh, nkv)
+    kc, vc = _ring(g, M, dim // nh * nkv, start)
+    X = g.standard_normal((S, dim)).astype(np.float32)
+    th = O.theta_inv(1e6, dim // nh)
+    k1, v1, k2, v2 = kc.copy(), vc.copy(), kc.copy(), vc.copy()
+    a = O.prefill_layer(W, X, k1, v1, start, S, dim, hidden, nh, nkv, th)
+    b = O.prefill_layer_typed(W, {k: O.TYPE_Q4_0 for k in O.MATS}, X, k2, v2, start, S, dim,
+                              hidden, nh, nkv, th)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+
+
+@pytest.mark.parametrize("mix", ["q4_k_m", "f16_f32"])
+def test_prefill_layer_typed_matches_float64(mix):
+    g = np.random.default_rng(42)
+    types = Q4_K_M if mix == "q4_k_m" else {
+        "wq": O.TYPE_F16, "wk": O.TYPE_F32, "wv": O.TYPE_F16, "wo": O.TYPE_Q4_0,
+        "w1": O.TYPE_F32, "w3": O.TYPE_Q4_K, "w2": O.TYPE_F16}
+    dim, hidden, nh, nkv, M, start, S = 512, 768, 4, 1, 32, 5, 8
+    W = make_layer_typed(g, types, dim, hidden, nh, nkv)
+    kc, vc = _ring(g, M, dim // nh * nkv, start)
+    X = g.standard_normal((S, dim)).astype(np.float32)
+    th = O.theta_inv(1e6, dim // nh)
+    ref, kring = P._layer64(W, X, kc, vc, start, S, dim, hidden, nh, nkv, th, 1e-5, types)
+    ko, vo = kc.copy(), vc.copy()
+    out = O.prefill_layer_typed(W, types, X, ko, vo, start, S, dim, hidden, nh, nkv, th)
+    assert np.abs(out - ref).max() <= 2e-4 * max(1.0, np.abs(ref).max())
+    slots = np.arange(start, start + S) % M
+    assert np.abs(D.f16_bits_to_f32(ko[slots]) - kring[slots]).max() <= 2e-3 * max(
+        1.0, np.abs(kring[slots]).max())

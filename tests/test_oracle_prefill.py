@@ -73,11 +73,13 @@ def _rope64(x, pos, th, n_heads, hd):
     return np.stack([e * c - o * s, o * c + e * s], axis=-1).reshape(-1)
 
 
-def _layer64(W, X, kc, vc, start, S, dim, hidden, nh, nkv, th, eps):
-    """The prefill layer in float64 (fp16 ring entries as the ring holds them)."""
+def _layer64(W, X, kc, vc, start, S, dim, hidden, nh, nkv, th, eps, types=None):
+    """The prefill layer in float64 (fp16 ring entries as the ring holds them);
+    types: GGML type of each matrix (default all Q4_0)."""
     hd, M = dim // nh, kc.shape[0]
     kvd = nkv * hd
-    dq = {k: O.dequant_q4_0(W[k], *shape) for k, shape in
+    types = types or {k: O.TYPE_Q4_0 for k in O.MATS}
+    dq = {k: O.dequant_typed(W[k], types[k], *shape).astype(np.float64) for k, shape in
           (("wq", (dim, dim)), ("wk", (kvd, dim)), ("wv", (kvd, dim)), ("wo", (dim, dim)),
            ("w1", (hidden, dim)), ("w3", (hidden, dim)), ("w2", (dim, hidden)))}
 
