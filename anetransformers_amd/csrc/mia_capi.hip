@@ -53,8 +53,9 @@ struct DevCtx {
   size_t split_work_bytes = 0;
   int *owner = nullptr;  // long chunks of mia_attention_chunk: last token per ring slot, -1 at rest
   int owner_slots = 0;
-  // Weight types other than Q4_0 in the GEMM: the dequantised fp32 matrix,
-  // multiplied by rocBLAS sgemm (handle created on first use).
+  // Weight types other than Q4_0 in the GEMM: the weights' fp16 planes and
+  // the partial products, multiplied by rocBLAS gemm_ex (handle created on
+  // first use).
   float *wbuf = nullptr;
   size_t wbuf_bytes = 0;
   rocblas_handle blas = nullptr;
@@ -1102,24 +1103,53 @@ static int check_typed(int type, int in_dim, const void *W) {
   return MIA_OK;
 }
 
-// Y [S][N] (+)= X [S][K] . W^T for a weight type other than Q4_0: the fp32
-// weights into wbuf, then sgemm.  rocBLAS is column-major: Y^T [N][S] =
-// (W^T [K][N])^T . X^T [K][S], so W is the transposed A operand with lda K.
+// Y [S][N] (+)= X [S][K] . W^T for a weight type other than Q4_0, on fp16
+// MFMA with fp32 accumulation (rocBLAS gemm_ex): X as fp16 hi + lo planes
+// (launch_split_hilo), W as its fp16 values (Q4_K, F16: exact) or as row-scaled
+// hi + lo planes (Q6_K, F32: launch_typed_split).  C1 = [Xhi; Xlo] . Whi^T in
+// one GEMM of 2S columns, C2 = Xhi . Wlo^T; the combine kernel sums the parts
+// (the Xlo . Wlo term, ~2^-22 of the product, is dropped).  rocBLAS is
+// column-major: C^T [N][cols] = (W^T [K][N])^T . B^T [K][cols], so W is the
+// transposed A operand with lda K and C's leading dimension is N.
+// reuse_x: split_work already holds X's planes (the call before split the
+// same X on this stream), and X is not read.
 static int typed_gemm_impl(DevCtx *c, const void *W, int type, const float *X, float *Y, int N,
-                           int K, int S, bool add, hipStream_t s) {
+                           int K, int S, bool add, hipStream_t s, bool reuse_x = false) {
   if (type == MIA_TYPE_Q4_0)
     return gemm_impl(c, W, nullptr, nullptr, N, 0, 0, X, K, S, Y, nullptr, nullptr,
-                     add ? mia::kGemmAdd : mia::kGemmStore, s);
-  if (int rc = ensure_wbuf(c, (size_t)N * K * sizeof(float))) return rc;
+                     add ? mia::kGemmAdd : mia::kGemmStore, s, reuse_x);
+  const bool lo = !mia::typed_is_f16_exact(type);
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  const size_t bw = al((size_t)N * K * 2), bc1 = al((size_t)2 * S * N * 4),
+               bc2 = al((size_t)S * N * 4), br = al((size_t)N * 4);
+  if (int rc = ensure_wbuf(c, bw * (lo ? 2 : 1) + bc1 + (lo ? bc2 + br : 0))) return rc;
+  if (int rc = ensure_split_work(c, (size_t)2 * S * K * sizeof(_Float16))) return rc;
   if (int rc = ensure_blas(c)) return rc;
-  HIP_TRY(mia::launch_typed_dequant(W, type, c->wbuf, N, K, s));
-  const float one = 1.0f, beta = add ? 1.0f : 0.0f;
+  char *w = reinterpret_cast<char *>(c->wbuf);
+  _Float16 *whi = reinterpret_cast<_Float16 *>(w);
+  _Float16 *wlo = lo ? reinterpret_cast<_Float16 *>(w + bw) : nullptr;
+  float *C1 = reinterpret_cast<float *>(w + bw * (lo ? 2 : 1));
+  float *C2 = lo ? reinterpret_cast<float *>(w + bw * 2 + bc1) : nullptr;
+  float *rs = lo ? reinterpret_cast<float *>(w + bw * 2 + bc1 + bc2) : nullptr;
+  _Float16 *xhi = reinterpret_cast<_Float16 *>(c->split_work);  // [2][S][K]: hi, then lo
+  HIP_TRY(mia::launch_typed_split(W, type, whi, wlo, rs, N, K, s));
+  if (!reuse_x)
+    HIP_TRY(mia::launch_split_hilo(X, (long)S * K, xhi, xhi + (size_t)S * K, c->num_cus, s));
+  const float one = 1.0f, zero = 0.0f;
   rocblas_status st = rocblas_set_stream(c->blas, s);
   if (st == rocblas_status_success)
-    st = rocblas_sgemm(c->blas, rocblas_operation_transpose, rocblas_operation_none, N, S, K, &one,
-                       c->wbuf, K, X, K, &beta, Y, N);
+    st = rocblas_gemm_ex(c->blas, rocblas_operation_transpose, rocblas_operation_none, N, 2 * S,
+                         K, &one, whi, rocblas_datatype_f16_r, K, xhi, rocblas_datatype_f16_r, K,
+                         &zero, C1, rocblas_datatype_f32_r, N, C1, rocblas_datatype_f32_r, N,
+                         rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  if (st == rocblas_status_success && lo)
+    st = rocblas_gemm_ex(c->blas, rocblas_operation_transpose, rocblas_operation_none, N, S, K,
+                         &one, wlo, rocblas_datatype_f16_r, K, xhi, rocblas_datatype_f16_r, K,
+                         &zero, C2, rocblas_datatype_f32_r, N, C2, rocblas_datatype_f32_r, N,
+                         rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
   if (st != rocblas_status_success)
-    return set_err(MIA_ERR_HIP, "rocblas_sgemm: %s", rocblas_status_to_string(st));
+    return set_err(MIA_ERR_HIP, "rocblas_gemm_ex: %s", rocblas_status_to_string(st));
+  HIP_TRY(mia::launch_hilo_combine(C1, C2, rs, Y, S, N, add, s));
   return MIA_OK;
 }
 
@@ -1236,9 +1266,12 @@ int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const f
   float *U = reinterpret_cast<float *>(w + 3 * bd + 2 * bk + bh);
   // mistral_ane_prefill.h:1092-1110
   HIP_TRY(mia::launch_rmsnorm(XN, X, lw->rms_att, dim, S, eps, s));
+  // (the normalised rows are split into fp16 planes once for Q, K and V)
   if (int rc = typed_gemm_impl(c, lw->wq, lw->wq_type, XN, Q, dim, dim, S, false, s)) return rc;
-  if (int rc = typed_gemm_impl(c, lw->wk, lw->wk_type, XN, K, kv_dim, dim, S, false, s)) return rc;
-  if (int rc = typed_gemm_impl(c, lw->wv, lw->wv_type, XN, V, kv_dim, dim, S, false, s)) return rc;
+  if (int rc = typed_gemm_impl(c, lw->wk, lw->wk_type, XN, K, kv_dim, dim, S, false, s, true))
+    return rc;
+  if (int rc = typed_gemm_impl(c, lw->wv, lw->wv_type, XN, V, kv_dim, dim, S, false, s, true))
+    return rc;
   // apply_rope_batch, kv_write_batch, attention_batch, as mia_prefill_layer
   if (int rc = ensure_work(c, (size_t)S * kHD * sizeof(float))) return rc;
   float *cs = reinterpret_cast<float *>(c->work);
@@ -1252,7 +1285,8 @@ int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const f
   if (int rc = typed_gemm_impl(c, lw->wo, lw->wo_type, A, X, dim, dim, S, true, s)) return rc;
   HIP_TRY(mia::launch_rmsnorm(XN, X, lw->rms_ffn, dim, S, eps, s));
   if (int rc = typed_gemm_impl(c, lw->w1, lw->w1_type, XN, G, hidden, dim, S, false, s)) return rc;
-  if (int rc = typed_gemm_impl(c, lw->w3, lw->w3_type, XN, U, hidden, dim, S, false, s)) return rc;
+  if (int rc = typed_gemm_impl(c, lw->w3, lw->w3_type, XN, U, hidden, dim, S, false, s, true))
+    return rc;
   HIP_TRY(mia::launch_silu_mul(G, U, (long)S * hidden, s));
   return typed_gemm_impl(c, lw->w2, lw->w2_type, G, X, dim, hidden, S, true, s);
 }

@@ -195,6 +195,16 @@ hipError_t launch_typed_matvec(const void *W, int type, const void *x, bool x_q8
 // out [rows][cols] fp32 = the weights the reference multiplies.
 hipError_t launch_typed_dequant(const void *W, int type, float *out, int rows, int cols,
                                 hipStream_t s);
+// The weights as the fp16 GEMM operands: hi [rows][cols]; for types whose
+// values are not fp16 (Q6_K, F32) also lo [rows][cols] and rscale [rows], with
+// w = (hi + lo) * rscale to 2^-22 relative (lo, rscale unused otherwise).
+bool typed_is_f16_exact(int type);
+hipError_t launch_typed_split(const void *W, int type, _Float16 *hi, _Float16 *lo, float *rscale,
+                              int rows, int cols, hipStream_t s);
+// Y [S][N] (+)= rscale[n] * ((C1[s][n] + C1[S + s][n]) + C2[s][n]); C2 and
+// rscale null: Y (+)= C1[s][n] + C1[S + s][n].
+hipError_t launch_hilo_combine(const float *C1, const float *C2, const float *rscale, float *Y,
+                               int S, int N, bool add, hipStream_t s);
 // gate [n] = gate * sigmoid(gate) * up (the SwiGLU product).
 hipError_t launch_silu_mul(float *gate, const float *up, long n, hipStream_t s);
 

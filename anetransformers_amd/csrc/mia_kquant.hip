@@ -9,21 +9,28 @@
 //         w = fp16(fp16(q * vd) - vm)
 //   Q6_K  w = (d * scales[n / 16]) * (q - 32) in fp32 (dequant_q6_K_block,
 //         dequant.h:291-307), value n taken from ql / qh as that function does
-//   Q4_0  (prefill GEMM only) w = d * (q - 8) in fp32 (mistral_ane_prefill.h:921-939)
-// Every kernel here forms those weights bit for bit, 32 consecutive values
-// of a row at a time (a "group": a Q4_K sub-block, two Q6_K sub-blocks, a
-// Q4_0 block), and then
-//   typed_matvec_kernel   y = W . x, one wave per row, lane l taking the row's
-//                         groups l, l + 64, ...; x fp32 or Q8_0 blocks (the
-//                         reference's non-Q4_0 decode path dequantises its
-//                         Q8_0 activations, mistral_model.h:656-670); fp32
-//                         fma per lane, then a wave sum (the reference's
-//                         sgemv / four-lane NEON sums in another order)
-//   typed_dequant_kernel  the fp32 weight rows, for the prefill GEMM, which
-//                         the library then hands to the BLAS library's sgemm
-//                         as the reference does (mistral_ane_prefill.h:1018-1042)
-// Memory-bound like the Q4_0 matvec: 0.5625 (Q4_K), 0.82 (Q6_K), 2 or 4
-// bytes per weight.
+//   Q4_0  w = d * (q - 8) in fp32 (q4_0_matvec_f32, dequant.h:142-278;
+//         mistral_ane_prefill.h:921-939)
+// Every kernel here forms those weights bit for bit, 32 consecutive values of
+// a row at a time (a "group": a Q4_K sub-block, two Q6_K sub-blocks, a Q4_0
+// block):
+//   kquant_matvec_kernel  y = W . x for Q4_K / Q6_K, x fp32 or Q8_0 blocks
+//                         (the reference's non-Q4_0 decode path dequantises
+//                         its Q8_0 activations, mistral_model.h:656-670); R
+//                         rows per wave sharing the lane's x values
+//   typed_matvec_kernel   the same for F16, F32 and Q4_0 with fp32 x, one
+//                         wave per row
+//   typed_dequant_kernel  the fp32 weight rows (dequant_weight_to_fp32_buf)
+//   typed_split_kernel    the prefill GEMM's fp16 operands: the fp16 values of
+//                         Q4_K / F16 weights, row-scaled hi + lo halves of
+//                         Q6_K / F32 weights, for rocBLAS gemm_ex
+//   hilo_combine_kernel   the GEMM's partial products summed (+ residual)
+//   silu_mul_kernel       the SwiGLU product between the FFN GEMMs
+// Every matvec row sums its fp32 products in another order than the
+// reference's sgemv / four-lane NEON sums.  The matvecs are memory-bound:
+// 0.5625 (Q4_K), 0.82 (Q6_K), 2 or 4 bytes per weight.
+#include <type_traits>
+
 #include "mia_device.h"
 #include "mia_kernels.h"
 
@@ -167,6 +174,196 @@ __global__ void __launch_bounds__(512) typed_matvec_kernel(const uint8_t *W, lon
   if (lane == 0) y[row] = acc;
 }
 
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ u4 load_u4_unaligned(const uint8_t *p) {
+  u4 v;
+  __builtin_memcpy(&v, p, 16);
+  return v;
+}
+
+// The K-quant matvec: each wave takes kKqRows consecutive rows and lane l the
+// 32-value groups l, l + 64, ... of all of them, so that the lane's 32 x
+// values are loaded (and, from Q8_0 blocks, formed) once for kKqRows rows.
+//   Q4_K: the group's 32 nibbles as packed fp16 pairs (0x6400 | n is
+//         1024 + n), then p = fl16(n * vd) as one packed fma, (1024 + n) * vd
+//         - 1024 * vd, whose exact value is n * vd (1024 * vd is exact in
+//         fp16 while |vd| <= 63.5; otherwise 1024 is subtracted first), and
+//         w = fl16(p - vm): every weight is the reference's; fp32 fma against x.
+//   Q6_K: the values q - 32 as fp32 (exact), sum_k q_k x_k per 16-value
+//         sub-block, times d * scale: w = d * scale * q is exact in fp32
+//         (11 + 7 + 5 significant bits), so this is the reference's sum
+//         reassociated.
+constexpr int kKqRows = 4;
+
+template <int E>
+__device__ __forceinline__ float ubyte_f32(unsigned q) {
+  float f;
+  if constexpr (E == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(q));
+  if constexpr (E == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(q));
+  if constexpr (E == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(q));
+  if constexpr (E == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(q));
+  return f;
+}
+
+// A group's raw bytes, loaded for every row before any is used.
+struct Q4KRaw {
+  u4 hdr, qa, qb;
+};
+struct Q6KRaw {
+  u4 ql0, ql1, qh0, qh1;
+  unsigned sc2;  // the two int8 scales of the group's sub-blocks
+  unsigned dh;   // fp16 d
+};
+
+__device__ __forceinline__ void kq_load(const uint8_t *row, int g, Q4KRaw &r) {
+  const uint8_t *blk = row + (size_t)(g >> 3) * kQ4KBytes;
+  const int j = g & 7;
+  r.hdr = *reinterpret_cast<const u4 *>(blk);
+  r.qa = *reinterpret_cast<const u4 *>(blk + 16 + 32 * (j >> 1));
+  r.qb = *reinterpret_cast<const u4 *>(blk + 32 + 32 * (j >> 1));
+}
+
+__device__ __forceinline__ void kq_load(const uint8_t *row, int g, Q6KRaw &r) {
+  const uint8_t *blk = row + (size_t)(g >> 3) * kQ6KBytes;
+  const int n0 = 32 * (g & 7);
+  const uint8_t *qlp = blk + (n0 < 128 ? n0 : n0 - 128);
+  const uint8_t *qhp = blk + 128 + (n0 & 63);
+  r.ql0 = load_u4_unaligned(qlp);
+  r.ql1 = load_u4_unaligned(qlp + 16);
+  r.qh0 = load_u4_unaligned(qhp);
+  r.qh1 = load_u4_unaligned(qhp + 16);
+  r.sc2 = load_u16(blk + 192 + (n0 >> 4));
+  r.dh = load_u16(blk + 208);
+}
+
+__device__ __forceinline__ float kq_dot(const Q4KRaw &raw, int g, const float (&x)[32]) {
+#pragma clang fp contract(off)
+  const int j = g & 7;
+  const u4 hdr = raw.hdr;
+  const float d = half_bits(hdr[0] & 0xFFFF), dmin = half_bits(hdr[0] >> 16);
+  // get_scale_min_k4 (dequant.h:58-66): the bytes sit at position j % 4 of
+  // the words holding scale bytes 0-3, 4-7 and 8-11
+  const int p8 = 8 * (j & 3);
+  const unsigned x1 = hdr[1] >> p8, x2 = hdr[2] >> p8, x3 = hdr[3] >> p8;
+  const unsigned sv = j < 4 ? (x1 & 63) : ((x3 & 0xF) | ((x1 >> 2) & 0x30));
+  const unsigned mv = j < 4 ? (x2 & 63) : (((x3 >> 4) & 0xF) | ((x2 >> 2) & 0x30));
+  const _Float16 vd = (_Float16)(d * (float)sv), vm = (_Float16)(dmin * (float)mv);
+  const h2 vd2 = {vd, vd}, vm2 = {vm, vm};
+  const _Float16 c = (_Float16)-1024.0f * vd;
+  const h2 c2 = {c, c}, k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+  const int sh = 4 * (j & 1);
+  const unsigned magic = 0x64006400u;
+  const bool fast = __all(__builtin_fabsf((float)vd) <= 63.5f);
+  const u4 qv[2] = {raw.qa, raw.qb};
+  float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const unsigned t = qv[i >> 2][i & 3] >> sh;
+    // bytes 0, 2 and bytes 1, 3 of the word: values 4i, 4i + 2 and 4i + 1, 4i + 3
+    unsigned ua, ub;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(ua) : "v"(t), "s"(0x000F000Fu), "v"(magic));
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(ub) : "v"(t >> 8), "s"(0x000F000Fu), "v"(magic));
+    const h2 na = __builtin_bit_cast(h2, ua), nb = __builtin_bit_cast(h2, ub);
+    h2 pa, pb;
+    if (fast) {
+      pa = __builtin_elementwise_fma(na, vd2, c2);
+      pb = __builtin_elementwise_fma(nb, vd2, c2);
+    } else {
+      pa = (na - k1024) * vd2;
+      pb = (nb - k1024) * vd2;
+    }
+    const h2 wa = pa - vm2, wb = pb - vm2;
+    acc0 = __builtin_fmaf((float)wa[0], x[4 * i], acc0);
+    acc1 = __builtin_fmaf((float)wb[0], x[4 * i + 1], acc1);
+    acc0 = __builtin_fmaf((float)wa[1], x[4 * i + 2], acc0);
+    acc1 = __builtin_fmaf((float)wb[1], x[4 * i + 3], acc1);
+  }
+  return acc0 + acc1;
+}
+
+__device__ __forceinline__ float kq_dot(const Q6KRaw &raw, int g, const float (&x)[32]) {
+#pragma clang fp contract(off)
+  const int n0 = 32 * (g & 7);
+  const int lo_sh = n0 < 128 ? 0 : 4;
+  const int r = n0 >> 6;
+  const int hi_sh = r == 0 ? 0 : (r == 1 ? 4 : (r == 2 ? 2 : 6));
+  const float d = half_bits(raw.dh);
+  const float ds0 = d * (float)(int)(signed char)(raw.sc2 & 0xFF);
+  const float ds1 = d * (float)(int)(signed char)(raw.sc2 >> 8);
+  const u4 ql[2] = {raw.ql0, raw.ql1}, qh[2] = {raw.qh0, raw.qh1};
+  float acc[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const unsigned q = ((ql[i >> 2][i & 3] >> lo_sh) & 0x0F0F0F0Fu) |
+                       (((qh[i >> 2][i & 3] >> hi_sh) & 0x03030303u) << 4);
+    float(&a)[2] = acc[i >> 2];
+    a[0] = __builtin_fmaf(ubyte_f32<0>(q) - 32.0f, x[4 * i], a[0]);
+    a[1] = __builtin_fmaf(ubyte_f32<1>(q) - 32.0f, x[4 * i + 1], a[1]);
+    a[0] = __builtin_fmaf(ubyte_f32<2>(q) - 32.0f, x[4 * i + 2], a[0]);
+    a[1] = __builtin_fmaf(ubyte_f32<3>(q) - 32.0f, x[4 * i + 3], a[1]);
+  }
+  return ds0 * (acc[0][0] + acc[0][1]) + ds1 * (acc[1][0] + acc[1][1]);
+}
+
+template <int TYPE>
+using KqRaw = typename std::conditional<TYPE == kTypeQ4K, Q4KRaw, Q6KRaw>::type;
+
+// R rows per wave, 4 waves per workgroup.
+template <int TYPE, bool XQ8, int R>
+__global__ void __launch_bounds__(256) kquant_matvec_kernel(const uint8_t *W, long row_bytes,
+                                                            const void *x, float *y, int rows,
+                                                            int cols) {
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  if (row0 >= rows) return;  // whole wave
+  const int ngroups = cols >> 5;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  for (int g = lane; g < ngroups; g += 64) {
+    KqRaw<TYPE> raw[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)  // a row past the end reloads the last row
+      kq_load(W + (size_t)min(row0 + r, rows - 1) * row_bytes, g, raw[r]);
+    float xs[32];
+    if constexpr (XQ8) {
+      // Q8_0 block g (fp32 d, 32 int8; 4-byte aligned): values d * q in fp32
+      // as the reference forms them (mistral_model.h:662-666)
+      const unsigned *blk = reinterpret_cast<const unsigned *>(
+          reinterpret_cast<const uint8_t *>(x) + (size_t)g * 36);
+      unsigned w[9];
+#pragma unroll
+      for (int k = 0; k < 9; ++k) w[k] = blk[k];
+      const float d = __builtin_bit_cast(float, w[0]);
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xs[4 * k + e] = d * (float)(int)(signed char)((w[1 + k] >> (8 * e)) & 0xFF);
+    } else {
+      const f4 *xv = reinterpret_cast<const f4 *>(reinterpret_cast<const float *>(x) + 32 * g);
+      f4 v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = xv[k];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        xs[4 * k] = v[k].x;
+        xs[4 * k + 1] = v[k].y;
+        xs[4 * k + 2] = v[k].z;
+        xs[4 * k + 3] = v[k].w;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] += kq_dot(raw[r], g, xs);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float v = wave_sum(acc[r]);
+    if (lane == 0 && row0 + r < rows) y[row0 + r] = v;
+  }
+}
+
 // One thread per group: 32 fp32 weights of a row.
 template <int TYPE>
 __global__ void __launch_bounds__(256) typed_dequant_kernel(const uint8_t *W, long row_bytes,
@@ -180,6 +377,106 @@ __global__ void __launch_bounds__(256) typed_dequant_kernel(const uint8_t *W, lo
     f4 *dst = reinterpret_cast<f4 *>(out + (size_t)r * cols + 32 * g);
 #pragma unroll
     for (int k = 0; k < 8; ++k) dst[k] = (f4){w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]};
+  }
+}
+
+// The GEMM's fp16 operands, one workgroup per row.  Q4_K and F16 weights are
+// fp16 values already: hi = w, no lo plane.  Q6_K and F32 weights are scaled by
+// a power of two 2^e per row (the row's largest |w| lands in [2^13, 2^14), so
+// that lo stays a normal fp16 for every weight within 2^-17 of the row's
+// largest) and split, w 2^e = hi + lo to 2^-22 relative; rscale[row] = 2^-e.
+template <int TYPE>
+__global__ void __launch_bounds__(256) typed_f16_kernel(const uint8_t *W, long row_bytes,
+                                                        _Float16 *hi, int rows, int cols) {
+  const int ngroups = cols >> 5;
+  const long total = (long)rows * ngroups;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    const int r = (int)(i / ngroups), g = (int)(i % ngroups);
+    float v[32];
+    dequant_group<TYPE>(W + (size_t)r * row_bytes, g, v);
+    h8 h[4];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) h[k >> 3][k & 7] = (_Float16)v[k];  // exact
+    h8 *dh = reinterpret_cast<h8 *>(hi + (size_t)r * cols + 32 * g);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) dh[k] = h[k];
+  }
+}
+
+template <int TYPE, bool LO>
+__global__ void __launch_bounds__(256) typed_split_kernel(const uint8_t *W, long row_bytes,
+                                                          _Float16 *hi, _Float16 *lo,
+                                                          float *rscale, int rows, int cols) {
+  __shared__ float wmax[4];
+  const int ngroups = cols >> 5;
+  for (int r = blockIdx.x; r < rows; r += gridDim.x) {
+    const uint8_t *wr = W + (size_t)r * row_bytes;
+    float scale = 1.0f;
+    if constexpr (LO) {
+      float m = 0.f;
+      for (int g = threadIdx.x; g < ngroups; g += 256) {
+        float v[32];
+        dequant_group<TYPE>(wr, g, v);
+#pragma unroll
+        for (int l = 0; l < 32; ++l) m = fmaxf(m, fabsf(v[l]));
+      }
+      m = wave_max(m);
+      if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+      __syncthreads();
+      m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+      __syncthreads();  // wmax is rewritten for the next row
+      int ex = 0;
+      if (m > 0.f && m <= 3.4e38f) (void)frexpf(m, &ex);
+      const int e = min(max(14 - ex, -60), 60);
+      scale = ldexpf(1.0f, e);
+      if (threadIdx.x == 0) rscale[r] = ldexpf(1.0f, -e);
+    }
+    for (int g = threadIdx.x; g < ngroups; g += 256) {
+      float v[32];
+      dequant_group<TYPE>(wr, g, v);
+      h8 h[4], l4[4];
+#pragma unroll
+      for (int k = 0; k < 32; ++k) {
+        const float x = v[k] * scale;
+        const _Float16 xh = (_Float16)x;
+        h[k >> 3][k & 7] = xh;
+        if constexpr (LO) l4[k >> 3][k & 7] = (_Float16)(x - (float)xh);
+      }
+      h8 *dh = reinterpret_cast<h8 *>(hi + (size_t)r * cols + 32 * g);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) dh[k] = h[k];
+      if constexpr (LO) {
+        h8 *dl = reinterpret_cast<h8 *>(lo + (size_t)r * cols + 32 * g);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) dl[k] = l4[k];
+      }
+    }
+  }
+}
+
+// Y [S][N] (+)= rscale[n] * ((C1 [S][N] + C1 [S + s][N]) + C2 [S][N]): the
+// hi-activation and lo-activation products of the hi weights, plus the lo
+// weights' product (C2, rscale: null for fp16-valued weights).
+__global__ void __launch_bounds__(256) hilo_combine_kernel(const float *C1, const float *C2,
+                                                           const float *rscale, float *Y, int S,
+                                                           int N, bool add) {
+#pragma clang fp contract(off)
+  const long total = (long)S * N;
+  if ((N & 3) == 0) {  // four outputs per thread (16-byte aligned rows)
+    const long t4 = total >> 2;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < t4; i += (long)gridDim.x * 256) {
+      f4 v = reinterpret_cast<const f4 *>(C1)[i] + reinterpret_cast<const f4 *>(C1 + total)[i];
+      if (C2) v = (v + reinterpret_cast<const f4 *>(C2)[i]) *
+                  reinterpret_cast<const f4 *>(rscale)[(4 * i) % N >> 2];
+      f4 *y = reinterpret_cast<f4 *>(Y) + i;
+      *y = add ? *y + v : v;
+    }
+    return;
+  }
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    float v = C1[i] + C1[total + i];
+    if (C2) v = (v + C2[i]) * rscale[i % N];
+    Y[i] = add ? Y[i] + v : v;
   }
 }
 
@@ -204,6 +501,37 @@ hipError_t launch_matvec_t(const void *W, long rb, const void *x, bool xq8, floa
   else
     hipExtLaunchKernelGGL((typed_matvec_kernel<TYPE, false>), grid, block, 0, s, ev0, ev1, 0, w,
                           rb, x, y, rows, cols);
+  return hipGetLastError();
+}
+
+template <int TYPE, int R>
+void launch_kq_r(const uint8_t *w, long rb, const void *x, bool xq8, float *y, int rows, int cols,
+                 hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
+  const dim3 grid((rows + 4 * R - 1) / (4 * R)), block(256);
+  if (xq8)
+    hipExtLaunchKernelGGL((kquant_matvec_kernel<TYPE, true, R>), grid, block, 0, s, ev0, ev1, 0,
+                          w, rb, x, y, rows, cols);
+  else
+    hipExtLaunchKernelGGL((kquant_matvec_kernel<TYPE, false, R>), grid, block, 0, s, ev0, ev1, 0,
+                          w, rb, x, y, rows, cols);
+}
+
+// Rows per wave, measured on the Mistral shapes: one row per wave while the
+// matrix is small (the most waves in flight), more rows once there are
+// enough waves and the x loads (128 B per lane and row for fp32 x, 36 B for
+// Q8_0 blocks) start to cost.
+template <int TYPE>
+hipError_t launch_kq_matvec_t(const void *W, long rb, const void *x, bool xq8, float *y,
+                              int rows, int cols, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
+  const uint8_t *w = reinterpret_cast<const uint8_t *>(W);
+  const bool large = (long)rows * cols >= (32L << 20);
+  const int R = xq8 ? (large ? 2 : 1) : (rows < 2048 ? 1 : (large ? 4 : 2));
+  if (R == 4)
+    launch_kq_r<TYPE, 4>(w, rb, x, xq8, y, rows, cols, s, ev0, ev1);
+  else if (R == 2)
+    launch_kq_r<TYPE, 2>(w, rb, x, xq8, y, rows, cols, s, ev0, ev1);
+  else
+    launch_kq_r<TYPE, 1>(w, rb, x, xq8, y, rows, cols, s, ev0, ev1);
   return hipGetLastError();
 }
 
@@ -237,8 +565,8 @@ hipError_t launch_typed_matvec(const void *W, int type, const void *x, bool x_q8
   const long rb = typed_row_bytes(type, cols);
   if (rb == 0 || rows <= 0) return hipErrorInvalidValue;
   switch (type) {
-    case kTypeQ4K: return launch_matvec_t<kTypeQ4K>(W, rb, x, x_q8, y, rows, cols, s, ev0, ev1);
-    case kTypeQ6K: return launch_matvec_t<kTypeQ6K>(W, rb, x, x_q8, y, rows, cols, s, ev0, ev1);
+    case kTypeQ4K: return launch_kq_matvec_t<kTypeQ4K>(W, rb, x, x_q8, y, rows, cols, s, ev0, ev1);
+    case kTypeQ6K: return launch_kq_matvec_t<kTypeQ6K>(W, rb, x, x_q8, y, rows, cols, s, ev0, ev1);
     case kTypeF16: return launch_matvec_t<kTypeF16>(W, rb, x, x_q8, y, rows, cols, s, ev0, ev1);
     case kTypeF32: return launch_matvec_t<kTypeF32>(W, rb, x, x_q8, y, rows, cols, s, ev0, ev1);
     case kTypeQ40: return launch_matvec_t<kTypeQ40>(W, rb, x, x_q8, y, rows, cols, s, ev0, ev1);
@@ -258,6 +586,49 @@ hipError_t launch_typed_dequant(const void *W, int type, float *out, int rows, i
     case kTypeF32: return launch_dequant_t<kTypeF32>(W, rb, out, rows, cols, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+template <int TYPE, bool LO>
+hipError_t launch_split_t(const void *W, long rb, _Float16 *hi, _Float16 *lo, float *rscale,
+                          int rows, int cols, hipStream_t s) {
+  const uint8_t *w = reinterpret_cast<const uint8_t *>(W);
+  if constexpr (LO) {
+    const int blocks = rows < 16384 ? rows : 16384;
+    hipLaunchKernelGGL((typed_split_kernel<TYPE, true>), dim3(blocks), dim3(256), 0, s, w, rb, hi,
+                       lo, rscale, rows, cols);
+  } else {
+    const long total = (long)rows * (cols >> 5);
+    long blocks = (total + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL((typed_f16_kernel<TYPE>), dim3((unsigned)blocks), dim3(256), 0, s, w, rb,
+                       hi, rows, cols);
+  }
+  return hipGetLastError();
+}
+
+bool typed_is_f16_exact(int type) { return type == kTypeQ4K || type == kTypeF16; }
+
+hipError_t launch_typed_split(const void *W, int type, _Float16 *hi, _Float16 *lo, float *rscale,
+                              int rows, int cols, hipStream_t s) {
+  const long rb = typed_row_bytes(type, cols);
+  if (rb == 0 || rows <= 0) return hipErrorInvalidValue;
+  switch (type) {
+    case kTypeQ4K: return launch_split_t<kTypeQ4K, false>(W, rb, hi, lo, rscale, rows, cols, s);
+    case kTypeF16: return launch_split_t<kTypeF16, false>(W, rb, hi, lo, rscale, rows, cols, s);
+    case kTypeQ6K: return launch_split_t<kTypeQ6K, true>(W, rb, hi, lo, rscale, rows, cols, s);
+    case kTypeF32: return launch_split_t<kTypeF32, true>(W, rb, hi, lo, rscale, rows, cols, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_hilo_combine(const float *C1, const float *C2, const float *rscale, float *Y,
+                               int S, int N, bool add, hipStream_t s) {
+  const long total = (long)S * N;
+  long blocks = (total + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(hilo_combine_kernel, dim3((unsigned)blocks), dim3(256), 0, s, C1, C2, rscale,
+                     Y, S, N, add);
+  return hipGetLastError();
 }
 
 hipError_t launch_silu_mul(float *gate, const float *up, long n, hipStream_t s) {

@@ -647,6 +647,127 @@ class PrefillLayers:
                      None), "prefill_layer")
 
 
+# Q4_K_M's mix (the reference's target files): Q4_K everywhere but the value
+# and down projections, which are Q6_K
+TYPE_Q4_K, TYPE_Q6_K = mia.TYPE_Q4_K, mia.TYPE_Q6_K
+KM_SIZES = (("wq", DIM, DIM, TYPE_Q4_K), ("wk", KV_DIM, DIM, TYPE_Q4_K),
+            ("wv", KV_DIM, DIM, TYPE_Q6_K), ("wo", DIM, DIM, TYPE_Q4_K),
+            ("w1", HIDDEN, DIM, TYPE_Q4_K), ("w2", DIM, HIDDEN, TYPE_Q6_K),
+            ("w3", HIDDEN, DIM, TYPE_Q4_K))
+
+
+def km_bytes(rows: int, cols: int, t: int) -> int:
+    return rows * (cols // 256) * (144 if t == TYPE_Q4_K else 210)
+
+
+class TypedLayers:
+    """32 layers of Q4_K_M weights (4.45 GB): the decode projections through
+    mia_matvec_q8 (the reference's non-Q4_0 branch of q4_matvec_sdot_parallel,
+    seven launches per layer on Q8_0 inputs) and the prefill layer through
+    mia_prefill_layer_typed (S = 512 after 1536 cached, X carried).  The
+    weight bytes are a seeded fp16 N(0,1) stream with the block scales scaled
+    down so that the activations stay O(1)."""
+
+    def __init__(self, lib, seed: int = 61):
+        self.lib = lib
+        g = np.random.default_rng(seed)
+        self.offs, off = {}, 0
+        for name, r, c, t in KM_SIZES:
+            self.offs[name] = off
+            off += (km_bytes(r, c, t) + 255) // 256 * 256
+        self.lw_bytes = off
+        self.w = DeviceBuffer(N_LAYERS * self.lw_bytes)
+        check(lib.mia_fill_normal_f16(self.w.ptr, N_LAYERS * self.lw_bytes // 2, seed, None))
+        for l in range(N_LAYERS):
+            for name, r, c, t in KM_SIZES:
+                base = self.w.ptr + l * self.lw_bytes + self.offs[name]
+                n16 = km_bytes(r, c, t) // 2
+                if t == TYPE_Q4_K:   # d and dmin: the first 2 of each block's 72 fp16
+                    check(lib.mia_scale_rows_f16(base, n16 // 2, 2, 36, 0, 1.0 / 16384, None))
+                else:                # d: fp16 104 of each block's 105
+                    check(lib.mia_scale_rows_f16(base, n16, 1, 105, 104, 1.0 / 65536, None))
+        self.norms = DeviceBuffer.from_array(
+            (1.0 + 0.1 * g.standard_normal((N_LAYERS, 2, DIM))).astype(np.float32))
+        # decode: Q8_0 inputs (the 4096-wide and 14336-wide vectors of each layer)
+        self.x_dim = DeviceBuffer.from_array(g.standard_normal(DIM, np.float32))
+        self.x_hid = DeviceBuffer.from_array(g.standard_normal(HIDDEN, np.float32))
+        self.q8_dim, self.q8_hid = DeviceBuffer(DIM // 32 * 36), DeviceBuffer(HIDDEN // 32 * 36)
+        check(lib.mia_quantize_q8_0(self.x_dim.ptr, self.q8_dim.ptr, DIM, None))
+        check(lib.mia_quantize_q8_0(self.x_hid.ptr, self.q8_hid.ptr, HIDDEN, None))
+        self.y = DeviceBuffer(N_LAYERS * (DIM * 3 + 2 * KV_DIM + 2 * HIDDEN) * 4)
+        # prefill
+        lay = PF_M * KV_DIM
+        self.kc = DeviceBuffer(N_LAYERS * lay * 2)
+        self.vc = DeviceBuffer(N_LAYERS * lay * 2)
+        self.kc.zero()
+        self.vc.zero()
+        for l in range(N_LAYERS):
+            check(lib.mia_fill_normal_f16(self.kc.ptr + l * lay * 2, PF_START * KV_DIM, 4000 + l, None))
+            check(lib.mia_fill_normal_f16(self.vc.ptr + l * lay * 2, PF_START * KV_DIM, 5000 + l, None))
+        self.X = DeviceBuffer.from_array(g.standard_normal((PF_S, DIM)).astype(np.float32))
+        self.th = DeviceBuffer.from_array(theta_inv())
+        self.lws = []
+        for l in range(N_LAYERS):
+            p = {n: self.w.ptr + l * self.lw_bytes + self.offs[n] for n, _, _, _ in KM_SIZES}
+            t = {n: tt for n, _, _, tt in KM_SIZES}
+            nb = self.norms.ptr + l * 2 * DIM * 4
+            self.lws.append(mia.LayerWeightsTyped(
+                *(p[n] for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3")),
+                *(t[n] for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3")), nb, nb + DIM * 4))
+        check(lib.mia_device_sync())
+        self.decode_bytes = sum(km_bytes(r, c, t) for _, r, c, t in KM_SIZES)
+
+    def decode_step(self) -> None:
+        y = self.y.ptr
+        for l in range(N_LAYERS):
+            for name, r, c, t in KM_SIZES:
+                x = self.q8_hid.ptr if c == HIDDEN else self.q8_dim.ptr
+                check(self.lib.mia_matvec_q8(self.w.ptr + l * self.lw_bytes + self.offs[name], t,
+                                             x, y, r, c, None), "matvec_q8")
+                y += r * 4
+
+    def prefill_step(self) -> None:
+        lay = PF_M * KV_DIM * 2
+        for l in range(N_LAYERS):
+            check(self.lib.mia_prefill_layer_typed(
+                self.X.ptr, ctypes.byref(self.lws[l]), self.th.ptr, self.kc.ptr + l * lay,
+                self.vc.ptr + l * lay, DIM, HIDDEN, N_HEADS, N_KV, 1e-5, PF_M, PF_START, PF_S,
+                None), "prefill_layer_typed")
+
+
+def typed_leg(lib, steps: int, warmup: int) -> dict:
+    tl = TypedLayers(lib)
+    dec_ms = timed(lib, tl.decode_step, steps, warmup)
+    n, k_ms = kernel_stats(lib, tl.decode_step, steps, 5)
+    per_launch = tl.decode_bytes / 7                 # mean weight bytes per launch
+    kern_gbs = per_launch / (k_ms * 1e-3) / 1e9
+    pf_steps = max(steps // 8, 2)
+    pf_ms = timed(lib, tl.prefill_step, pf_steps, 1)
+    layer_flop = LAYER_GEMM_FLOP + PF_FLOP_PER_LAYER
+    out = {
+        "workload": "Q4_K_M weights (Q4_K; Q6_K for Wv and W2), 32 layers, 4.45 GB",
+        "decode_projections": {
+            "workload": "7 matvecs per layer on Q8_0 inputs (mia_matvec_q8: Wq, Wk, Wv, Wo, W1, "
+                        "W2, W3), 32 layers",
+            "value": round(N_LAYERS * tl.decode_bytes / (dec_ms * 1e-3) / 1e9, 2), "unit": "GB/s",
+            "ms_per_step": round(dec_ms, 4), "weight_bytes_per_layer": tl.decode_bytes,
+            "matvec_kernel_us": round(k_ms * 1e3, 3), "matvec_launches": n,
+            "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
+                         "traffic": None,
+                         "note": "mean weight bytes per launch over the kernel's mean duration"},
+        },
+        "prefill_layer": {
+            "workload": "mia_prefill_layer_typed x 32, S 512 after 1536 cached: each matrix "
+                        "dequantised to fp32 and multiplied by rocBLAS sgemm",
+            "value": round(N_LAYERS * layer_flop / (pf_ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
+            "ms_per_step": round(pf_ms, 3), "flop_per_layer": layer_flop,
+        },
+    }
+    del tl
+    return out
+
+
 def cpu_baseline_prefill_layer():
     """The oracle's prefill layer (timing build, OpenMP) on 1 of the 32 layers."""
     sys.path.insert(0, os.path.join(REPO, "tests"))
@@ -815,6 +936,8 @@ def main() -> int:
     ap.add_argument("--skip-configs", action="store_true",
                     help="skip the side configs 1, 2 and 5 (profiling)")
     ap.add_argument("--skip-peaks", action="store_true", help="skip the measured-peaks leg")
+    ap.add_argument("--skip-typed", action="store_true",
+                    help="skip the Q4_K_M weight leg (projections and prefill layer)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 5 device-to-device copies of 512 MiB (a copy kernel of known "
                          "size, to scale HBM byte counters)")
@@ -961,6 +1084,16 @@ def main() -> int:
         }
         del pl
 
+    typed = None
+    if not args.skip_typed:
+        log("typed weights: Q4_K_M decode projections and prefill layer, 32 layers")
+        typed = typed_leg(lib, args.steps, args.warmup)
+        log(f"typed weights: decode projections {typed['decode_projections']['ms_per_step']:.3f} "
+            f"ms/step ({typed['decode_projections']['value']:.0f} GB/s, kernel "
+            f"{typed['decode_projections']['roofline']['achieved']:.0f} GB/s); prefill layer "
+            f"{typed['prefill_layer']['ms_per_step']:.2f} ms/step "
+            f"({typed['prefill_layer']['value']:.1f} TFLOP/s)")
+
     configs = None
     if not args.skip_configs and not args.skip_decode:
         log("other configs: 1 (L 513), 2 (32 x L 4097), 5 (32 x verify S 8 on a wrapped ring)")
@@ -1071,6 +1204,7 @@ def main() -> int:
         "projections": projections,
         "gguf": gguf,
         "prefill_layer": layer,
+        "typed_weights": typed,
     }
     print(json.dumps(line), flush=True)
     return 0

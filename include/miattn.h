@@ -351,9 +351,15 @@ int mia_matvec_q8(const void *W, int type, const void *x_q8, float *y, int out_d
 
 /* tiled_q4_gemm for every type (mistral/mistral_ane_prefill.h:1018-1042):
  * Y[S][out_dim] = X[S][in_dim] . W^T, fp32 X and Y (dev, 16-byte aligned).
- * Q4_0 is mia_q4_0_gemm_f32.  The other types are dequantised into a
- * per-device fp32 area of out_dim * in_dim * 4 bytes and multiplied by
- * rocBLAS sgemm in fp32, as the reference hands them to cblas_sgemm. */
+ * Q4_0 is mia_q4_0_gemm_f32.  The other types multiply on fp16 MFMA with fp32
+ * accumulation (rocBLAS gemm_ex), within fp32 rounding of the reference's
+ * dequantise + cblas_sgemm: X is split into fp16 hi + lo halves, as for Q4_0;
+ * Q4_K and F16 weights are fp16 values and enter exactly; Q6_K and F32
+ * weights are scaled per row by a power of two and split into hi + lo halves
+ * (2^-22 relative).  Per-device work areas: out_dim * in_dim * 2 bytes
+ * (twice that for Q6_K / F32) and 12 * S * out_dim bytes.  Range as
+ * mia_q4_0_gemm_f32's: every |x| below 65504, below 2^-3 carried to 2^-25
+ * absolute. */
 int mia_gemm_f32(const void *W, int type, const float *X, float *Y, int out_dim, int in_dim,
                  int S, void *stream);
 
@@ -368,8 +374,9 @@ typedef struct {
 /* blas_prefill_layer (mistral/mistral_ane_prefill.h:1081-1110) with each
  * matrix of its own type, as mia_prefill_layer otherwise (same arguments,
  * attention step and ring semantics).  A layer whose seven matrices are all
- * Q4_0 is mia_prefill_layer; any other mix multiplies every matrix as
- * mia_gemm_f32, with the activations in fp32 and the SwiGLU product
+ * Q4_0 is mia_prefill_layer; any other mix multiplies each matrix as
+ * mia_gemm_f32 does for its type, with the activations in fp32 and the
+ * SwiGLU product
  * gate * (1 / (1 + exp(-gate))) * up (silu_mul_neon, mistral_model.h:
  * 174-199) in between. */
 int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const float *theta_inv,

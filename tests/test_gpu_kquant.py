@@ -7,10 +7,13 @@ types.
 Bars:
 - Dequantisation is bit-exact (the Q4_K fp16 steps, the Q6_K value mapping,
   fp16 and fp32 rows).
-- Matvec and GEMM rows: the weights are exact and only the fp32 order of a
-  row's sum differs from the oracle's, so |gpu - oracle| <= 2 * K * 2^-24 *
+- Matvec rows: the weights are exact and only the fp32 order of a row's sum
+  differs from the oracle's, so |gpu - oracle| <= 2 * K * 2^-24 *
   sum_k |w_k x_k| (both within K * 2^-24 of the exact sum); a lost or doubled
   group, a wrong nibble, scale or min exceeds that by orders of magnitude.
+  GEMM rows to the same bound: x enters as fp16 hi + lo (2^-22 relative,
+  2^-25 absolute below 2^-3) and Q6_K / F32 weights as row-scaled hi + lo
+  (2^-22 relative), both far inside it.
   The attention tolerance (2e-3 abs + 1e-2 rel) is checked as well.
 - The layer normwise within 2e-3 of the oracle (the attention's fp16 ring and
   operands carried through Wo and the FFN), to fp32 level when Wo is zero;
@@ -174,6 +177,35 @@ def test_gemm_f32(t, S, N, K):
     got = gpu_gemm(W, t, X, N, K)
     ref = O.typed_gemm(W, t, N, K, X)
     _assert_close(got, ref, _bound(O.dequant_typed(W, t, N, K), X), f"gemm {NAMES[t]}")
+
+
+@pytest.mark.parametrize("t", [O.TYPE_F32, O.TYPE_Q6_K])
+def test_gemm_rows_of_every_magnitude(t):
+    # the row-scaled hi + lo split of weights that are not fp16 values: rows
+    # from 1e-7 to 1e4 in size (F32), Q6_K steps from fp16 subnormals up, an
+    # all-zero row, and a single-token batch
+    G.say(f"kquant: gemm {NAMES[t]} row magnitudes")
+    g = np.random.default_rng(600 + t)
+    N, K = 64, 512
+    if t == O.TYPE_F32:
+        w = g.standard_normal((N, K)).astype(np.float32)
+        w *= (10.0 ** np.linspace(-7, 4, N)).astype(np.float32)[:, None]
+        w[5] = 0
+        W = w.view(np.uint8).reshape(N, K * 4)
+    else:
+        W = O.make_q6_k(g, N, K)
+        d = (2.0 ** np.linspace(-24, 2, N)).astype(np.float16)     # subnormal to 4
+        Wb = W.reshape(N, K // 256, 210)
+        Wb[:, :, 208:210] = d.view(np.uint8).reshape(N, 1, 2)
+        Wb[5, :, 208:210] = 0
+        W = Wb.reshape(N, -1)
+    for S in (1, 9):
+        X = g.standard_normal((S, K)).astype(np.float32)
+        got = gpu_gemm(W, t, X, N, K)
+        ref = O.typed_gemm(W, t, N, K, X)
+        _assert_close(got, ref, _bound(O.dequant_typed(W, t, N, K), X),
+                      f"gemm {NAMES[t]} S={S}")
+        assert np.all(got[:, 5] == 0)
 
 
 def test_gemm_q4_0_is_the_q4_0_gemm():
