@@ -193,6 +193,13 @@ _SIGS = {
         [_P, POINTER(LayerWeightsTyped), _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,
          c_int, c_int, _P],
     ),
+    # KV-ring snapshots
+    "mia_kv_snapshot_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "mia_kv_snapshot_save": (c_int, [_P, c_size_t, _P, _P, c_int, c_int, c_int, c_int, c_int,
+                                     c_int]),
+    "mia_kv_snapshot_load": (c_int, [_P, c_size_t, _P, _P, c_int, c_int, c_int, c_int,
+                                     POINTER(c_int), POINTER(c_int)]),
+    "mia_kv_snapshot_info": (c_int, [_P, c_size_t] + [POINTER(c_int)] * 6),
     # GGUF weight files (include/mia_gguf.h); the config struct is MistralConfig's layout
     "mia_gguf_open": (c_int, [ctypes.c_char_p, POINTER(c_void_p)]),
     "mia_gguf_close": (None, [_P]),
@@ -244,6 +251,8 @@ _SIGS = {
     ),
     "mia_dropin_verify_commit": (None, [POINTER(KVCache), c_int, c_int]),
     "mia_dropin_quantize_q8_0": (None, [_P, _P, c_int]),
+    "mia_dropin_kv_save": (c_int, [POINTER(KVCache), ctypes.c_char_p]),
+    "mia_dropin_kv_load": (c_int, [POINTER(KVCache), ctypes.c_char_p]),
     "mia_dropin_q4_matvec_sdot_parallel": (None, [_P, ctypes.c_uint32, _P, _P, c_int, c_int]),
     "mia_dropin_q4_matvec_sdot_parallel_fused_qkv": (
         None,

@@ -182,9 +182,9 @@ __device__ __forceinline__ u4 load_u4_unaligned(const uint8_t *p) {
   return v;
 }
 
-// The K-quant matvec: each wave takes kKqRows consecutive rows and lane l the
+// The K-quant matvec: each wave takes R consecutive rows and lane l the
 // 32-value groups l, l + 64, ... of all of them, so that the lane's 32 x
-// values are loaded (and, from Q8_0 blocks, formed) once for kKqRows rows.
+// values are loaded (and, from Q8_0 blocks, formed) once for R rows.
 //   Q4_K: the group's 32 nibbles as packed fp16 pairs (0x6400 | n is
 //         1024 + n), then p = fl16(n * vd) as one packed fma, (1024 + n) * vd
 //         - 1024 * vd, whose exact value is n * vd (1024 * vd is exact in
@@ -194,7 +194,6 @@ __device__ __forceinline__ u4 load_u4_unaligned(const uint8_t *p) {
 //         sub-block, times d * scale: w = d * scale * q is exact in fp32
 //         (11 + 7 + 5 significant bits), so this is the reference's sum
 //         reassociated.
-constexpr int kKqRows = 4;
 
 template <int E>
 __device__ __forceinline__ float ubyte_f32(unsigned q) {

@@ -154,6 +154,14 @@ void mia_dropin_q4_matvec_sdot_parallel_fused_qkv(const void *Wq, const void *Wk
                                                   float *yk, float *yv, int dim, int kv_dim,
                                                   int in_dim);
 
+/* The cache saved to / resumed from a file in the snapshot format of
+ * mia_kv_snapshot_save (no counterpart in the reference, whose cache lives and
+ * dies with the process): k_cache, v_cache, pos and len.  kv_load needs a
+ * cache of the same shape from kv_alloc and sets its pos and len.  They
+ * return a mia_status (and never abort). */
+int mia_dropin_kv_save(const KVCache *c, const char *path);
+int mia_dropin_kv_load(KVCache *c, const char *path);
+
 #ifndef MIA_DROPIN_NO_REFERENCE_NAMES
 /* Reference names (mistral/kv_cache.h, mistral_model.h, mistral_ane_prefill.h). */
 static inline KVCache kv_alloc(int n_layers, int n_kv_heads, int head_dim, int max_seq) {

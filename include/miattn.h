@@ -384,6 +384,35 @@ int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const f
                             int n_heads, int n_kv_heads, float eps, int max_seq, int start_pos,
                             int S, void *stream);
 
+/* ---- KV-ring snapshots (no counterpart in the reference) ------------------ */
+/* The rings of all layers (k_cache / v_cache: device memory holding
+ * [n_layers][max_seq][n_kv_heads][head_dim] fp16 each, the KVCache arrays of
+ * mistral/kv_cache.h:10-20) with the cache's sizes and its pos / len cursors,
+ * as one host byte string for saving and resuming a session.  Little-endian:
+ * a 64-byte header ("MIAKVRG1", u32 64, u32 2, the seven int fields of
+ * KVCache in its order: n_layers, n_kv_heads, head_dim, max_seq, kv_dim, pos,
+ * len; u32 0; u64 bytes of one array; u64 0), then k_cache's bytes, then
+ * v_cache's, each exactly as it lies in memory.  Synchronous. */
+
+/* Bytes of a snapshot of this shape (0 for a non-positive size). */
+size_t mia_kv_snapshot_bytes(int n_layers, int n_kv_heads, int head_dim, int max_seq);
+
+/* Writes the snapshot into dst (host, dst_bytes >= mia_kv_snapshot_bytes). */
+int mia_kv_snapshot_save(void *dst, size_t dst_bytes, const uint16_t *k_cache,
+                         const uint16_t *v_cache, int n_layers, int n_kv_heads, int head_dim,
+                         int max_seq, int pos, int len);
+
+/* Reads a snapshot into rings of the same shape (MIA_ERR_INVALID when the
+ * header is not a snapshot's, the shape differs or src is truncated); pos and
+ * len (may be NULL) receive the saved cursors. */
+int mia_kv_snapshot_load(const void *src, size_t src_bytes, uint16_t *k_cache, uint16_t *v_cache,
+                         int n_layers, int n_kv_heads, int head_dim, int max_seq, int *pos,
+                         int *len);
+
+/* The header's fields (any output may be NULL); no device work. */
+int mia_kv_snapshot_info(const void *src, size_t src_bytes, int *n_layers, int *n_kv_heads,
+                         int *head_dim, int *max_seq, int *pos, int *len);
+
 #ifdef __cplusplus
 }
 #endif
