@@ -802,6 +802,58 @@ def cpu_baseline_prefill_layer():
                       "GEMMs and attention, OpenMP over tokens / heads"}
 
 
+def cpu_baseline_typed(n_layers: int = 2) -> dict:
+    """The oracle on the Q4_K_M leg's shapes: the typed matvec on Q8_0 inputs
+    (one thread, as the oracle's typed matvec is) over n_layers layers' seven
+    matrices, and the typed prefill layer (timing build, OpenMP) on 1 of the
+    32 layers."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import _oracle as O
+
+    g = np.random.default_rng(16)
+    types = {n: t for n, _, _, t in KM_SIZES}
+    Ws = [{n: O.make_typed(g, t, r, c, d_scale=0.07) for n, r, c, t in KM_SIZES}
+          for _ in range(n_layers)]
+    xq = {DIM: O.quantize_q8_0(g.standard_normal(DIM).astype(np.float32)),
+          HIDDEN: O.quantize_q8_0(g.standard_normal(HIDDEN).astype(np.float32))}
+    t0 = time.perf_counter()
+    for W in Ws:
+        for n, r, c, t in KM_SIZES:
+            O.typed_matvec_q8(W[n], t, xq[c], r, c)
+    dt = time.perf_counter() - t0
+    nbytes = n_layers * sum(km_bytes(r, c, t) for _, r, c, t in KM_SIZES)
+    dec = {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+           "sample": f"{n_layers} of 32 layers, the seven matvecs on Q8_0 inputs, oracle "
+                     f"(scalar, one thread)"}
+    W = dict(Ws[0])
+    W["rms_att"] = np.ones(DIM, np.float32)
+    W["rms_ffn"] = np.ones(DIM, np.float32)
+    kc = np.zeros((PF_M, KV_DIM), np.uint16)
+    vc = np.zeros((PF_M, KV_DIM), np.uint16)
+    kc[:PF_START] = g.standard_normal((PF_START, KV_DIM), np.float32).astype(np.float16).view(np.uint16)
+    vc[:PF_START] = g.standard_normal((PF_START, KV_DIM), np.float32).astype(np.float16).view(np.uint16)
+    X = g.standard_normal((PF_S, DIM)).astype(np.float32)
+    threads = O.num_threads(fast=True)
+    lib = O.load(True)
+    kv = O.make_kv(kc, vc, N_KV, HD, PF_M)
+    arrs = {k: np.ascontiguousarray(v) for k, v in W.items()}
+    lw = O.OraLayerWeightsTyped(*[arrs[n].ctypes.data for n in O.MATS],
+                                *[types[n] for n in O.MATS], arrs["rms_att"].ctypes.data,
+                                arrs["rms_ffn"].ctypes.data)
+    th = theta_inv()
+    t0 = time.perf_counter()
+    rc = lib.ora_prefill_layer_typed(ctypes.byref(lw), ctypes.byref(kv), X.ctypes.data, 0,
+                                     PF_START, PF_S, DIM, HIDDEN, N_HEADS, N_KV, 1e-5,
+                                     th.ctypes.data, threads)
+    dt = time.perf_counter() - t0
+    assert rc == 0
+    pf = {"value": round((LAYER_GEMM_FLOP + PF_FLOP_PER_LAYER) / dt / 1e12, 4),
+          "unit": "TFLOP/s", "cores": threads, "kind": "port",
+          "sample": "1 of 32 layers (S 512 after 1536), oracle timing build: dequantised fp32 "
+                    "GEMMs and attention, OpenMP"}
+    return {"decode_projections": dec, "prefill_layer": pf}
+
+
 def gguf_upload(lib, n_layers: int = 8):
     """A GGUF file holding n_layers layers of Mistral-7B attention weights
     (Q4_0, written to a temp dir from the format): time to open (map + parse)
@@ -1161,6 +1213,10 @@ def main() -> int:
         if projections is not None:
             log("cpu baseline: projections sample")
             projections["cpu_baseline"] = cpu_baseline_projections()
+        if typed is not None:
+            log("cpu baseline: Q4_K_M projections and prefill layer samples")
+            for k, v in cpu_baseline_typed().items():
+                typed[k]["cpu_baseline"] = v
         if configs is not None:
             log("cpu baseline: configs 1, 2, 5")
             for k, v in cpu_other_configs().items():
