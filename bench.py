@@ -754,8 +754,9 @@ def typed_leg(lib, steps: int, warmup: int) -> dict:
             "matvec_kernel_us": round(k_ms * 1e3, 3), "matvec_launches": n,
             "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
-                         "traffic": None,
-                         "note": "mean weight bytes per launch over the kernel's mean duration"},
+                         "traffic": load_traffic("kquant_matvec"),
+                         "note": "mean weight bytes per launch over the kernel's mean duration; "
+                                 "traffic: FETCH + WRITE bytes per launch, mean over the seven"},
         },
         "prefill_layer": {
             "workload": "mia_prefill_layer_typed x 32, S 512 after 1536 cached: each matrix "
