@@ -114,6 +114,63 @@ def test_matvec_f32(t, rows, cols):
     _assert_close(got, ref, _bound(O.dequant_typed(W, t, rows, cols), x), f"matvec {NAMES[t]}")
 
 
+def _wide_q4_k(g, rows, cols):
+    """Q4_K rows with large block scales: d up to 3.7 (sub-block steps vd far
+    above 63.5) in half the rows, so waves mix both forms of the kernel's
+    n * vd, and dmin up to 61.3."""
+    W = O.make_q4_k(g, rows, cols)
+    Wb = W.reshape(rows, cols // 256, 144)
+    Wb[::2, :, 0:2] = np.frombuffer(np.float16(3.7).tobytes(), np.uint8)
+    Wb[1::4, :, 2:4] = np.frombuffer(np.float16(61.3).tobytes(), np.uint8)
+    return Wb.reshape(rows, -1)
+
+
+@pytest.mark.parametrize("t,big", [(O.TYPE_Q4_K, False), (O.TYPE_Q4_K, True),
+                                   (O.TYPE_Q6_K, False), (O.TYPE_F16, False),
+                                   (O.TYPE_F32, False), (O.TYPE_Q4_0, False)])
+@pytest.mark.parametrize("rows", [37, 4096, 14336])
+def test_matvec_weights_exact(t, big, rows):
+    # x = a one-hot vector e_k: y = column k of W, every product w * 1 and
+    # every sum with zeros exact, so each weight the matvec forms must equal
+    # the reference's (the bound tests cannot see one weight off by an ulp);
+    # compared as values, so that a zero weight may come out as +0 or -0;
+    # fp32 x and Q8_0 x (d = 1, q = 1) alike, rows per wave 1, 2, 4
+    G.say(f"kquant: exact weights {NAMES[t]} big={big} rows={rows}")
+    g = np.random.default_rng(900 + t + rows)
+    cols = 1024
+    W = _wide_q4_k(g, rows, cols) if big else O.make_typed(g, t, rows, cols, d_scale=0.07)
+    Wd = O.dequant_typed(W, t, rows, cols)
+    for k in (0, 1, 17, 31, 32, 255, 256, 511, 1000, 1023):
+        x = np.zeros(cols, np.float32)
+        x[k] = 1.0
+        got = gpu_matvec(W, t, x, rows, cols)
+        assert np.array_equal(got, Wd[:, k]), k
+        if t in (O.TYPE_Q4_K, O.TYPE_Q6_K):
+            xq = O.quantize_q8_0(x)
+            xq["d"][:] = 0.0
+            xq["qs"][:] = 0
+            xq["d"][k // 32] = 1.0
+            xq["qs"][k // 32][k % 32] = 1
+            got = gpu_matvec(W, t, xq, rows, cols, q8=True)
+            assert np.array_equal(got, Wd[:, k]), ("q8", k)
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_F16])
+def test_gemm_weights_exact(t):
+    # one-hot token rows: Y = columns of W; fp16-valued weights enter the GEMM
+    # exactly, so Y is bit-exact
+    G.say(f"kquant: gemm exact weights {NAMES[t]}")
+    g = np.random.default_rng(950 + t)
+    N, K = 96, 512
+    W = _wide_q4_k(g, N, K) if t == O.TYPE_Q4_K else O.make_typed(g, t, N, K)
+    ks = [0, 3, 31, 255, 256, 300, 511]
+    X = np.zeros((len(ks), K), np.float32)
+    X[np.arange(len(ks)), ks] = 1.0
+    got = gpu_gemm(W, t, X, N, K)
+    Wd = O.dequant_typed(W, t, N, K)
+    assert np.array_equal(got, Wd[:, ks].T)
+
+
 @pytest.mark.parametrize("t,rows,cols", [
     (O.TYPE_Q4_K, 4096, 4096), (O.TYPE_Q6_K, 4096, 14336), (O.TYPE_F16, 96, 512),
     (O.TYPE_F32, 40, 1024),
