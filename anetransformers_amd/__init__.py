@@ -188,6 +188,14 @@ _SIGS = {
     "mia_matvec_f32": (c_int, [_P, c_int, _P, _P, c_int, c_int, _P]),
     "mia_matvec_q8": (c_int, [_P, c_int, _P, _P, c_int, c_int, _P]),
     "mia_gemm_f32": (c_int, [_P, c_int, _P, _P, c_int, c_int, c_int, _P]),
+    "mia_gemm_pack_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "mia_gemm_pack": (c_int, [_P, c_int, _P, c_int, c_int, _P]),
+    "mia_gemm_packed_f32": (c_int, [_P, c_int, _P, _P, c_int, c_int, c_int, _P]),
+    "mia_prefill_layer_typed_packed": (
+        c_int,
+        [_P, POINTER(LayerWeightsTyped), _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,
+         c_int, c_int, _P],
+    ),
     "mia_prefill_layer_typed": (
         c_int,
         [_P, POINTER(LayerWeightsTyped), _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,

@@ -1111,28 +1111,42 @@ static int check_typed(int type, int in_dim, const void *W) {
 // (the Xlo . Wlo term, ~2^-22 of the product, is dropped).  rocBLAS is
 // column-major: C^T [N][cols] = (W^T [K][N])^T . B^T [K][cols], so W is the
 // transposed A operand with lda K and C's leading dimension is N.
+static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// The typed GEMM's packed form of a matrix of a type other than Q4_0: the fp16
+// hi plane [N][K], then for Q6_K / F32 the lo plane [N][K] and the row scales
+// [N] fp32, each at a 256-byte aligned offset (launch_typed_split's output).
+static size_t typed_planes_bytes(int type, int N, int K) {
+  const bool lo = !mia::typed_is_f16_exact(type);
+  const size_t bw = al256((size_t)N * K * 2);
+  return lo ? 2 * bw + al256((size_t)N * 4) : bw;
+}
+
 // reuse_x: split_work already holds X's planes (the call before split the
-// same X on this stream), and X is not read.
+// same X on this stream), and X is not read.  packed: W is in the packed form
+// (Q4_0: mia_q4_0_pack_gemm's tile layout; other types: the planes above).
 static int typed_gemm_impl(DevCtx *c, const void *W, int type, const float *X, float *Y, int N,
-                           int K, int S, bool add, hipStream_t s, bool reuse_x = false) {
+                           int K, int S, bool add, hipStream_t s, bool reuse_x = false,
+                           bool packed = false) {
   if (type == MIA_TYPE_Q4_0)
     return gemm_impl(c, W, nullptr, nullptr, N, 0, 0, X, K, S, Y, nullptr, nullptr,
-                     add ? mia::kGemmAdd : mia::kGemmStore, s, reuse_x);
+                     add ? mia::kGemmAdd : mia::kGemmStore, s, reuse_x, nullptr, nullptr, packed);
   const bool lo = !mia::typed_is_f16_exact(type);
-  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
-  const size_t bw = al((size_t)N * K * 2), bc1 = al((size_t)2 * S * N * 4),
-               bc2 = al((size_t)S * N * 4), br = al((size_t)N * 4);
-  if (int rc = ensure_wbuf(c, bw * (lo ? 2 : 1) + bc1 + (lo ? bc2 + br : 0))) return rc;
+  const size_t bp = packed ? 0 : typed_planes_bytes(type, N, K);
+  const size_t bc1 = al256((size_t)2 * S * N * 4), bc2 = al256((size_t)S * N * 4);
+  if (int rc = ensure_wbuf(c, bp + bc1 + (lo ? bc2 : 0))) return rc;
   if (int rc = ensure_split_work(c, (size_t)2 * S * K * sizeof(_Float16))) return rc;
   if (int rc = ensure_blas(c)) return rc;
   char *w = reinterpret_cast<char *>(c->wbuf);
-  _Float16 *whi = reinterpret_cast<_Float16 *>(w);
-  _Float16 *wlo = lo ? reinterpret_cast<_Float16 *>(w + bw) : nullptr;
-  float *C1 = reinterpret_cast<float *>(w + bw * (lo ? 2 : 1));
-  float *C2 = lo ? reinterpret_cast<float *>(w + bw * 2 + bc1) : nullptr;
-  float *rs = lo ? reinterpret_cast<float *>(w + bw * 2 + bc1 + bc2) : nullptr;
+  char *planes = packed ? reinterpret_cast<char *>(const_cast<void *>(W)) : w;
+  const size_t bw = al256((size_t)N * K * 2);
+  _Float16 *whi = reinterpret_cast<_Float16 *>(planes);
+  _Float16 *wlo = lo ? reinterpret_cast<_Float16 *>(planes + bw) : nullptr;
+  float *rs = lo ? reinterpret_cast<float *>(planes + 2 * bw) : nullptr;
+  float *C1 = reinterpret_cast<float *>(w + bp);
+  float *C2 = lo ? reinterpret_cast<float *>(w + bp + bc1) : nullptr;
   _Float16 *xhi = reinterpret_cast<_Float16 *>(c->split_work);  // [2][S][K]: hi, then lo
-  HIP_TRY(mia::launch_typed_split(W, type, whi, wlo, rs, N, K, s));
+  if (!packed) HIP_TRY(mia::launch_typed_split(W, type, whi, wlo, rs, N, K, s));
   if (!reuse_x)
     HIP_TRY(mia::launch_split_hilo(X, (long)S * K, xhi, xhi + (size_t)S * K, c->num_cus, s));
   const float one = 1.0f, zero = 0.0f;
@@ -1210,10 +1224,10 @@ int mia_gemm_f32(const void *W, int type, const float *X, float *Y, int out_dim,
   return typed_gemm_impl(c, W, type, X, Y, out_dim, in_dim, S, false, pick_stream(c, stream));
 }
 
-int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const float *theta_inv,
+static int typed_layer_impl(float *X, const mia_layer_weights_typed *lw, const float *theta_inv,
                             uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden,
                             int n_heads, int n_kv_heads, float eps, int max_seq, int start_pos,
-                            int S, void *stream) {
+                            int S, void *stream, bool packed) {
   if (!lw) return set_err(MIA_ERR_INVALID, "NULL pointer");
   const int types[7] = {lw->wq_type, lw->wk_type, lw->wv_type, lw->wo_type,
                         lw->w1_type, lw->w2_type, lw->w3_type};
@@ -1223,7 +1237,7 @@ int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const f
     const mia_layer_weights q{lw->wq, lw->wk, lw->wv, lw->wo, lw->w1,
                               lw->w2, lw->w3, lw->rms_att, lw->rms_ffn};
     return prefill_layer_impl(X, &q, theta_inv, k_layer, v_layer, dim, hidden, n_heads,
-                              n_kv_heads, eps, max_seq, start_pos, S, stream, false);
+                              n_kv_heads, eps, max_seq, start_pos, S, stream, packed);
   }
   if (!X || !theta_inv || !k_layer || !v_layer) return set_err(MIA_ERR_INVALID, "NULL pointer");
   if (!lw->wq || !lw->wk || !lw->wv || !lw->wo || !lw->w1 || !lw->w2 || !lw->w3 || !lw->rms_att ||
@@ -1236,6 +1250,7 @@ int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const f
   const int kv_dim = n_kv_heads * kHD;
   const void *const ws[7] = {lw->wq, lw->wk, lw->wv, lw->wo, lw->w1, lw->w2, lw->w3};
   const int in_dims[7] = {dim, dim, dim, dim, dim, hidden, dim};
+  const int out_dims[7] = {dim, kv_dim, kv_dim, dim, hidden, dim, hidden};
   for (int i = 0; i < 7; ++i) {
     if (int rc = check_typed(types[i], in_dims[i], ws[i])) return rc;
     // Q4_0 matrices take the fp16-MFMA GEMM (4-byte aligned, in_dim a multiple of 64)
@@ -1243,6 +1258,10 @@ int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const f
       if (in_dims[i] % 64) return set_err(MIA_ERR_UNSUPPORTED, "Q4_0 GEMM needs in_dim %% 64 == 0");
       if ((uintptr_t)ws[i] & 3) return set_err(MIA_ERR_INVALID, "Q4_0 weights must be 4-byte aligned");
     }
+    if (packed && ((uintptr_t)ws[i] & 15))
+      return set_err(MIA_ERR_INVALID, "packed weights must be 16-byte aligned");
+    if (packed && types[i] == MIA_TYPE_Q4_0 && out_dims[i] % 64)
+      return set_err(MIA_ERR_UNSUPPORTED, "packed Q4_0 needs out_dim %% 64 == 0");
   }
   if (hidden <= 0 || (long)S * hidden > INT_MAX || (long)S * dim > INT_MAX)
     return set_err(MIA_ERR_UNSUPPORTED, "bad hidden %d or S x dim above 2^31", hidden);
@@ -1267,10 +1286,11 @@ int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const f
   // mistral_ane_prefill.h:1092-1110
   HIP_TRY(mia::launch_rmsnorm(XN, X, lw->rms_att, dim, S, eps, s));
   // (the normalised rows are split into fp16 planes once for Q, K and V)
-  if (int rc = typed_gemm_impl(c, lw->wq, lw->wq_type, XN, Q, dim, dim, S, false, s)) return rc;
-  if (int rc = typed_gemm_impl(c, lw->wk, lw->wk_type, XN, K, kv_dim, dim, S, false, s, true))
+  if (int rc = typed_gemm_impl(c, lw->wq, lw->wq_type, XN, Q, dim, dim, S, false, s, false, packed))
     return rc;
-  if (int rc = typed_gemm_impl(c, lw->wv, lw->wv_type, XN, V, kv_dim, dim, S, false, s, true))
+  if (int rc = typed_gemm_impl(c, lw->wk, lw->wk_type, XN, K, kv_dim, dim, S, false, s, true, packed))
+    return rc;
+  if (int rc = typed_gemm_impl(c, lw->wv, lw->wv_type, XN, V, kv_dim, dim, S, false, s, true, packed))
     return rc;
   // apply_rope_batch, kv_write_batch, attention_batch, as mia_prefill_layer
   if (int rc = ensure_work(c, (size_t)S * kHD * sizeof(float))) return rc;
@@ -1282,13 +1302,79 @@ int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const f
                           start_pos, S, s))
     return rc;
   // X + A . Wo^T (vDSP_vadd after the GEMM: the sum rounded once more)
-  if (int rc = typed_gemm_impl(c, lw->wo, lw->wo_type, A, X, dim, dim, S, true, s)) return rc;
+  if (int rc = typed_gemm_impl(c, lw->wo, lw->wo_type, A, X, dim, dim, S, true, s, false, packed))
+    return rc;
   HIP_TRY(mia::launch_rmsnorm(XN, X, lw->rms_ffn, dim, S, eps, s));
-  if (int rc = typed_gemm_impl(c, lw->w1, lw->w1_type, XN, G, hidden, dim, S, false, s)) return rc;
-  if (int rc = typed_gemm_impl(c, lw->w3, lw->w3_type, XN, U, hidden, dim, S, false, s, true))
+  if (int rc = typed_gemm_impl(c, lw->w1, lw->w1_type, XN, G, hidden, dim, S, false, s, false, packed))
+    return rc;
+  if (int rc = typed_gemm_impl(c, lw->w3, lw->w3_type, XN, U, hidden, dim, S, false, s, true, packed))
     return rc;
   HIP_TRY(mia::launch_silu_mul(G, U, (long)S * hidden, s));
-  return typed_gemm_impl(c, lw->w2, lw->w2_type, G, X, dim, hidden, S, true, s);
+  return typed_gemm_impl(c, lw->w2, lw->w2_type, G, X, dim, hidden, S, true, s, false, packed);
+}
+
+int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const float *theta_inv,
+                            uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden,
+                            int n_heads, int n_kv_heads, float eps, int max_seq, int start_pos,
+                            int S, void *stream) {
+  return typed_layer_impl(X, lw, theta_inv, k_layer, v_layer, dim, hidden, n_heads, n_kv_heads,
+                          eps, max_seq, start_pos, S, stream, false);
+}
+
+int mia_prefill_layer_typed_packed(float *X, const mia_layer_weights_typed *lw,
+                                   const float *theta_inv, uint16_t *k_layer, uint16_t *v_layer,
+                                   int dim, int hidden, int n_heads, int n_kv_heads, float eps,
+                                   int max_seq, int start_pos, int S, void *stream) {
+  return typed_layer_impl(X, lw, theta_inv, k_layer, v_layer, dim, hidden, n_heads, n_kv_heads,
+                          eps, max_seq, start_pos, S, stream, true);
+}
+
+size_t mia_gemm_pack_bytes(int type, int out_dim, int in_dim) {
+  if (out_dim <= 0 || mia::typed_row_bytes(type, in_dim) == 0) return 0;
+  if (type == MIA_TYPE_Q4_0)
+    return (out_dim % 64 || in_dim % 64) ? 0 : (size_t)out_dim * (in_dim / 32) * 18;
+  return typed_planes_bytes(type, out_dim, in_dim);
+}
+
+int mia_gemm_pack(const void *W, int type, void *Wp, int out_dim, int in_dim, void *stream) {
+  if (type == MIA_TYPE_Q4_0) return mia_q4_0_pack_gemm(W, Wp, out_dim, in_dim, stream);
+  if (!W || !Wp) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (out_dim <= 0) return set_err(MIA_ERR_INVALID, "bad out_dim %d", out_dim);
+  if (int rc = check_typed(type, in_dim, W)) return rc;
+  if ((uintptr_t)Wp & 15) return set_err(MIA_ERR_INVALID, "Wp must be 16-byte aligned");
+  const size_t nb = typed_planes_bytes(type, out_dim, in_dim);
+  const uintptr_t wb = (uintptr_t)out_dim * (uintptr_t)mia::typed_row_bytes(type, in_dim);
+  const uintptr_t a = (uintptr_t)W, b = (uintptr_t)Wp;
+  if (a < b + nb && b < a + wb) return set_err(MIA_ERR_INVALID, "W and Wp overlap");
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  char *p = reinterpret_cast<char *>(Wp);
+  const size_t bw = al256((size_t)out_dim * in_dim * 2);
+  const bool lo = !mia::typed_is_f16_exact(type);
+  HIP_TRY(mia::launch_typed_split(W, type, reinterpret_cast<_Float16 *>(p),
+                                  lo ? reinterpret_cast<_Float16 *>(p + bw) : nullptr,
+                                  lo ? reinterpret_cast<float *>(p + 2 * bw) : nullptr, out_dim,
+                                  in_dim, pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_gemm_packed_f32(const void *Wp, int type, const float *X, float *Y, int out_dim,
+                        int in_dim, int S, void *stream) {
+  if (type == MIA_TYPE_Q4_0)
+    return mia_q4_0_gemm_packed_f32(Wp, X, Y, out_dim, in_dim, S, stream);
+  if (!Wp || !X || !Y) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (out_dim <= 0 || in_dim <= 0 || S <= 0)
+    return set_err(MIA_ERR_INVALID, "bad sizes (out_dim=%d in_dim=%d S=%d)", out_dim, in_dim, S);
+  if (mia::typed_row_bytes(type, in_dim) == 0)
+    return set_err(MIA_ERR_UNSUPPORTED, "weight type %d with in_dim %d", type, in_dim);
+  if ((uintptr_t)Wp & 15) return set_err(MIA_ERR_INVALID, "Wp must be 16-byte aligned");
+  if ((long)S * in_dim > INT_MAX || (long)S * out_dim > INT_MAX)
+    return set_err(MIA_ERR_UNSUPPORTED, "S x dim above 2^31");
+  if (int rc = check_align16(X, Y, nullptr, nullptr)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  return typed_gemm_impl(c, Wp, type, X, Y, out_dim, in_dim, S, false, pick_stream(c, stream),
+                         false, true);
 }
 
 int mia_quantize_q8_0(const float *x, void *out_q8, int n, void *stream) {

@@ -663,10 +663,12 @@ def km_bytes(rows: int, cols: int, t: int) -> int:
 class TypedLayers:
     """32 layers of Q4_K_M weights (4.45 GB): the decode projections through
     mia_matvec_q8 (the reference's non-Q4_0 branch of q4_matvec_sdot_parallel,
-    seven launches per layer on Q8_0 inputs) and the prefill layer through
-    mia_prefill_layer_typed (S = 512 after 1536 cached, X carried).  The
-    weight bytes are a seeded fp16 N(0,1) stream with the block scales scaled
-    down so that the activations stay O(1)."""
+    seven launches per layer on Q8_0 inputs) and the prefill layer (S = 512
+    after 1536 cached, X carried) through mia_prefill_layer_typed_packed on
+    the weights packed once (mia_gemm_pack), and through
+    mia_prefill_layer_typed on the GGUF blocks.  The weight bytes are a seeded
+    fp16 N(0,1) stream with the block scales scaled down so that the
+    activations stay O(1)."""
 
     def __init__(self, lib, seed: int = 61):
         self.lib = lib
@@ -716,6 +718,25 @@ class TypedLayers:
                 *(t[n] for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3")), nb, nb + DIM * 4))
         check(lib.mia_device_sync())
         self.decode_bytes = sum(km_bytes(r, c, t) for _, r, c, t in KM_SIZES)
+        # the GEMM operand form, converted once as a loader would (mia_gemm_pack)
+        self.poffs, off = {}, 0
+        for name, r, c, t in KM_SIZES:
+            self.poffs[name] = off
+            off += (lib.mia_gemm_pack_bytes(t, r, c) + 255) // 256 * 256
+        self.plw_bytes = off
+        self.wp = DeviceBuffer(N_LAYERS * self.plw_bytes)
+        self.plws = []
+        for l in range(N_LAYERS):
+            p = {n: self.wp.ptr + l * self.plw_bytes + self.poffs[n] for n, _, _, _ in KM_SIZES}
+            for name, r, c, t in KM_SIZES:
+                check(lib.mia_gemm_pack(self.w.ptr + l * self.lw_bytes + self.offs[name], t,
+                                        p[name], r, c, None), "gemm_pack")
+            lw = self.lws[l]
+            self.plws.append(mia.LayerWeightsTyped(
+                *(p[n] for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3")),
+                lw.wq_type, lw.wk_type, lw.wv_type, lw.wo_type, lw.w1_type, lw.w2_type,
+                lw.w3_type, lw.rms_att, lw.rms_ffn))
+        check(lib.mia_device_sync())
 
     def decode_step(self) -> None:
         y = self.y.ptr
@@ -726,13 +747,14 @@ class TypedLayers:
                                              x, y, r, c, None), "matvec_q8")
                 y += r * 4
 
-    def prefill_step(self) -> None:
+    def prefill_step(self, packed: bool = True) -> None:
         lay = PF_M * KV_DIM * 2
+        fn = self.lib.mia_prefill_layer_typed_packed if packed else self.lib.mia_prefill_layer_typed
+        lws = self.plws if packed else self.lws
         for l in range(N_LAYERS):
-            check(self.lib.mia_prefill_layer_typed(
-                self.X.ptr, ctypes.byref(self.lws[l]), self.th.ptr, self.kc.ptr + l * lay,
-                self.vc.ptr + l * lay, DIM, HIDDEN, N_HEADS, N_KV, 1e-5, PF_M, PF_START, PF_S,
-                None), "prefill_layer_typed")
+            check(fn(self.X.ptr, ctypes.byref(lws[l]), self.th.ptr, self.kc.ptr + l * lay,
+                     self.vc.ptr + l * lay, DIM, HIDDEN, N_HEADS, N_KV, 1e-5, PF_M, PF_START, PF_S,
+                     None), "prefill_layer_typed")
 
 
 def typed_leg(lib, steps: int, warmup: int) -> dict:
@@ -743,6 +765,7 @@ def typed_leg(lib, steps: int, warmup: int) -> dict:
     kern_gbs = per_launch / (k_ms * 1e-3) / 1e9
     pf_steps = max(steps // 8, 2)
     pf_ms = timed(lib, tl.prefill_step, pf_steps, 1)
+    pf_conv_ms = timed(lib, lambda: tl.prefill_step(packed=False), pf_steps, 1)
     layer_flop = LAYER_GEMM_FLOP + PF_FLOP_PER_LAYER
     out = {
         "workload": "Q4_K_M weights (Q4_K; Q6_K for Wv and W2), 32 layers, 4.45 GB",
@@ -759,10 +782,15 @@ def typed_leg(lib, steps: int, warmup: int) -> dict:
                                  "traffic: FETCH + WRITE bytes per launch, mean over the seven"},
         },
         "prefill_layer": {
-            "workload": "mia_prefill_layer_typed x 32, S 512 after 1536 cached: each matrix "
-                        "dequantised to fp32 and multiplied by rocBLAS sgemm",
+            "workload": "mia_prefill_layer_typed_packed x 32, S 512 after 1536 cached: the "
+                        "weights in the GEMM operand form made once at set-up (mia_gemm_pack: "
+                        "fp16 values of Q4_K, row-scaled hi + lo halves of Q6_K, 18 GB), fp16 "
+                        "MFMA GEMMs (rocBLAS gemm_ex) on the activations' hi + lo halves",
             "value": round(N_LAYERS * layer_flop / (pf_ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
             "ms_per_step": round(pf_ms, 3), "flop_per_layer": layer_flop,
+            "per_call_conversion_ms_per_step": round(pf_conv_ms, 3),
+            "per_call_conversion": "mia_prefill_layer_typed on the GGUF blocks: the same "
+                                   "layer converting each matrix on every call",
         },
     }
     del tl
@@ -1145,7 +1173,8 @@ def main() -> int:
             f"ms/step ({typed['decode_projections']['value']:.0f} GB/s, kernel "
             f"{typed['decode_projections']['roofline']['achieved']:.0f} GB/s); prefill layer "
             f"{typed['prefill_layer']['ms_per_step']:.2f} ms/step "
-            f"({typed['prefill_layer']['value']:.1f} TFLOP/s)")
+            f"({typed['prefill_layer']['value']:.1f} TFLOP/s; converting per call "
+            f"{typed['prefill_layer']['per_call_conversion_ms_per_step']:.2f} ms)")
 
     configs = None
     if not args.skip_configs and not args.skip_decode:

@@ -363,6 +363,22 @@ int mia_matvec_q8(const void *W, int type, const void *x_q8, float *y, int out_d
 int mia_gemm_f32(const void *W, int type, const float *X, float *Y, int out_dim, int in_dim,
                  int S, void *stream);
 
+/* The same weights converted once, at load time, into the GEMM's operand form
+ * (no reference counterpart; the reference dequantises per call,
+ * mistral/mistral_ane_prefill.h:1018-1042), so that the per-call conversion
+ * drops out: results are bit-identical to mia_gemm_f32's.  Q4_0 is
+ * mia_q4_0_pack_gemm's tile layout (out_dim and in_dim multiples of 64, the
+ * size of the GGUF form); Q4_K and F16 become their fp16 values [out_dim]
+ * [in_dim] (4x / 1x the Q4_K / F16 bytes); Q6_K and F32 the row-scaled fp16
+ * hi and lo halves and the row scales.  mia_gemm_pack_bytes gives the size
+ * (0 for a shape the GEMM does not take); Wp is 16-byte aligned device memory
+ * not overlapping W. */
+size_t mia_gemm_pack_bytes(int type, int out_dim, int in_dim);
+int mia_gemm_pack(const void *W, int type, void *Wp, int out_dim, int in_dim, void *stream);
+/* mia_gemm_f32 on a packed matrix. */
+int mia_gemm_packed_f32(const void *Wp, int type, const float *X, float *Y, int out_dim,
+                        int in_dim, int S, void *stream);
+
 /* One layer's weights with their types (LayerWeights, mistral/
  * mistral_model.h:16-28). */
 typedef struct {
@@ -383,6 +399,13 @@ int mia_prefill_layer_typed(float *X, const mia_layer_weights_typed *lw, const f
                             uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden,
                             int n_heads, int n_kv_heads, float eps, int max_seq, int start_pos,
                             int S, void *stream);
+
+/* mia_prefill_layer_typed with the seven matrices in mia_gemm_pack's form
+ * (16-byte aligned; the types as before): bit-identical results. */
+int mia_prefill_layer_typed_packed(float *X, const mia_layer_weights_typed *lw,
+                                   const float *theta_inv, uint16_t *k_layer, uint16_t *v_layer,
+                                   int dim, int hidden, int n_heads, int n_kv_heads, float eps,
+                                   int max_seq, int start_pos, int S, void *stream);
 
 /* ---- KV-ring snapshots (no counterpart in the reference) ------------------ */
 /* The rings of all layers (k_cache / v_cache: device memory holding

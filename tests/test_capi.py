@@ -266,6 +266,33 @@ _Static_assert(sizeof(mia_layer_weights_typed) == %d, "size");
         subprocess.run([CLANG, "-std=c11", "-fsyntax-only", "-I", INCLUDE, str(src)], check=True)
 
 
+def test_typed_pack_sizes_and_errors_without_device_work():
+    lib = mia.load()
+    a = lambda n: (n + 255) // 256 * 256
+    assert lib.mia_gemm_pack_bytes(mia.TYPE_Q4_K, 4096, 4096) == a(4096 * 4096 * 2)
+    assert lib.mia_gemm_pack_bytes(mia.TYPE_F16, 100, 96) == a(100 * 96 * 2)
+    assert lib.mia_gemm_pack_bytes(mia.TYPE_Q6_K, 4096, 14336) == \
+        2 * a(4096 * 14336 * 2) + a(4096 * 4)
+    assert lib.mia_gemm_pack_bytes(mia.TYPE_F32, 40, 1024) == 2 * a(40 * 1024 * 2) + a(40 * 4)
+    assert lib.mia_gemm_pack_bytes(mia.TYPE_Q4_0, 4096, 4096) == 4096 * 128 * 18
+    assert lib.mia_gemm_pack_bytes(mia.TYPE_Q4_0, 100, 4096) == 0        # tile layout: x 64
+    assert lib.mia_gemm_pack_bytes(mia.TYPE_Q4_K, 64, 100) == 0
+    assert lib.mia_gemm_pack_bytes(3, 64, 256) == 0
+    buf = np.zeros(4096, np.float32)
+    p = (buf.ctypes.data + 15) // 16 * 16
+    assert lib.mia_gemm_pack(p, mia.TYPE_Q4_K, p + 8, 4, 256, None) == mia.MIA_ERR_INVALID
+    assert lib.mia_gemm_pack(p, mia.TYPE_Q4_K, p + 512, 4, 256, None) == mia.MIA_ERR_INVALID
+    assert b"overlap" in lib.mia_last_error()
+    assert lib.mia_gemm_packed_f32(p + 8, mia.TYPE_Q4_K, p, p, 4, 256, 2, None) == \
+        mia.MIA_ERR_INVALID
+    lw = mia.LayerWeightsTyped(*([p] * 7), *([mia.TYPE_Q4_K] * 7), p, p)
+    lw.wo = p + 32 + 2                      # Q6_K-legal alignment, not the packed form's
+    lw.wo_type = mia.TYPE_Q6_K
+    assert lib.mia_prefill_layer_typed_packed(p, ctypes.byref(lw), p, p, p, 512, 1024, 4, 1,
+                                              1e-5, 64, 0, 4, None) == mia.MIA_ERR_INVALID
+    assert b"16-byte" in lib.mia_last_error()
+
+
 def test_q4_argument_errors_without_device_work():
     lib = mia.load()
     buf = np.zeros(64, np.float32)

@@ -265,6 +265,35 @@ def test_gemm_rows_of_every_magnitude(t):
         assert np.all(got[:, 5] == 0)
 
 
+def gpu_pack(W, t, N, K):
+    L = G.lib()
+    dw = DB.from_array(W)
+    nb = L.mia_gemm_pack_bytes(t, N, K)
+    assert nb > 0
+    dp = DB(nb)
+    check(L.mia_gemm_pack(dw.ptr, t, dp.ptr, N, K, None), "pack")
+    check(L.mia_stream_sync(None), "sync")
+    return dp
+
+
+@pytest.mark.parametrize("t,S,N,K", [
+    (O.TYPE_Q4_K, 64, 1024, 4096), (O.TYPE_Q6_K, 32, 4096, 14336), (O.TYPE_F16, 5, 96, 512),
+    (O.TYPE_F32, 3, 40, 256), (O.TYPE_Q4_0, 20, 1024, 4096),
+])
+def test_packed_gemm_is_bit_identical(t, S, N, K):
+    G.say(f"kquant: packed gemm {NAMES[t]} S={S} {N}x{K}")
+    L = G.lib()
+    g = np.random.default_rng(700 + S + N + t)
+    W = O.make_typed(g, t, N, K, d_scale=0.07)
+    X = g.standard_normal((S, K)).astype(np.float32)
+    dp = gpu_pack(W, t, N, K)
+    dx, dy = DB.from_array(X), DB(S * N * 4)
+    check(L.mia_gemm_packed_f32(dp.ptr, t, dx.ptr, dy.ptr, N, K, S, None), "packed gemm")
+    check(L.mia_stream_sync(None), "sync")
+    got = dy.download((S, N), np.float32)
+    assert np.array_equal(got.view(np.uint32), gpu_gemm(W, t, X, N, K).view(np.uint32))
+
+
 def test_gemm_q4_0_is_the_q4_0_gemm():
     G.say("kquant: gemm Q4_0 == mia_q4_0_gemm_f32")
     L = G.lib()
@@ -356,6 +385,35 @@ def test_prefill_layer_typed_matches_oracle(mix, dim, hidden, nh, nkv, M, start,
         ulp = np.spacing(np.maximum(np.abs(fa), np.abs(fb)).astype(np.float16)).astype(np.float32)
         row = np.abs(fb).max(axis=1, keepdims=True)
         assert np.all(np.abs(fa - fb) <= ulp + 1e-5 * row)
+
+
+@pytest.mark.parametrize("mix", ["q4_k_m", "mixed"])
+def test_prefill_layer_typed_packed_is_bit_identical(mix):
+    G.say(f"kquant: packed layer {mix}")
+    L = G.lib()
+    dim, hidden, nh, nkv, M, start, S = 512, 1024, 4, 1, 64, 10, 20
+    types = MIXES[mix]
+    g = np.random.default_rng(71 + len(mix))
+    W = _layer(g, types, dim, hidden, nh, nkv)
+    kc, vc = D.ring(g, M, kv_dim=dim // nh * nkv, filled=start)
+    X = g.standard_normal((S, dim)).astype(np.float32)
+    th = O.theta_inv(D.THETA, 128)
+    want, kc_w, vc_w = _run_layer(L, W, types, X, th, kc, vc, dim, hidden, nh, nkv, M, start, S)
+    kvd = dim // nh * nkv
+    shapes = {"wq": (dim, dim), "wk": (kvd, dim), "wv": (kvd, dim), "wo": (dim, dim),
+              "w1": (hidden, dim), "w3": (hidden, dim), "w2": (dim, hidden)}
+    packs = {n: gpu_pack(W[n], types[n], *shapes[n]) for n in O.MATS}
+    norms = {n: DB.from_array(W[n]) for n in ("rms_att", "rms_ffn")}
+    lw = mia.LayerWeightsTyped(*[packs[n].ptr for n in O.MATS], *[types[n] for n in O.MATS],
+                               norms["rms_att"].ptr, norms["rms_ffn"].ptr)
+    dX, dth, dkc, dvc = DB.from_array(X), DB.from_array(th), DB.from_array(kc), DB.from_array(vc)
+    check(L.mia_prefill_layer_typed_packed(dX.ptr, ctypes.byref(lw), dth.ptr, dkc.ptr, dvc.ptr,
+                                           dim, hidden, nh, nkv, 1e-5, M, start, S, None),
+          "layer_typed_packed")
+    check(L.mia_stream_sync(None), "sync")
+    assert np.array_equal(dX.download(X.shape, np.float32).view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(dkc.download(kc.shape, np.uint16), kc_w)
+    assert np.array_equal(dvc.download(vc.shape, np.uint16), vc_w)
 
 
 def test_prefill_layer_typed_all_q4_0_is_prefill_layer():
