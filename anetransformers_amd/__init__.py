@@ -168,6 +168,14 @@ _SIGS = {
         c_int,
         [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, _P],
     ),
+    "mia_q4_0_matvec_pair": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, _P]),
+    "mia_q4_0_matvec_pair_f32": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, _P]),
+    "mia_silu_mul_f32": (c_int, [_P, _P, c_long, _P]),
+    "mia_decode_layer": (
+        c_int,
+        [_P, POINTER(LayerWeightsTyped), _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,
+         c_int, _P],
+    ),
     "mia_rmsnorm_f32": (c_int, [_P, _P, _P, c_int, c_int, c_float, _P]),
     "mia_q4_0_gemm_f32": (c_int, [_P, _P, _P, c_int, c_int, c_int, _P]),
     "mia_q4_0_pack_gemm": (c_int, [_P, _P, c_int, c_int, _P]),
@@ -262,6 +270,10 @@ _SIGS = {
     "mia_dropin_kv_save": (c_int, [POINTER(KVCache), ctypes.c_char_p]),
     "mia_dropin_kv_load": (c_int, [POINTER(KVCache), ctypes.c_char_p]),
     "mia_dropin_q4_matvec_sdot_parallel": (None, [_P, ctypes.c_uint32, _P, _P, c_int, c_int]),
+    "mia_dropin_q4_matvec_sdot_parallel_fused_pair": (
+        None,
+        [_P, _P, _P, _P, _P, c_int, c_int],
+    ),
     "mia_dropin_q4_matvec_sdot_parallel_fused_qkv": (
         None,
         [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int],

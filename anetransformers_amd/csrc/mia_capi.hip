@@ -59,6 +59,8 @@ struct DevCtx {
   float *wbuf = nullptr;
   size_t wbuf_bytes = 0;
   rocblas_handle blas = nullptr;
+  void *dl_work = nullptr;  // mia_decode_layer's vectors
+  size_t dl_work_bytes = 0;
   // Opt-in kernel timing: an event pair around the main kernel of each call
   // (kind 0 = decode kernel, 1 = flash kernel, 2 = Q4_0 matvec kernel,
   // 3 = Q4_0 GEMM kernel, 4 = the empty kernel of mia_peak_empty, 5 = the
@@ -188,6 +190,18 @@ int ensure_wbuf(DevCtx *c, size_t bytes) {
     c->wbuf_bytes = 0;
     HIP_TRY(hipMalloc((void **)&c->wbuf, bytes));
     c->wbuf_bytes = bytes;
+  }
+  return MIA_OK;
+}
+
+int ensure_dl_work(DevCtx *c, size_t bytes) {
+  if (bytes > c->dl_work_bytes) {
+    HIP_TRY(hipDeviceSynchronize());
+    if (c->dl_work) HIP_TRY(hipFree(c->dl_work));
+    c->dl_work = nullptr;
+    c->dl_work_bytes = 0;
+    HIP_TRY(hipMalloc(&c->dl_work, bytes));
+    c->dl_work_bytes = bytes;
   }
   return MIA_OK;
 }
@@ -1410,6 +1424,155 @@ int mia_q4_0_matvec_qkv_f32(const void *Wq, const void *Wk, const void *Wv, cons
                             float *yq, float *yk, float *yv, int dim, int kv_dim, int in_dim,
                             void *stream) {
   return q4_impl(Wq, Wk, Wv, nullptr, x, yq, yk, yv, dim, kv_dim, in_dim, stream);
+}
+
+// Two matrices of out_dim rows against one input: W1 (gate) and W3 (up) of
+// the FFN, mistral_model.h:750-811.
+static int q4_pair_impl(const void *W1, const void *W3, const void *x_q8, const float *xf,
+                        float *y1, float *y3, int out_dim, int in_dim, void *stream) {
+  if (!W1 || !W3 || !(x_q8 || xf) || !y1 || !y3) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (out_dim <= 0 || in_dim <= 0 || in_dim % 32 || out_dim > INT_MAX / 2)
+    return set_err(MIA_ERR_INVALID, "bad sizes (out_dim=%d in_dim=%d)", out_dim, in_dim);
+  if (in_dim % 64)
+    return set_err(MIA_ERR_UNSUPPORTED, "in_dim %d: the kernel needs an even number of blocks per row",
+                   in_dim);
+  if (xf && in_dim > mia::kQ4MaxF32InDim)
+    return set_err(MIA_ERR_UNSUPPORTED, "in_dim %d above %d for fp32 input (quantize first)", in_dim,
+                   mia::kQ4MaxF32InDim);
+  const uintptr_t bits = (uintptr_t)W1 | (uintptr_t)W3 | (uintptr_t)x_q8 | (uintptr_t)y1 |
+                         (uintptr_t)y3;
+  if (bits & 3) return set_err(MIA_ERR_INVALID, "weights, x_q8 and y must be 4-byte aligned");
+  if ((uintptr_t)xf & 15) return set_err(MIA_ERR_INVALID, "x must be 16-byte aligned");
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  mia::Q4MatvecParams p{};
+  p.w0 = reinterpret_cast<const uint8_t *>(W1);
+  p.w1 = reinterpret_cast<const uint8_t *>(W3);
+  p.y0 = y1;
+  p.y1 = y3;
+  p.x = reinterpret_cast<const uint8_t *>(x_q8);
+  p.xf = xf;
+  p.rows0 = out_dim;
+  p.rows01 = 2 * out_dim;
+  p.total_rows = 2 * out_dim;
+  p.bpr = in_dim / 32;
+  hipEvent_t ev0, ev1;
+  if (int rc = prof_pair(c, 2, &ev0, &ev1)) return rc;
+  HIP_TRY(mia::launch_q4_matvec(p, pick_stream(c, stream), ev0, ev1));
+  return MIA_OK;
+}
+
+int mia_q4_0_matvec_pair(const void *W1, const void *W3, const void *x_q8, float *y1, float *y3,
+                         int out_dim, int in_dim, void *stream) {
+  return q4_pair_impl(W1, W3, x_q8, nullptr, y1, y3, out_dim, in_dim, stream);
+}
+
+int mia_q4_0_matvec_pair_f32(const void *W1, const void *W3, const float *x, float *y1,
+                             float *y3, int out_dim, int in_dim, void *stream) {
+  return q4_pair_impl(W1, W3, nullptr, x, y1, y3, out_dim, in_dim, stream);
+}
+
+// ---- the decode layer -------------------------------------------------------
+
+// y [rows] = W . x for the layer's matrices on Q8_0 input blocks, by type as
+// q4_matvec_sdot_parallel dispatches (mistral_model.h:649-670).
+static int layer_matvec_q8(const void *W, int type, const void *xq8, float *y, int rows, int cols,
+                           void *stream) {
+  if (type == MIA_TYPE_Q4_0) return mia_q4_0_matvec(W, xq8, y, rows, cols, stream);
+  return typed_matvec_impl(W, type, xq8, true, y, rows, cols, stream);
+}
+
+int mia_silu_mul_f32(float *gate, const float *up, long n, void *stream) {
+  if (!gate || !up) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (n < 0) return set_err(MIA_ERR_INVALID, "bad size %ld", n);
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  HIP_TRY(mia::launch_silu_mul(gate, up, n, pick_stream(c, stream)));
+  return MIA_OK;
+}
+
+int mia_decode_layer(float *x, const mia_layer_weights_typed *lw, const float *theta_inv,
+                     uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden, int n_heads,
+                     int n_kv_heads, float eps, int max_seq, int pos, void *stream) {
+  if (!x || !lw || !theta_inv || !k_layer || !v_layer)
+    return set_err(MIA_ERR_INVALID, "NULL pointer");
+  if (!lw->wq || !lw->wk || !lw->wv || !lw->wo || !lw->w1 || !lw->w2 || !lw->w3 || !lw->rms_att ||
+      !lw->rms_ffn)
+    return set_err(MIA_ERR_INVALID, "NULL weight pointer");
+  if (n_heads <= 0 || dim != n_heads * kHD)
+    return set_err(MIA_ERR_UNSUPPORTED, "dim %d must be n_heads x 128", dim);
+  if (int rc = check_shape(n_heads, n_kv_heads, kHD, max_seq)) return rc;
+  if (int rc = check_pos(pos, 1)) return rc;
+  if (hidden <= 0) return set_err(MIA_ERR_INVALID, "bad hidden %d", hidden);
+  const int kv_dim = n_kv_heads * kHD;
+  const void *const ws[7] = {lw->wq, lw->wk, lw->wv, lw->wo, lw->w1, lw->w2, lw->w3};
+  const int types[7] = {lw->wq_type, lw->wk_type, lw->wv_type, lw->wo_type,
+                        lw->w1_type, lw->w2_type, lw->w3_type};
+  const int in_dims[7] = {dim, dim, dim, dim, dim, hidden, dim};
+  for (int i = 0; i < 7; ++i) {
+    if (int rc = check_typed(types[i], in_dims[i], ws[i])) return rc;
+    if (types[i] == MIA_TYPE_Q4_0) {  // the W4A8 kernel: whole block pairs, 4-byte aligned
+      if (in_dims[i] % 64)
+        return set_err(MIA_ERR_UNSUPPORTED, "Q4_0 matvec needs in_dim %% 64 == 0");
+      if ((uintptr_t)ws[i] & 3)
+        return set_err(MIA_ERR_INVALID, "Q4_0 weights must be 4-byte aligned");
+    }
+  }
+  if (int rc = check_align16(x, lw->rms_att, lw->rms_ffn, nullptr)) return rc;
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  hipStream_t s = pick_stream(c, stream);
+  // xb, xb2, q [dim] | k, v [kv_dim] | hb, hb2 [hidden] | Q8_0 blocks of the
+  // longest input
+  const size_t bd = al256((size_t)dim * 4), bk = al256((size_t)kv_dim * 4),
+               bh = al256((size_t)hidden * 4),
+               bq = al256((size_t)(dim > hidden ? dim : hidden) / 32 * 36);
+  if (int rc = ensure_dl_work(c, 3 * bd + 2 * bk + 2 * bh + bq)) return rc;
+  char *w = reinterpret_cast<char *>(c->dl_work);
+  float *xb = reinterpret_cast<float *>(w);
+  float *xb2 = reinterpret_cast<float *>(w + bd);
+  float *q = reinterpret_cast<float *>(w + 2 * bd);
+  float *k = reinterpret_cast<float *>(w + 3 * bd);
+  float *v = reinterpret_cast<float *>(w + 3 * bd + bk);
+  float *hb = reinterpret_cast<float *>(w + 3 * bd + 2 * bk);
+  float *hb2 = reinterpret_cast<float *>(w + 3 * bd + 2 * bk + bh);
+  void *q8 = w + 3 * bd + 2 * bk + 2 * bh;
+  const bool fused_in = dim <= mia::kQ4MaxF32InDim;  // x quantised inside the Q4_0 launch
+  // mistral_model.h:830-899
+  HIP_TRY(mia::launch_rmsnorm(xb, x, lw->rms_att, dim, 1, eps, s));
+  if (types[0] == MIA_TYPE_Q4_0 && types[1] == MIA_TYPE_Q4_0 && types[2] == MIA_TYPE_Q4_0 &&
+      fused_in) {
+    if (int rc = mia_q4_0_matvec_qkv_f32(lw->wq, lw->wk, lw->wv, xb, q, k, v, dim, kv_dim, dim, s))
+      return rc;
+  } else {
+    HIP_TRY(mia::launch_quantize_q8_0(xb, reinterpret_cast<uint8_t *>(q8), dim / 32, s));
+    if (int rc = layer_matvec_q8(lw->wq, types[0], q8, q, dim, dim, s)) return rc;
+    if (int rc = layer_matvec_q8(lw->wk, types[1], q8, k, kv_dim, dim, s)) return rc;
+    if (int rc = layer_matvec_q8(lw->wv, types[2], q8, v, kv_dim, dim, s)) return rc;
+  }
+  // RoPE, fp16 ring write at pos % max_seq, attention: one fused launch + merge
+  if (int rc = decode_impl(q, k, v, theta_inv, k_layer, v_layer, xb2, n_heads, n_kv_heads, max_seq,
+                           pos, true, s))
+    return rc;
+  if (types[3] == MIA_TYPE_Q4_0 && fused_in) {
+    if (int rc = mia_q4_0_matvec_f32(lw->wo, xb2, xb, dim, dim, s)) return rc;
+  } else {
+    HIP_TRY(mia::launch_quantize_q8_0(xb2, reinterpret_cast<uint8_t *>(q8), dim / 32, s));
+    if (int rc = layer_matvec_q8(lw->wo, types[3], q8, xb, dim, dim, s)) return rc;
+  }
+  HIP_TRY(mia::launch_residual_rmsnorm(x, xb, lw->rms_ffn, xb, dim, eps, s));
+  if (types[4] == MIA_TYPE_Q4_0 && types[6] == MIA_TYPE_Q4_0 && fused_in) {
+    if (int rc = mia_q4_0_matvec_pair_f32(lw->w1, lw->w3, xb, hb, hb2, hidden, dim, s)) return rc;
+  } else {
+    HIP_TRY(mia::launch_quantize_q8_0(xb, reinterpret_cast<uint8_t *>(q8), dim / 32, s));
+    if (int rc = layer_matvec_q8(lw->w1, types[4], q8, hb, hidden, dim, s)) return rc;
+    if (int rc = layer_matvec_q8(lw->w3, types[6], q8, hb2, hidden, dim, s)) return rc;
+  }
+  HIP_TRY(mia::launch_silu_mul(hb, hb2, hidden, s));
+  HIP_TRY(mia::launch_quantize_q8_0(hb, reinterpret_cast<uint8_t *>(q8), hidden / 32, s));
+  if (int rc = layer_matvec_q8(lw->w2, types[5], q8, xb, dim, hidden, s)) return rc;
+  HIP_TRY(mia::launch_add(x, xb, dim, s));
+  return MIA_OK;
 }
 
 }  // extern "C"

@@ -385,6 +385,28 @@ void mia_dropin_q4_matvec_sdot_parallel_fused_qkv(const void *Wq, const void *Wk
     }
 }
 
+void mia_dropin_q4_matvec_sdot_parallel_fused_pair(const void *W1, const void *W3,
+                                                   const mia_block_q8_0 *x_q8, float *y1,
+                                                   float *y3, int out_dim, int in_dim) {
+    const char *what = "q4_matvec_sdot_parallel_fused_pair";
+    g_status = 0;
+    if (out_dim <= 0 || in_dim <= 0 || in_dim % 32) {
+        fail(MIA_ERR_INVALID, "q4_matvec (bad sizes)");
+        return;
+    }
+    size_t xb = (size_t)(in_dim / 32) * sizeof(mia_block_q8_0);
+    size_t yb = (size_t)out_dim * sizeof(float);
+    TRY(what, dbuf(align256(xb) + 2 * align256(yb)));
+    void *dx = g_dbuf;
+    float *dy1 = (float *)(g_dbuf + align256(xb));
+    float *dy3 = (float *)(g_dbuf + align256(xb) + align256(yb));
+    TRY(what, mia_memcpy_h2d(dx, x_q8, xb));
+    TRY(what, mia_q4_0_matvec_pair(W1, W3, dx, dy1, dy3, out_dim, in_dim, NULL));
+    TRY(what, mia_stream_sync(NULL));
+    TRY(what, mia_memcpy_d2h(y1, dy1, yb));
+    TRY(what, mia_memcpy_d2h(y3, dy3, yb));
+}
+
 void mia_dropin_q4_matvec_sdot_parallel(const void *W, uint32_t type, const mia_block_q8_0 *x_q8,
                                         float *y, int out_dim, int in_dim) {
     const char *what = "q4_matvec_sdot_parallel";

@@ -205,6 +205,11 @@ hipError_t launch_typed_split(const void *W, int type, _Float16 *hi, _Float16 *l
 // rscale null: Y (+)= C1[s][n] + C1[S + s][n].
 hipError_t launch_hilo_combine(const float *C1, const float *C2, const float *rscale, float *Y,
                                int S, int N, bool add, hipStream_t s);
+// The decode layer's residual steps (mia_layer.hip): x += y, then out =
+// rmsnorm(x) (dim a multiple of 4, pointers 16-byte aligned); x += y.
+hipError_t launch_residual_rmsnorm(float *x, const float *y, const float *w, float *out, int dim,
+                                   float eps, hipStream_t s);
+hipError_t launch_add(float *x, const float *y, int n, hipStream_t s);
 // gate [n] = gate * sigmoid(gate) * up (the SwiGLU product).
 hipError_t launch_silu_mul(float *gate, const float *up, long n, hipStream_t s);
 

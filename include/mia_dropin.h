@@ -148,6 +148,10 @@ void mia_dropin_quantize_q8_0(const float *x, mia_block_q8_0 *out, int n);
  * MIA_ERR_UNSUPPORTED) */
 void mia_dropin_q4_matvec_sdot_parallel(const void *W, uint32_t type, const mia_block_q8_0 *x_q8,
                                         float *y, int out_dim, int in_dim);
+/* mistral/mistral_model.h:750-811 */
+void mia_dropin_q4_matvec_sdot_parallel_fused_pair(const void *W1, const void *W3,
+                                                   const mia_block_q8_0 *x_q8, float *y1,
+                                                   float *y3, int out_dim, int in_dim);
 /* mistral/mistral_model.h:676-745 */
 void mia_dropin_q4_matvec_sdot_parallel_fused_qkv(const void *Wq, const void *Wk, const void *Wv,
                                                   const mia_block_q8_0 *x_q8, float *yq,
@@ -228,6 +232,11 @@ static inline void quantize_f32_to_q8_0(const float *x, block_q8_0 *out, int n) 
 static inline void q4_matvec_sdot_parallel(const void *W, uint32_t type, const block_q8_0 *x_q8,
                                            float *y, int out_dim, int in_dim) {
     mia_dropin_q4_matvec_sdot_parallel(W, type, x_q8, y, out_dim, in_dim);
+}
+static inline void q4_matvec_sdot_parallel_fused_pair(const void *W1, const void *W3,
+                                                      const block_q8_0 *x_q8, float *y1,
+                                                      float *y3, int out_dim, int in_dim) {
+    mia_dropin_q4_matvec_sdot_parallel_fused_pair(W1, W3, x_q8, y1, y3, out_dim, in_dim);
 }
 static inline void q4_matvec_sdot_parallel_fused_qkv(const void *Wq, const void *Wk,
                                                      const void *Wv, const block_q8_0 *x_q8,

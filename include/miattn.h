@@ -237,6 +237,17 @@ int mia_q4_0_matvec_qkv_f32(const void *Wq, const void *Wk, const void *Wv, cons
                             float *yq, float *yk, float *yv, int dim, int kv_dim, int in_dim,
                             void *stream);
 
+/* The FFN's gate and up projections against one quantised input in one
+ * launch.  Replaces q4_matvec_sdot_parallel_fused_pair (mistral/
+ * mistral_model.h:750-811, called at :880-885): y1 [out_dim] = W1 . x,
+ * y3 [out_dim] = W3 . x, each row as in mia_q4_0_matvec; the _f32 form
+ * quantises x inside the launch as mia_q4_0_matvec_f32 does (in_dim <= 8192,
+ * bit-identical to mia_quantize_q8_0 + mia_q4_0_matvec_pair). */
+int mia_q4_0_matvec_pair(const void *W1, const void *W3, const void *x_q8, float *y1, float *y3,
+                         int out_dim, int in_dim, void *stream);
+int mia_q4_0_matvec_pair_f32(const void *W1, const void *W3, const float *x, float *y1,
+                             float *y3, int out_dim, int in_dim, void *stream);
+
 /* ---- the rest of the prefill layer ---------------------------------------- */
 
 /* rmsnorm_batch (mistral/mistral_ane_prefill.h:163-175): out[t] = in[t] *
@@ -406,6 +417,29 @@ int mia_prefill_layer_typed_packed(float *X, const mia_layer_weights_typed *lw,
                                    const float *theta_inv, uint16_t *k_layer, uint16_t *v_layer,
                                    int dim, int hidden, int n_heads, int n_kv_heads, float eps,
                                    int max_seq, int start_pos, int S, void *stream);
+
+/* ---- the decode layer ------------------------------------------------------ */
+/* silu_mul_neon (mistral/mistral_model.h:174-199): gate[i] = gate[i] *
+ * (1 / (1 + exp(-gate[i]))) * up[i] for n fp32 (dev) values, the SwiGLU
+ * product of both layers' FFN; exp is the GPU's (within ulps of libm's). */
+int mia_silu_mul_f32(float *gate, const float *up, long n, void *stream);
+
+/* mistral_layer_decode_parallel (mistral/mistral_model.h:818-899) on the GPU
+ * for the token at pos: x [dim] fp32 dev (16-byte aligned) is updated in
+ * place, the layer's ring gets the token's rotated fp16 K / V at slot
+ * pos % max_seq (the caller keeps kv->len, as the reference's caller does).
+ * Steps and their arithmetic as the reference's: RMSNorm; x quantised to
+ * Q8_0 once for Q, K and V (one fused launch when all three are Q4_0,
+ * mia_q4_0_matvec_qkv_f32; otherwise each by type as mia_matvec_q8);
+ * mia_decode_step; the attention output quantised for Wo; x += Wo . a; RMSNorm
+ * (one launch with the residual add); gate and up (mia_q4_0_matvec_pair_f32
+ * when both are Q4_0); gate * sigmoid(gate) * up; its Q8_0 blocks for W2;
+ * x += W2 . h.  Weights in the GGUF layout with their types
+ * (mia_layer_weights_typed); dim = n_heads * 128.  The vectors live in a
+ * per-device work area (~190 KB at Mistral-7B's sizes). */
+int mia_decode_layer(float *x, const mia_layer_weights_typed *lw, const float *theta_inv,
+                     uint16_t *k_layer, uint16_t *v_layer, int dim, int hidden, int n_heads,
+                     int n_kv_heads, float eps, int max_seq, int pos, void *stream);
 
 /* ---- KV-ring snapshots (no counterpart in the reference) ------------------ */
 /* The rings of all layers (k_cache / v_cache: device memory holding

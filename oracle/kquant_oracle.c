@@ -273,3 +273,52 @@ int ora_prefill_layer_typed(const OraLayerWeightsTyped *lw, OraKV *kv, float *X,
     free(Xn); free(Q); free(K); free(V); free(A); free(G); free(U); free(att);
     return bad ? -1 : 0;
 }
+
+/* y = W . x_q8 by type, as q4_matvec_sdot_parallel dispatches
+ * (mistral_model.h:649-670) */
+static int layer_matvec(const void *W, int type, const OraQ8Block *xq, float *y, int rows,
+                        int cols) {
+    if (type == ORA_TYPE_Q4_0) {
+        ora_q4_0_q8_0_matvec(W, xq, y, rows, cols);
+        return 0;
+    }
+    return ora_typed_matvec_q8(W, type, xq, y, rows, cols);
+}
+
+int ora_decode_layer_typed(const OraLayerWeightsTyped *lw, OraKV *kv, float *x, int layer,
+                           int pos, int dim, int hidden, int n_heads, int n_kv_heads, float eps,
+                           const float *theta_inv) {
+    const int kv_dim = n_kv_heads * (dim / n_heads);
+    float *xb = (float *)malloc((size_t)dim * sizeof(float));
+    float *xb2 = (float *)malloc((size_t)dim * sizeof(float));
+    float *q = (float *)malloc((size_t)dim * sizeof(float));
+    float *k = (float *)malloc((size_t)kv_dim * sizeof(float));
+    float *v = (float *)malloc((size_t)kv_dim * sizeof(float));
+    float *hb = (float *)malloc((size_t)hidden * sizeof(float));
+    float *hb2 = (float *)malloc((size_t)hidden * sizeof(float));
+    float *att = (float *)malloc((size_t)n_heads * kv->max_seq * sizeof(float));
+    OraQ8Block *xq = (OraQ8Block *)malloc((size_t)(dim > hidden ? dim : hidden) / ORA_QK *
+                                          sizeof(OraQ8Block));
+    if (!xb || !xb2 || !q || !k || !v || !hb || !hb2 || !att || !xq) abort();
+    int bad = 0;
+    /* mistral_model.h:830-899 */
+    ora_rmsnorm_batch(xb, x, lw->rms_att, dim, 1, eps);
+    ora_quantize_q8_0(xb, xq, dim);
+    bad |= layer_matvec(lw->wq, lw->wq_type, xq, q, dim, dim);
+    bad |= layer_matvec(lw->wk, lw->wk_type, xq, k, kv_dim, dim);
+    bad |= layer_matvec(lw->wv, lw->wv_type, xq, v, kv_dim, dim);
+    ora_decode_step(kv, layer, q, k, v, pos, theta_inv, n_heads, n_kv_heads, att, xb2);
+    ora_quantize_q8_0(xb2, xq, dim);
+    bad |= layer_matvec(lw->wo, lw->wo_type, xq, xb, dim, dim);
+    for (int i = 0; i < dim; i++) x[i] = x[i] + xb[i];
+    ora_rmsnorm_batch(xb, x, lw->rms_ffn, dim, 1, eps);
+    ora_quantize_q8_0(xb, xq, dim);
+    bad |= layer_matvec(lw->w1, lw->w1_type, xq, hb, hidden, dim);
+    bad |= layer_matvec(lw->w3, lw->w3_type, xq, hb2, hidden, dim);
+    ora_silu_mul(hb, hb2, hidden);
+    ora_quantize_q8_0(hb, xq, hidden);
+    bad |= layer_matvec(lw->w2, lw->w2_type, xq, xb, dim, hidden);
+    for (int i = 0; i < dim; i++) x[i] = x[i] + xb[i];
+    free(xb); free(xb2); free(q); free(k); free(v); free(hb); free(hb2); free(att); free(xq);
+    return bad ? -1 : 0;
+}

@@ -31,6 +31,8 @@
  *   ora_prefill_layer_typed all-Q4_0 weights reproduce ora_prefill_layer
  *                           bit for bit; its other steps are that
  *                           function's (prefill_oracle.h)            pinned
+ *   ora_decode_layer_typed  against a float64 numpy layer on the oracle's
+ *                           own Q8_0 activations                     pinned
  */
 #ifndef KQUANT_ORACLE_H
 #define KQUANT_ORACLE_H
@@ -90,6 +92,17 @@ typedef struct {
 int ora_prefill_layer_typed(const OraLayerWeightsTyped *lw, OraKV *kv, float *X, int layer,
                             int start_pos, int S, int dim, int hidden, int n_heads,
                             int n_kv_heads, float eps, const float *theta_inv, int threads);
+
+/* mistral_layer_decode_parallel (mistral/mistral_model.h:818-899) for one
+ * token: x [dim] updated in place, the layer's ring written at pos % max_seq.
+ * Composed of the pinned pieces: ora_rmsnorm_batch (S = 1, the same formula
+ * as rmsnorm_vec, :202-208), ora_quantize_q8_0, the W4A8 matvec for Q4_0
+ * (ora_q4_0_q8_0_matvec; the fused QKV and gate/up dispatches compute the
+ * same rows) or ora_typed_matvec_q8 for the other types, ora_decode_step,
+ * ora_silu_mul.  0 on success, -1 for a type it does not know. */
+int ora_decode_layer_typed(const OraLayerWeightsTyped *lw, OraKV *kv, float *x, int layer,
+                           int pos, int dim, int hidden, int n_heads, int n_kv_heads, float eps,
+                           const float *theta_inv);
 
 #ifdef __cplusplus
 }

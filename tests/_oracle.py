@@ -87,6 +87,10 @@ _SIGS = {
     "ora_typed_matvec": (c_int, [_P, c_int, _P, _P, c_int, c_int]),
     "ora_typed_matvec_q8": (c_int, [_P, c_int, _P, _P, c_int, c_int]),
     "ora_typed_gemm": (c_int, [_P, c_int, c_int, c_int, _P, c_int, _P, c_int]),
+    "ora_decode_layer_typed": (
+        c_int,
+        [_P, POINTER(OraKV), _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P],
+    ),
     "ora_prefill_layer_typed": (
         c_int,
         [_P, POINTER(OraKV), _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P,
@@ -485,3 +489,17 @@ def prefill_layer_typed(W, types, X, kc, vc, start_pos, S, dim, hidden, n_heads,
                                           start_pos, S, dim, hidden, n_heads, n_kv, eps,
                                           _p(np.ascontiguousarray(th, np.float32)), threads) == 0
     return Xo
+
+
+def decode_layer_typed(W, types, x, kc, vc, pos, dim, hidden, n_heads, n_kv, th, eps=1e-5):
+    """ora_decode_layer_typed on copies: returns x'; kc/vc (one layer) updated."""
+    hd = dim // n_heads
+    kv = make_kv(kc, vc, n_kv, hd, kc.shape[0])
+    arrs = {k: np.ascontiguousarray(v) for k, v in W.items()}
+    lw = OraLayerWeightsTyped(*[_p(arrs[n]) for n in MATS], *[types[n] for n in MATS],
+                              _p(arrs["rms_att"]), _p(arrs["rms_ffn"]))
+    xo = np.array(x, np.float32, copy=True)
+    assert load().ora_decode_layer_typed(ctypes.byref(lw), ctypes.byref(kv), _p(xo), 0, pos, dim,
+                                         hidden, n_heads, n_kv, eps,
+                                         _p(np.ascontiguousarray(th, np.float32))) == 0
+    return xo

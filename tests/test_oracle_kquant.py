@@ -221,11 +221,11 @@ Q4_K_M = {"wq": O.TYPE_Q4_K, "wk": O.TYPE_Q4_K, "wv": O.TYPE_Q6_K, "wo": O.TYPE_
           "w1": O.TYPE_Q4_K, "w3": O.TYPE_Q4_K, "w2": O.TYPE_Q6_K}
 
 
-def make_layer_typed(g, types, dim, hidden, nh, nkv):
+def make_layer_typed(g, types, dim, hidden, nh, nkv, d_scale=1.0):
     kvd = dim // nh * nkv
     shapes = {"wq": (dim, dim), "wk": (kvd, dim), "wv": (kvd, dim), "wo": (dim, dim),
               "w1": (hidden, dim), "w3": (hidden, dim), "w2": (dim, hidden)}
-    W = {k: O.make_typed(g, types[k], *shapes[k]) for k in O.MATS}
+    W = {k: O.make_typed(g, types[k], *shapes[k], d_scale=d_scale) for k in O.MATS}
     W["rms_att"] = (1.0 + 0.1 * g.standard_normal(dim)).astype(np.float32)
     W["rms_ffn"] = (1.0 + 0.1 * g.standard_normal(dim)).astype(np.float32)
     return W
@@ -272,3 +272,75 @@ def test_prefill_layer_typed_matches_float64(mix):
     slots = np.arange(start, start + S) % M
     assert np.abs(D.f16_bits_to_f32(ko[slots]) - kring[slots]).max() <= 2e-3 * max(
         1.0, np.abs(kring[slots]).max())
+
+
+def _q8_64(x):
+    """Q8_0 quantisation in float64 (d = amax / 127, q = round-half-even(x / d)
+    saturated; dequant.h:545-612): the values d * q."""
+    b = x.reshape(-1, 32)
+    amax = np.abs(b).max(axis=1, keepdims=True)
+    d = amax / 127.0
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = np.where(d > 0, np.clip(np.rint(b / d), -128, 127), 0.0)
+    return (q * d).reshape(-1)
+
+
+def _decode_layer64(W, types, x, kc, vc, pos, dim, hidden, nh, nkv, th, eps):
+    """mistral_layer_decode_parallel (mistral_model.h:818-899) in float64 with
+    the Q8_0 rounding of the activations (fp16 ring entries as the ring holds
+    them)."""
+    hd, M = dim // nh, kc.shape[0]
+    kvd = nkv * hd
+    shapes = {"wq": (dim, dim), "wk": (kvd, dim), "wv": (kvd, dim), "wo": (dim, dim),
+              "w1": (hidden, dim), "w3": (hidden, dim), "w2": (dim, hidden)}
+    dq = {k: O.dequant_typed(W[k], types[k], *shapes[k]).astype(np.float64) for k in O.MATS}
+
+    def rms(v, w):
+        return v / np.sqrt((v * v).mean() + eps) * w.astype(np.float64)
+
+    x = x.astype(np.float64)
+    xq = _q8_64(rms(x, W["rms_att"]))
+    q, k, v = dq["wq"] @ xq, dq["wk"] @ xq, dq["wv"] @ xq
+    kring = D.f16_bits_to_f32(kc).astype(np.float64)
+    vring = D.f16_bits_to_f32(vc).astype(np.float64)
+    slot = pos % M
+    kring[slot] = P._rope64(k, pos, th, nkv, hd).astype(np.float16)
+    vring[slot] = v.astype(np.float16)
+    qr = P._rope64(q, pos, th, nh, hd).reshape(nh, hd)
+    L = min(pos + 1, M)
+    slots = [(pos + 1 - L + t) % M for t in range(L)]
+    a = np.zeros(dim)
+    for h in range(nh):
+        kvh = h // (nh // nkv)
+        sc = kring[slots][:, kvh * hd:(kvh + 1) * hd] @ qr[h] / np.sqrt(hd)
+        pr = np.exp(sc - sc.max())
+        a[h * hd:(h + 1) * hd] = (pr / pr.sum()) @ vring[slots][:, kvh * hd:(kvh + 1) * hd]
+    x = x + dq["wo"] @ _q8_64(a)
+    xq = _q8_64(rms(x, W["rms_ffn"]))
+    g, u = dq["w1"] @ xq, dq["w3"] @ xq
+    h = g / (1.0 + np.exp(-g)) * u
+    return x + dq["w2"] @ _q8_64(h), kring[slot]
+
+
+@pytest.mark.parametrize("mix,pos", [("q4_0", 5), ("q4_k_m", 40), ("q4_k_m", 100)])
+def test_decode_layer_typed_matches_float64(mix, pos):
+    # the Q8_0 rounding is reproduced in float64, so the oracle's fp32
+    # arithmetic differs from this only by fp32 rounding and the occasional
+    # activation whose Q8_0 step differs when its value sits at a rounding
+    # boundary: a normwise 2e-3 of the output's scale (a dropped residual, a
+    # swapped gate / up or a missing requantisation errs by tens of percent)
+    g = np.random.default_rng(60 + pos)
+    types = {k: O.TYPE_Q4_0 for k in O.MATS} if mix == "q4_0" else Q4_K_M
+    dim, hidden, nh, nkv, M = 512, 768, 4, 1, 64
+    W = make_layer_typed(g, types, dim, hidden, nh, nkv, 0.07) if mix != "q4_0" else \
+        P.make_layer(g, dim, hidden, nh, nkv)
+    kc, vc = _ring(g, M, dim // nh * nkv, min(pos, M))
+    x = g.standard_normal(dim).astype(np.float32)
+    th = O.theta_inv(1e6, dim // nh)
+    ref, krow = _decode_layer64(W, types, x, kc, vc, pos, dim, hidden, nh, nkv, th, 1e-5)
+    ko, vo = kc.copy(), vc.copy()
+    out = O.decode_layer_typed(W, types, x, ko, vo, pos, dim, hidden, nh, nkv, th)
+    assert np.abs(out - ref).max() <= 2e-3 * np.abs(ref).max()
+    assert np.abs(D.f16_bits_to_f32(ko[pos % M]) - krow).max() <= 2e-3 * np.abs(krow).max()
+    others = np.setdiff1d(np.arange(M), [pos % M])
+    assert np.array_equal(ko[others], kc[others]) and np.array_equal(vo[others], vc[others])
