@@ -660,6 +660,126 @@ def km_bytes(rows: int, cols: int, t: int) -> int:
     return rows * (cols // 256) * (144 if t == TYPE_Q4_K else 210)
 
 
+def km_weights(lib, seed: int):
+    """32 layers of Q4_K_M matrices in one device buffer: (buffer, offsets of
+    the seven matrices in a layer, bytes per layer).  A seeded fp16 N(0,1)
+    stream read as the blocks, with the block scales scaled down so that the
+    activations stay O(1)."""
+    offs, off = {}, 0
+    for name, r, c, t in KM_SIZES:
+        offs[name] = off
+        off += (km_bytes(r, c, t) + 255) // 256 * 256
+    w = DeviceBuffer(N_LAYERS * off)
+    check(lib.mia_fill_normal_f16(w.ptr, N_LAYERS * off // 2, seed, None))
+    for l in range(N_LAYERS):
+        for name, r, c, t in KM_SIZES:
+            base = w.ptr + l * off + offs[name]
+            n16 = km_bytes(r, c, t) // 2
+            if t == TYPE_Q4_K:   # d and dmin: the first 2 of each block's 72 fp16
+                check(lib.mia_scale_rows_f16(base, n16 // 2, 2, 36, 0, 1.0 / 16384, None))
+            else:                # d: fp16 104 of each block's 105
+                check(lib.mia_scale_rows_f16(base, n16, 1, 105, 104, 1.0 / 65536, None))
+    return w, offs, off
+
+
+class DecodeLayers:
+    """The whole decode layer on the GPU (mia_decode_layer), 32 layers, for the
+    token at position 32768 over the headline's full 32768-slot rings: Q4_0
+    weights (3.9 GB, the reference's fused QKV and gate / up dispatches) or
+    Q4_K_M weights (4.45 GB, per-type matvecs); x carried from layer to
+    layer."""
+
+    Q4_SIZES = (("wq", DIM, DIM), ("wk", KV_DIM, DIM), ("wv", KV_DIM, DIM), ("wo", DIM, DIM),
+                ("w1", HIDDEN, DIM), ("w2", DIM, HIDDEN), ("w3", HIDDEN, DIM))
+
+    def __init__(self, lib, dec: "Decode", kind: str, seed: int = 71):
+        self.lib, self.dec, self.kind = lib, dec, kind
+        g = np.random.default_rng(seed)
+        if kind == "q4_0":
+            offs, off = {}, 0
+            for name, r, c in self.Q4_SIZES:
+                offs[name] = off
+                off += (q4_bytes(r, c) + 255) // 256 * 256
+            self.w = DeviceBuffer(N_LAYERS * off)
+            check(lib.mia_fill_normal_f16(self.w.ptr, N_LAYERS * off // 2, seed, None))
+            # x 2^-12 keeps the block scales near 2.4e-4: the residual stream stays O(1)
+            check(lib.mia_scale_rows_f16(self.w.ptr, N_LAYERS * off // 2048, 1024, 1, 0,
+                                         1.0 / 4096, None))
+            types = {n: mia.TYPE_Q4_0 for n, _, _ in self.Q4_SIZES}
+            self.weight_bytes = sum(q4_bytes(r, c) for _, r, c in self.Q4_SIZES)
+        else:
+            self.w, offs, off = km_weights(lib, seed)
+            types = {n: t for n, _, _, t in KM_SIZES}
+            self.weight_bytes = sum(km_bytes(r, c, t) for _, r, c, t in KM_SIZES)
+        self.norms = DeviceBuffer.from_array(
+            (1.0 + 0.1 * g.standard_normal((N_LAYERS, 2, DIM))).astype(np.float32))
+        self.x = DeviceBuffer.from_array(g.standard_normal(DIM).astype(np.float32))
+        names = ("wq", "wk", "wv", "wo", "w1", "w2", "w3")
+        self.lws = []
+        for l in range(N_LAYERS):
+            nb = self.norms.ptr + l * 2 * DIM * 4
+            self.lws.append(mia.LayerWeightsTyped(
+                *(self.w.ptr + l * off + offs[n] for n in names), *(types[n] for n in names),
+                nb, nb + DIM * 4))
+        check(lib.mia_device_sync())
+
+    def step(self) -> None:
+        lay = DECODE_M * KV_DIM * 2
+        for l in range(N_LAYERS):
+            check(self.lib.mia_decode_layer(
+                self.x.ptr, ctypes.byref(self.lws[l]), self.dec.th.ptr,
+                self.dec.kc.ptr + l * lay, self.dec.vc.ptr + l * lay, DIM, HIDDEN, N_HEADS, N_KV,
+                1e-5, DECODE_M, DECODE_POS, None), "decode_layer")
+
+
+def decode_layer_leg(lib, dec: "Decode", steps: int, warmup: int) -> dict:
+    out = {"workload": "mia_decode_layer x 32 (RMSNorm, QKV, fused RoPE + ring write + "
+                       "attention at 32K context, Wo, residual, RMSNorm, gate / up, SwiGLU, W2, "
+                       "residual) for the token at position 32768 over the headline's full "
+                       "32768-slot rings"}
+    for kind in ("q4_0", "q4_k_m"):
+        dl = DecodeLayers(lib, dec, kind)
+        ms = timed(lib, dl.step, steps, warmup)
+        nbytes = N_LAYERS * (dl.weight_bytes + DECODE_BYTES_PER_LAYER)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[kind] = {"ms_per_token": round(ms, 4), "tokens_per_s": round(1e3 / ms, 2),
+                     "value": round(gbs, 2), "unit": "GB/s",
+                     "bytes_per_token": nbytes,
+                     "bytes": "weights of all 32 layers + the K / V window (32768 positions)",
+                     "roofline": {"bound": "hbm", "achieved": round(gbs, 2),
+                                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                                  "note": "the whole layer's bytes over the step's time "
+                                          "(11-16 launches per layer)"}}
+        del dl
+    return out
+
+
+def cpu_baseline_decode_layer() -> dict:
+    """The oracle's decode layer (strict build, one thread) on 1 of the 32
+    layers at the same 32K context, Q4_0 weights."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import _oracle as O
+
+    g = np.random.default_rng(17)
+    types = {n: O.TYPE_Q4_0 for n in O.MATS}
+    W = {n: O.make_q4_0(g, r, c) for n, r, c in DecodeLayers.Q4_SIZES}
+    W["rms_att"] = np.ones(DIM, np.float32)
+    W["rms_ffn"] = np.ones(DIM, np.float32)
+    kc = g.standard_normal((DECODE_M, KV_DIM), np.float32).astype(np.float16).view(np.uint16)
+    vc = g.standard_normal((DECODE_M, KV_DIM), np.float32).astype(np.float16).view(np.uint16)
+    x = g.standard_normal(DIM).astype(np.float32)
+    th = theta_inv()
+    t0 = time.perf_counter()
+    O.decode_layer_typed(W, types, x, kc, vc, DECODE_POS, DIM, HIDDEN, N_HEADS, N_KV, th)
+    dt = time.perf_counter() - t0
+    nbytes = sum(q4_bytes(r, c) for _, r, c in DecodeLayers.Q4_SIZES) + DECODE_BYTES_PER_LAYER
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "tokens_per_s": round(1.0 / (32 * dt), 4),
+            "sample": "1 of 32 layers (Q4_0, token at 32768 over a full 32768-slot ring), "
+                      "oracle strict build, one thread; tokens_per_s scaled by 32 layers"}
+
+
 class TypedLayers:
     """32 layers of Q4_K_M weights (4.45 GB): the decode projections through
     mia_matvec_q8 (the reference's non-Q4_0 branch of q4_matvec_sdot_parallel,
@@ -673,21 +793,7 @@ class TypedLayers:
     def __init__(self, lib, seed: int = 61):
         self.lib = lib
         g = np.random.default_rng(seed)
-        self.offs, off = {}, 0
-        for name, r, c, t in KM_SIZES:
-            self.offs[name] = off
-            off += (km_bytes(r, c, t) + 255) // 256 * 256
-        self.lw_bytes = off
-        self.w = DeviceBuffer(N_LAYERS * self.lw_bytes)
-        check(lib.mia_fill_normal_f16(self.w.ptr, N_LAYERS * self.lw_bytes // 2, seed, None))
-        for l in range(N_LAYERS):
-            for name, r, c, t in KM_SIZES:
-                base = self.w.ptr + l * self.lw_bytes + self.offs[name]
-                n16 = km_bytes(r, c, t) // 2
-                if t == TYPE_Q4_K:   # d and dmin: the first 2 of each block's 72 fp16
-                    check(lib.mia_scale_rows_f16(base, n16 // 2, 2, 36, 0, 1.0 / 16384, None))
-                else:                # d: fp16 104 of each block's 105
-                    check(lib.mia_scale_rows_f16(base, n16, 1, 105, 104, 1.0 / 65536, None))
+        self.w, self.offs, self.lw_bytes = km_weights(lib, seed)
         self.norms = DeviceBuffer.from_array(
             (1.0 + 0.1 * g.standard_normal((N_LAYERS, 2, DIM))).astype(np.float32))
         # decode: Q8_0 inputs (the 4096-wide and 14336-wide vectors of each layer)
@@ -1017,6 +1123,8 @@ def main() -> int:
     ap.add_argument("--skip-configs", action="store_true",
                     help="skip the side configs 1, 2 and 5 (profiling)")
     ap.add_argument("--skip-peaks", action="store_true", help="skip the measured-peaks leg")
+    ap.add_argument("--skip-decode-layer", action="store_true",
+                    help="skip the whole-decode-layer leg")
     ap.add_argument("--skip-typed", action="store_true",
                     help="skip the Q4_K_M weight leg (projections and prefill layer)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -1040,7 +1148,7 @@ def main() -> int:
         check(lib.mia_device_sync())
         del src, dst
     dec_ms = kern_ms = float("nan")
-    dropin = projections = peaks = None
+    dropin = projections = peaks = decode_layer = None
     if not args.skip_decode:
         log("decode: allocating 32 x 32768-slot rings (4 GiB)")
         dec = Decode(lib)
@@ -1092,6 +1200,14 @@ def main() -> int:
                                    "32K context (the headline's rings), mia_q4_0_matvec_f32 (Wo)",
             }
             del pj
+        if not args.skip_decode_layer:
+            log("decode layer: 32 layers x the whole layer at 32K context, Q4_0 and Q4_K_M")
+            decode_layer = decode_layer_leg(lib, dec, args.steps, args.warmup)
+            log(f"decode layer: Q4_0 {decode_layer['q4_0']['ms_per_token']:.3f} ms/token "
+                f"({decode_layer['q4_0']['tokens_per_s']:.1f} tokens/s, "
+                f"{decode_layer['q4_0']['value']:.0f} GB/s); Q4_K_M "
+                f"{decode_layer['q4_k_m']['ms_per_token']:.3f} ms/token "
+                f"({decode_layer['q4_k_m']['tokens_per_s']:.1f} tokens/s)")
         del dec
     achieved = DECODE_BYTES_PER_LAYER / (kern_ms * 1e-3) / 1e9
     value = N_LAYERS * DECODE_BYTES_PER_LAYER / (dec_ms * 1e-3) / 1e9
@@ -1243,6 +1359,9 @@ def main() -> int:
         if projections is not None:
             log("cpu baseline: projections sample")
             projections["cpu_baseline"] = cpu_baseline_projections()
+        if decode_layer is not None:
+            log("cpu baseline: decode layer sample")
+            decode_layer["cpu_baseline"] = cpu_baseline_decode_layer()
         if typed is not None:
             log("cpu baseline: Q4_K_M projections and prefill layer samples")
             for k, v in cpu_baseline_typed().items():
@@ -1291,6 +1410,7 @@ def main() -> int:
         "gguf": gguf,
         "prefill_layer": layer,
         "typed_weights": typed,
+        "decode_layer": decode_layer,
     }
     print(json.dumps(line), flush=True)
     return 0
