@@ -1538,6 +1538,56 @@ int mia_decode_layer(float *x, const mia_layer_weights_typed *lw, const float *t
   float *hb2 = reinterpret_cast<float *>(w + 3 * bd + 2 * bk + bh);
   void *q8 = w + 3 * bd + 2 * bk + 2 * bh;
   const bool fused_in = dim <= mia::kQ4MaxF32InDim;  // x quantised inside the Q4_0 launch
+  bool all_q4_0 = true;
+  for (int t : types) all_q4_0 = all_q4_0 && t == MIA_TYPE_Q4_0;
+  if (all_q4_0 && fused_in && hidden <= mia::kQ4MaxFusedInDim) {
+    // mistral_model.h:830-899 in four matvec launches around the attention:
+    // each RMSNorm and Q8_0 quantisation happens in the prologue of the
+    // matvec that reads it, each residual add and the SwiGLU product in the
+    // epilogue of the matvec that produces them; the arithmetic is that of
+    // the separate steps, bit for bit.
+    auto mv = [&](const void *w0, const void *w1, const void *w2, float *y0, float *y1,
+                  float *y2, int rows0, int rows1, int rows2, const float *xf, int in_dim,
+                  const float *rms_w, const float *up, const float *resid,
+                  bool swiglu = false) -> int {
+      mia::Q4MatvecParams p{};
+      p.w0 = reinterpret_cast<const uint8_t *>(w0);
+      p.w1 = reinterpret_cast<const uint8_t *>(w1);
+      p.w2 = reinterpret_cast<const uint8_t *>(w2);
+      p.y0 = y0;
+      p.y1 = y1;
+      p.y2 = y2;
+      p.xf = xf;
+      p.rows0 = rows0;
+      p.rows01 = rows0 + rows1;
+      p.total_rows = rows0 + rows1 + rows2;
+      p.bpr = in_dim / 32;
+      p.rms_w = rms_w;
+      p.eps = eps;
+      p.up = up;
+      p.resid = resid;
+      p.swiglu = swiglu ? 1 : 0;
+      hipEvent_t ev0, ev1;
+      if (int rc = prof_pair(c, 2, &ev0, &ev1)) return rc;
+      HIP_TRY(mia::launch_q4_matvec(p, s, ev0, ev1));
+      return MIA_OK;
+    };
+    if (int rc = mv(lw->wq, lw->wk, lw->wv, q, k, v, dim, kv_dim, kv_dim, x, dim, lw->rms_att,
+                    nullptr, nullptr))
+      return rc;
+    if (int rc = decode_impl(q, k, v, theta_inv, k_layer, v_layer, xb2, n_heads, n_kv_heads,
+                             max_seq, pos, true, s))
+      return rc;
+    if (int rc = mv(lw->wo, nullptr, nullptr, x, nullptr, nullptr, dim, 0, 0, xb2, dim, nullptr,
+                    nullptr, x))
+      return rc;
+    // gate and up rows interleaved: each wave ends with its row's SwiGLU product
+    if (int rc = mv(lw->w1, lw->w3, nullptr, hb, nullptr, nullptr, hidden, hidden, 0, x, dim,
+                    lw->rms_ffn, nullptr, nullptr, true))
+      return rc;
+    return mv(lw->w2, nullptr, nullptr, x, nullptr, nullptr, dim, 0, 0, hb, hidden, nullptr,
+              nullptr, x);
+  }
   // mistral_model.h:830-899
   HIP_TRY(mia::launch_rmsnorm(xb, x, lw->rms_att, dim, 1, eps, s));
   if (types[0] == MIA_TYPE_Q4_0 && types[1] == MIA_TYPE_Q4_0 && types[2] == MIA_TYPE_Q4_0 &&

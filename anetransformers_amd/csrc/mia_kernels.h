@@ -124,7 +124,8 @@ hipError_t launch_quantize_q8_0(const float *x, uint8_t *out, int nblocks, hipSt
 // y = W . x for up to three Q4_0 matrices stacked as virtual rows (w0's rows,
 // then w1's, then w2's); bpr = blocks per row, even; pointers 4-byte aligned.
 // x is either Q8_0 blocks (x) or fp32 values quantised in-kernel (xf, 16-byte
-// aligned, bpr * 32 <= kQ4MaxF32InDim).
+// aligned, bpr * 32 <= kQ4MaxFusedInDim; the C-ABI's fp32-input matvecs take
+// up to kQ4MaxF32InDim).
 constexpr int kQ4MaxF32InDim = 8192;
 struct Q4MatvecParams {
   const uint8_t *w0, *w1, *w2;
@@ -135,7 +136,22 @@ struct Q4MatvecParams {
   int rows01;        // rows of w0 + w1
   int total_rows;    // rows of w0 + w1 + w2
   int bpr;
+  // The decode layer's steps around a matvec, with xf only (each null when
+  // unused): rms_w: xf is RMS-normalised first, (xf * (1 / sqrtf(mean(xf^2) +
+  // eps))) * rms_w, as launch_rmsnorm does it; up: xf is the FFN gate and
+  // the input is gate * (1 / (1 + expf(-gate))) * up; resid: y = resid[row] +
+  // the row's sum (resid may be y itself).
+  const float *rms_w;
+  float eps;
+  const float *up;
+  const float *resid;
+  // swiglu: w0 (gate) and w1 (up) of rows0 rows each, their rows interleaved
+  // (virtual row 2j is w0's row j, 2j + 1 is w1's) so that one wave holds
+  // both sums of row j and writes y0[j] = gate * (1 / (1 + expf(-gate))) * up
+  // (total_rows = 2 * rows0; rows01, y1, y2 unused).
+  int swiglu;
 };
+constexpr int kQ4MaxFusedInDim = 16384;
 hipError_t launch_q4_matvec(const Q4MatvecParams &p, hipStream_t s, hipEvent_t ev0,
                             hipEvent_t ev1);
 hipError_t launch_scale_rows(_Float16 *base, long n_rows, int row_elems, int every, int offset,

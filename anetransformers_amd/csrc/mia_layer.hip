@@ -13,15 +13,16 @@ namespace mia {
 
 namespace {
 
-// One workgroup; dim a multiple of 4, x / y / w / out 16-byte aligned.
-__global__ __launch_bounds__(256) void residual_rmsnorm_kernel(float *x, const float *y,
+// One workgroup of 512 threads, the sum order of rmsnorm_kernel; dim a
+// multiple of 4, x / y / w / out 16-byte aligned.
+__global__ __launch_bounds__(512) void residual_rmsnorm_kernel(float *x, const float *y,
                                                                const float *w, float *out,
                                                                int dim, float eps) {
 #pragma clang fp contract(off)
-  __shared__ float red[4];
+  __shared__ float red[8];
   const int tid = threadIdx.x;
   float ss = 0.0f;
-  for (int i = 4 * tid; i < dim; i += 4 * 256) {
+  for (int i = 4 * tid; i < dim; i += 4 * 512) {
     const f4 a = *reinterpret_cast<const f4 *>(x + i);
     const f4 b = *reinterpret_cast<const f4 *>(y + i);
     f4 v;
@@ -33,9 +34,9 @@ __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(float *x, const f
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
-  ss = (red[0] + red[1]) + (red[2] + red[3]);
+  ss = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
   const float scale = 1.0f / sqrtf(ss / (float)dim + eps);
-  for (int i = 4 * tid; i < dim; i += 4 * 256) {  // the thread's own x values
+  for (int i = 4 * tid; i < dim; i += 4 * 512) {  // the thread's own x values
     const f4 v = *reinterpret_cast<const f4 *>(x + i);
     const f4 wv = *reinterpret_cast<const f4 *>(w + i);
     f4 r;
@@ -54,7 +55,7 @@ __global__ __launch_bounds__(256) void add_kernel(float *x, const float *y, int 
 
 hipError_t launch_residual_rmsnorm(float *x, const float *y, const float *w, float *out, int dim,
                                    float eps, hipStream_t s) {
-  hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(1), dim3(256), 0, s, x, y, w, out, dim, eps);
+  hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(1), dim3(512), 0, s, x, y, w, out, dim, eps);
   return hipGetLastError();
 }
 

@@ -488,25 +488,28 @@ __global__ __launch_bounds__(256) void split_hilo_kernel(const float *__restrict
 
 // With hi set, the normalised rows go out as the Q4_0 GEMM's fp16 hi + lo
 // planes (split exactly as split_hilo_kernel does) instead of fp32 to out.
-__global__ __launch_bounds__(256) void rmsnorm_kernel(float *out, const float *in, const float *w,
+// 512 threads; thread t sums the 4-value groups at 4t + 2048k in k order, then
+// the wave sums and their fixed combination: the order the Q4_0 matvec's
+// RMSNorm prologue reproduces.
+__global__ __launch_bounds__(512) void rmsnorm_kernel(float *out, const float *in, const float *w,
                                                       int dim, float eps, _Float16 *hi,
                                                       _Float16 *lo) {
 #pragma clang fp contract(off)
-  __shared__ float red[4];
+  __shared__ float red[8];
   const int t = blockIdx.x, tid = threadIdx.x;
   const float *x = in + (size_t)t * dim;
   float ss = 0.0f;
-  for (int i = 4 * tid; i < dim; i += 4 * 256) {
+  for (int i = 4 * tid; i < dim; i += 4 * 512) {
     const f4 v = *reinterpret_cast<const f4 *>(x + i);
     ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
   }
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
-  ss = (red[0] + red[1]) + (red[2] + red[3]);
+  ss = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
   const float scale = 1.0f / sqrtf(ss / (float)dim + eps);
   const size_t row = (size_t)t * dim;
-  for (int i = 4 * tid; i < dim; i += 4 * 256) {
+  for (int i = 4 * tid; i < dim; i += 4 * 512) {
     const f4 v = *reinterpret_cast<const f4 *>(x + i);
     const f4 wv = *reinterpret_cast<const f4 *>(w + i);
     f4 r;
@@ -607,14 +610,14 @@ hipError_t launch_split_hilo(const float *x, long n, _Float16 *hi, _Float16 *lo,
 
 hipError_t launch_rmsnorm(float *out, const float *in, const float *w, int dim, int S, float eps,
                           hipStream_t s) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(S), dim3(256), 0, s, out, in, w, dim, eps,
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(S), dim3(512), 0, s, out, in, w, dim, eps,
                      (_Float16 *)nullptr, (_Float16 *)nullptr);
   return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm_split(_Float16 *hi, _Float16 *lo, const float *in, const float *w,
                                 int dim, int S, float eps, hipStream_t s) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(S), dim3(256), 0, s, (float *)nullptr, in, w, dim, eps,
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(S), dim3(512), 0, s, (float *)nullptr, in, w, dim, eps,
                      hi, lo);
   return hipGetLastError();
 }

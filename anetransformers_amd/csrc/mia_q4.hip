@@ -25,6 +25,7 @@ namespace {
 
 constexpr int kQ4Threads = 512;
 constexpr int kQ4Waves = kQ4Threads / 64;
+static_assert(kQ4Waves == 8, "the RMSNorm prologue combines eight wave sums");
 constexpr unsigned kNib = 0x0F0F0F0Fu;
 
 __device__ __forceinline__ unsigned ld32(const uint8_t *p) {
@@ -79,11 +80,17 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
 // arithmetic as quantize_q8_0_kernel, so the blocks are bit-identical) while
 // its weight rows are in flight; each thread loads XP groups of 4 values, so
 // XP * kQ4Threads / 8 >= bpr.  XP = 0: x is Q8_0 blocks in global memory.
-template <int R, int XP>
+// PRO (XP > 0 only): 1 RMS-normalises x before quantising it, 2 forms the
+// SwiGLU product gate * sigmoid(gate) * up from x = gate (Q4MatvecParams).
+// Thread t holds x's 4-value groups at 4t + 2048k, so its sum of squares, the
+// wave sums and their fixed combination are rmsnorm_kernel's own, and the
+// normalised values equal launch_rmsnorm's bit for bit.
+template <int R, int XP, int PRO>
 __global__ __launch_bounds__(kQ4Threads) void q4_matvec_kernel(Q4MatvecParams p) {
 #pragma clang fp contract(off)
   constexpr bool kF32X = XP > 0;
-  __shared__ __attribute__((aligned(16))) uint8_t xq_lds[kF32X ? kQ4MaxF32InDim / 32 * 36 : 4];
+  __shared__ __attribute__((aligned(16))) uint8_t xq_lds[kF32X ? XP * (kQ4Threads / 8) * 36 : 4];
+  __shared__ float red[kQ4Waves];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row0 = (blockIdx.x * kQ4Waves + wave) * R;
@@ -97,7 +104,8 @@ __global__ __launch_bounds__(kQ4Threads) void q4_matvec_kernel(Q4MatvecParams p)
     const int g = min(row0 + r, p.total_rows - 1);
     const uint8_t *base = g < p.rows0 ? p.w0 : (g < p.rows01 ? p.w1 : p.w2);
     const int lr = g < p.rows0 ? g : (g < p.rows01 ? g - p.rows0 : g - p.rows01);
-    wrow[r] = base + (size_t)lr * row_bytes;
+    wrow[r] = p.swiglu ? ((g & 1) ? p.w1 : p.w0) + (size_t)(g >> 1) * row_bytes
+                       : base + (size_t)lr * row_bytes;
   }
 
   const int npairs = p.bpr >> 1;
@@ -117,15 +125,48 @@ __global__ __launch_bounds__(kQ4Threads) void q4_matvec_kernel(Q4MatvecParams p)
   if constexpr (kF32X) {
     // Activation loads first (clamped in bounds), then the first weight
     // rows: waiting for the activations then leaves the rows in flight.
-    f4 xr[XP];
+    f4 xr[XP], ar[PRO ? XP : 1];
 #pragma unroll
     for (int k = 0; k < XP; ++k) {
       const int blk = min(k * (kQ4Threads / 8) + (int)(threadIdx.x >> 3), p.bpr - 1);
-      xr[k] = *reinterpret_cast<const f4 *>(p.xf + (size_t)blk * 32 + (threadIdx.x & 7) * 4);
+      const size_t off = (size_t)blk * 32 + (threadIdx.x & 7) * 4;
+      xr[k] = *reinterpret_cast<const f4 *>(p.xf + off);
+      if constexpr (PRO == 1) ar[k] = *reinterpret_cast<const f4 *>(p.rms_w + off);
+      if constexpr (PRO == 2) ar[k] = *reinterpret_cast<const f4 *>(p.up + off);
     }
     __builtin_amdgcn_sched_barrier(0);
     load_rows(min(lane, npairs - 1));
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PRO == 1) {
+      // rmsnorm_vec (mistral_model.h:202-208) of the whole x
+      float ss = 0.0f;
+#pragma unroll
+      for (int k = 0; k < XP; ++k) {
+        const f4 v = xr[k];
+        if (k * (kQ4Threads / 8) + (int)(threadIdx.x >> 3) < p.bpr)
+          ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) red[wave] = ss;
+      __syncthreads();
+      ss = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
+      const float scale = 1.0f / sqrtf(ss / (float)(p.bpr * 32) + p.eps);
+#pragma unroll
+      for (int k = 0; k < XP; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xr[k][e] = (xr[k][e] * scale) * ar[k][e];
+    }
+    if constexpr (PRO == 2) {
+      // silu_mul_neon (mistral_model.h:174-199)
+#pragma unroll
+      for (int k = 0; k < XP; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float g = xr[k][e];
+          const float sig = 1.0f / (1.0f + expf(-g));
+          xr[k][e] = (g * sig) * ar[k][e];
+        }
+    }
 #pragma unroll
     for (int k = 0; k < XP; ++k) {
       const int blk = k * (kQ4Threads / 8) + (int)(threadIdx.x >> 3);
@@ -189,13 +230,25 @@ __global__ __launch_bounds__(kQ4Threads) void q4_matvec_kernel(Q4MatvecParams p)
     }
   }
 
+  float sum[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) sum[r] = wave_sum(acc[r]);
+  if (p.swiglu) {
+    static_assert(R == 2, "a wave holds one gate row and its up row");
+    // silu_mul_neon (mistral_model.h:174-199) of row j's gate and up sums
+    if (lane == 0 && row0 < p.total_rows) {
+      const float g = sum[0];
+      const float sig = 1.0f / (1.0f + expf(-g));
+      p.y0[row0 >> 1] = (g * sig) * sum[1];
+    }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float s = wave_sum(acc[r]);
     const int g = row0 + r;
     if (lane == 0 && g < p.total_rows) {
       float *y = g < p.rows0 ? p.y0 + g : (g < p.rows01 ? p.y1 + (g - p.rows0) : p.y2 + (g - p.rows01));
-      *y = s;
+      *y = p.resid ? p.resid[g] + sum[r] : sum[r];
     }
   }
 }
@@ -209,26 +262,43 @@ hipError_t launch_quantize_q8_0(const float *x, uint8_t *out, int nblocks, hipSt
   return hipGetLastError();
 }
 
+template <int PRO>
+hipError_t launch_q4_xp(const Q4MatvecParams &p, dim3 grid, hipStream_t s, hipEvent_t ev0,
+                        hipEvent_t ev1) {
+  constexpr int R = 2;
+  constexpr int kBlocksPerPass = kQ4Threads / 8;
+  static_assert(8 * kBlocksPerPass * 32 >= kQ4MaxFusedInDim, "fused passes cover the inputs");
+  if (p.bpr * 32 > kQ4MaxFusedInDim) return hipErrorInvalidValue;
+  if (p.bpr <= kBlocksPerPass)
+    hipExtLaunchKernelGGL((q4_matvec_kernel<R, 1, PRO>), grid, dim3(kQ4Threads), 0, s, ev0, ev1,
+                          0, p);
+  else if (p.bpr <= 2 * kBlocksPerPass)
+    hipExtLaunchKernelGGL((q4_matvec_kernel<R, 2, PRO>), grid, dim3(kQ4Threads), 0, s, ev0, ev1,
+                          0, p);
+  else if (p.bpr <= 4 * kBlocksPerPass)
+    hipExtLaunchKernelGGL((q4_matvec_kernel<R, 4, PRO>), grid, dim3(kQ4Threads), 0, s, ev0, ev1,
+                          0, p);
+  else
+    hipExtLaunchKernelGGL((q4_matvec_kernel<R, 8, PRO>), grid, dim3(kQ4Threads), 0, s, ev0, ev1,
+                          0, p);
+  return hipGetLastError();
+}
+
 hipError_t launch_q4_matvec(const Q4MatvecParams &p, hipStream_t s, hipEvent_t ev0,
                             hipEvent_t ev1) {
   constexpr int R = 2;
   const int rows_per_wg = kQ4Waves * R;
   const dim3 grid((p.total_rows + rows_per_wg - 1) / rows_per_wg);
-  constexpr int kBlocksPerPass = kQ4Threads / 8;
-  static_assert(8 * kBlocksPerPass * 32 >= kQ4MaxF32InDim, "fused passes cover kQ4MaxF32InDim");
-  if (!p.xf)
-    hipExtLaunchKernelGGL(q4_matvec_kernel<R, 0>, grid, dim3(kQ4Threads), 0, s, ev0, ev1, 0, p);
-  else if (p.bpr <= kBlocksPerPass)
-    hipExtLaunchKernelGGL(q4_matvec_kernel<R, 1>, grid, dim3(kQ4Threads), 0, s, ev0, ev1, 0, p);
-  else if (p.bpr <= 2 * kBlocksPerPass)
-    hipExtLaunchKernelGGL(q4_matvec_kernel<R, 2>, grid, dim3(kQ4Threads), 0, s, ev0, ev1, 0, p);
-  else if (p.bpr <= 4 * kBlocksPerPass)
-    hipExtLaunchKernelGGL(q4_matvec_kernel<R, 4>, grid, dim3(kQ4Threads), 0, s, ev0, ev1, 0, p);
-  else if (p.bpr * 32 <= kQ4MaxF32InDim)
-    hipExtLaunchKernelGGL(q4_matvec_kernel<R, 8>, grid, dim3(kQ4Threads), 0, s, ev0, ev1, 0, p);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  if (!p.xf) {
+    if (p.rms_w || p.up) return hipErrorInvalidValue;
+    hipExtLaunchKernelGGL((q4_matvec_kernel<R, 0, 0>), grid, dim3(kQ4Threads), 0, s, ev0, ev1, 0,
+                          p);
+    return hipGetLastError();
+  }
+  if (p.rms_w && p.up) return hipErrorInvalidValue;
+  if (p.rms_w) return launch_q4_xp<1>(p, grid, s, ev0, ev1);
+  if (p.up) return launch_q4_xp<2>(p, grid, s, ev0, ev1);
+  return launch_q4_xp<0>(p, grid, s, ev0, ev1);
 }
 
 }  // namespace mia
