@@ -1588,6 +1588,54 @@ int mia_decode_layer(float *x, const mia_layer_weights_typed *lw, const float *t
     return mv(lw->w2, nullptr, nullptr, x, nullptr, nullptr, dim, 0, 0, hb, hidden, nullptr,
               nullptr, x);
   }
+  bool all_kquant = types[4] == types[6];
+  for (int t : types) all_kquant = all_kquant && (t == MIA_TYPE_Q4_K || t == MIA_TYPE_Q6_K);
+  if (all_kquant && dim <= mia::kKqLayerMaxCols && hidden <= mia::kKqLayerMaxCols) {
+    // The same four matvec launches around the attention with Q4_K / Q6_K
+    // weights (Q4_K_M and its like): each forms its input's Q8_0 blocks, after
+    // the RMSNorm where there is one, in its prologue.
+    auto kl = [&](const void *w0, const void *w1, const void *w2, int t0, int t1, int t2,
+                  float *y0, float *y1, float *y2, int r0, int r1, int r2, const float *xf,
+                  int cols, const float *rms_w, const float *resid, bool swiglu) -> int {
+      mia::KqLayerParams p{};
+      p.w[0] = w0;
+      p.w[1] = w1;
+      p.w[2] = w2;
+      p.type[0] = t0;
+      p.type[1] = t1;
+      p.type[2] = t2;
+      p.y[0] = y0;
+      p.y[1] = y1;
+      p.y[2] = y2;
+      p.rows[0] = r0;
+      p.rows[1] = r1;
+      p.rows[2] = r2;
+      p.cols = cols;
+      p.xf = xf;
+      p.rms_w = rms_w;
+      p.eps = eps;
+      p.resid = resid;
+      p.swiglu = swiglu ? 1 : 0;
+      hipEvent_t ev0, ev1;
+      if (int rc = prof_pair(c, 5, &ev0, &ev1)) return rc;
+      HIP_TRY(mia::launch_kq_layer_matvec(p, s, ev0, ev1));
+      return MIA_OK;
+    };
+    if (int rc = kl(lw->wq, lw->wk, lw->wv, types[0], types[1], types[2], q, k, v, dim, kv_dim,
+                    kv_dim, x, dim, lw->rms_att, nullptr, false))
+      return rc;
+    if (int rc = decode_impl(q, k, v, theta_inv, k_layer, v_layer, xb2, n_heads, n_kv_heads,
+                             max_seq, pos, true, s))
+      return rc;
+    if (int rc = kl(lw->wo, nullptr, nullptr, types[3], 0, 0, x, nullptr, nullptr, dim, 0, 0, xb2,
+                    dim, nullptr, x, false))
+      return rc;
+    if (int rc = kl(lw->w1, lw->w3, nullptr, types[4], types[6], 0, hb, nullptr, nullptr, hidden,
+                    hidden, 0, x, dim, lw->rms_ffn, nullptr, true))
+      return rc;
+    return kl(lw->w2, nullptr, nullptr, types[5], 0, 0, x, nullptr, nullptr, dim, 0, 0, hb, hidden,
+              nullptr, x, false);
+  }
   // mistral_model.h:830-899
   HIP_TRY(mia::launch_rmsnorm(xb, x, lw->rms_att, dim, 1, eps, s));
   if (types[0] == MIA_TYPE_Q4_0 && types[1] == MIA_TYPE_Q4_0 && types[2] == MIA_TYPE_Q4_0 &&

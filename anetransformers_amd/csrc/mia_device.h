@@ -77,4 +77,43 @@ __device__ __forceinline__ void rope_pair(float &e, float &o, float c, float s) 
   o = no;
 }
 
+// One Q8_0 block from an aligned group of 8 lanes holding 4 values each
+// (values 4*sub .. 4*sub+3 of the block).  amax is order-free (max of absolute
+// values), d = amax / 127 and id = 1 / d are IEEE-rounded divides, and
+// q = round-half-even(x * id) saturated to int8, as vcvtnq_s32_f32 + vqmovn.
+// Returns d; q holds this lane's 4 integers (as floats).
+__device__ __forceinline__ float q8_block_q(const f4 v, f4 &q) {
+  float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  a = fmaxf(a, __shfl_xor(a, 1));
+  a = fmaxf(a, __shfl_xor(a, 2));
+  a = fmaxf(a, __shfl_xor(a, 4));
+  const float d = a / 127.0f;
+  q = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (a != 0.0f) {
+    const float id = 1.0f / d;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float r = __builtin_rintf(v[i] * id);
+      q[i] = fminf(fmaxf(r, -128.0f), 127.0f);
+    }
+  }
+  return d;
+}
+
+__device__ __forceinline__ unsigned q8_pack(const f4 q) {
+  unsigned packed = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) packed |= ((unsigned)(int)q[i] & 0xFFu) << (8 * i);
+  return packed;
+}
+
+// Writes d (lane sub 0) and this lane's 4 int8 to the 36-byte block at ob.
+template <typename Byte>
+__device__ __forceinline__ void q8_block_part(const f4 v, int sub, Byte *ob) {
+  f4 q;
+  const float d = q8_block_q(v, q);
+  if (sub == 0) *reinterpret_cast<float *>(ob) = d;
+  *reinterpret_cast<unsigned *>(ob + 4 + 4 * sub) = q8_pack(q);
+}
+
 }  // namespace mia

@@ -229,4 +229,33 @@ hipError_t launch_add(float *x, const float *y, int n, hipStream_t s);
 // gate [n] = gate * sigmoid(gate) * up (the SwiGLU product).
 hipError_t launch_silu_mul(float *gate, const float *up, long n, hipStream_t s);
 
+// The decode layer's Q4_K / Q6_K matvecs with their neighbouring steps
+// inside: up to three matrices of one input (each of type kTypeQ4K or
+// kTypeQ6K), their rows stacked as virtual rows (w[0]'s, then w[1]'s, then
+// w[2]'s).  The fp32 input xf [cols] (16-byte aligned, cols a multiple of 256
+// up to kKqLayerMaxCols) is RMS-normalised (when rms_w is set: (xf * (1 /
+// sqrtf(mean(xf^2) + eps))) * rms_w, launch_rmsnorm's arithmetic) and
+// quantised to Q8_0 blocks (launch_quantize_q8_0's) by every workgroup, so
+// each row's sum equals launch_typed_matvec's on the separately formed
+// blocks, bit for bit.  Epilogues: y = resid[row] + sum (resid may be y), or
+// swiglu: w[0] (gate) and w[1] (up) of rows[0] rows each, interleaved so that
+// one wave holds row j of both and writes y[0][j] = gate * (1 / (1 +
+// expf(-gate))) * up.  rows[0] and rows[0] + rows[1] must be multiples of the
+// workgroup's rows (launch_kq_layer_matvec checks it).
+constexpr int kKqLayerMaxCols = 16384;
+struct KqLayerParams {
+  const void *w[3];
+  int type[3];
+  float *y[3];
+  int rows[3];
+  int cols;
+  const float *xf;
+  const float *rms_w;
+  float eps;
+  const float *resid;
+  int swiglu;
+};
+hipError_t launch_kq_layer_matvec(const KqLayerParams &p, hipStream_t s, hipEvent_t ev0,
+                                  hipEvent_t ev1);
+
 }  // namespace mia

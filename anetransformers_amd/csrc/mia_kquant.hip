@@ -183,8 +183,9 @@ __device__ __forceinline__ u4 load_u4_unaligned(const uint8_t *p) {
 }
 
 // The K-quant matvec: each wave takes R consecutive rows and lane l the
-// 32-value groups l, l + 64, ... of all of them, so that the lane's 32 x
-// values are loaded (and, from Q8_0 blocks, formed) once for R rows.
+// 32-value groups l, l + 64, ... of all of them (with Q8_0 inputs the group
+// pairs l, l + 64, ..., kq_load_pair), so that the lane's x values are loaded
+// (and, from Q8_0 blocks, formed) once for R rows.
 //   Q4_K: the group's 32 nibbles as packed fp16 pairs (0x6400 | n is
 //         1024 + n), then p = fl16(n * vd) as one packed fma, (1024 + n) * vd
 //         - 1024 * vd, whose exact value is n * vd (1024 * vd is exact in
@@ -305,12 +306,198 @@ __device__ __forceinline__ float kq_dot(const Q6KRaw &raw, int g, const float (&
   return ds0 * (acc[0][0] + acc[0][1]) + ds1 * (acc[1][0] + acc[1][1]);
 }
 
+// Q8_0 inputs (x = d_x * q_x per 32-value block, the group): the same
+// weights against the integers q_x, the block's sum scaled by d_x once.
+//   Q6_K: the sub-block sums sum (q - 32) q_x are exact integers (v_dot4 on
+//         the 6-bit values, minus 32 sum q_x), then (ds0 S0 + ds1 S1) d_x.
+//   Q4_K: the fp16 weights (formed as above) against q_x as fp16 (exact), two
+//         products per v_dot2_f32_f16 (each product exact in fp32), then d_x.
+// Both are the reference's sum of w * (d_x q_x) reassociated.
+struct Q8Ints {   // one block: q_x as int8 and its two 16-value sums
+  unsigned q[8];
+  int s0, s1;
+  float d;
+};
+struct Q8Halves {  // one block: q_x as fp16, values {4i, 4i + 2} and {4i + 1, 4i + 3}
+  h2 a[8], b[8];
+  float d;
+};
+
+__device__ __forceinline__ int sdot4(unsigned a, unsigned b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// 36-byte Q8_0 block -> both forms (the int8 and the fp16 values)
+__device__ __forceinline__ void q8_ints(const unsigned (&blk)[9], Q8Ints &x) {
+  x.d = __builtin_bit_cast(float, blk[0]);
+  x.s0 = 0;
+  x.s1 = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    x.q[i] = blk[1 + i];
+    if (i < 4)
+      x.s0 = sdot4(x.q[i], 0x01010101u, x.s0);
+    else
+      x.s1 = sdot4(x.q[i], 0x01010101u, x.s1);
+  }
+}
+
+// four int8 -> fp16 pairs {q0, q2}, {q1, q3}: 1024 + (q + 128) by the 0x6400
+// exponent, minus 1152 (all exact)
+__device__ __forceinline__ void i8x4_halves(unsigned q, h2 &a, h2 &b) {
+  const unsigned t = q ^ 0x80808080u;
+  unsigned ua, ub;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(ua) : "v"(t), "s"(0x00FF00FFu), "v"(0x64006400u));
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(ub) : "v"(t >> 8), "s"(0x00FF00FFu), "v"(0x64006400u));
+  const h2 k = {(_Float16)1152.0f, (_Float16)1152.0f};
+  a = __builtin_bit_cast(h2, ua) - k;
+  b = __builtin_bit_cast(h2, ub) - k;
+}
+
+__device__ __forceinline__ void q8_halves(const unsigned (&blk)[9], Q8Halves &x) {
+  x.d = __builtin_bit_cast(float, blk[0]);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) i8x4_halves(blk[1 + i], x.a[i], x.b[i]);
+}
+
+__device__ __forceinline__ float kq_dot8(const Q6KRaw &raw, int g, const Q8Ints &x) {
+#pragma clang fp contract(off)
+  const int n0 = 32 * (g & 7);
+  const int lo_sh = n0 < 128 ? 0 : 4;
+  const int r = n0 >> 6;
+  const int hi_sh = r == 0 ? 0 : (r == 1 ? 4 : (r == 2 ? 2 : 6));
+  const float d = half_bits(raw.dh);
+  const float ds0 = d * (float)(int)(signed char)(raw.sc2 & 0xFF);
+  const float ds1 = d * (float)(int)(signed char)(raw.sc2 >> 8);
+  const u4 ql[2] = {raw.ql0, raw.ql1}, qh[2] = {raw.qh0, raw.qh1};
+  int s0 = -32 * x.s0, s1 = -32 * x.s1;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const unsigned q = ((ql[i >> 2][i & 3] >> lo_sh) & 0x0F0F0F0Fu) |
+                       (((qh[i >> 2][i & 3] >> hi_sh) & 0x03030303u) << 4);
+    if (i < 4)
+      s0 = sdot4(q, x.q[i], s0);
+    else
+      s1 = sdot4(q, x.q[i], s1);
+  }
+  return (ds0 * (float)s0 + ds1 * (float)s1) * x.d;
+}
+
+__device__ __forceinline__ float kq_dot8(const Q4KRaw &raw, int g, const Q8Halves &x) {
+#pragma clang fp contract(off)
+  const int j = g & 7;
+  const u4 hdr = raw.hdr;
+  const float d = half_bits(hdr[0] & 0xFFFF), dmin = half_bits(hdr[0] >> 16);
+  const int p8 = 8 * (j & 3);
+  const unsigned x1 = hdr[1] >> p8, x2 = hdr[2] >> p8, x3 = hdr[3] >> p8;
+  const unsigned sv = j < 4 ? (x1 & 63) : ((x3 & 0xF) | ((x1 >> 2) & 0x30));
+  const unsigned mv = j < 4 ? (x2 & 63) : (((x3 >> 4) & 0xF) | ((x2 >> 2) & 0x30));
+  const _Float16 vd = (_Float16)(d * (float)sv), vm = (_Float16)(dmin * (float)mv);
+  const h2 vd2 = {vd, vd}, vm2 = {vm, vm};
+  const _Float16 c = (_Float16)-1024.0f * vd;
+  const h2 c2 = {c, c}, k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+  const int sh = 4 * (j & 1);
+  const unsigned magic = 0x64006400u;
+  const bool fast = __all(__builtin_fabsf((float)vd) <= 63.5f);
+  const u4 qv[2] = {raw.qa, raw.qb};
+  float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const unsigned t = qv[i >> 2][i & 3] >> sh;
+    unsigned ua, ub;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(ua) : "v"(t), "s"(0x000F000Fu), "v"(magic));
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(ub) : "v"(t >> 8), "s"(0x000F000Fu), "v"(magic));
+    const h2 na = __builtin_bit_cast(h2, ua), nb = __builtin_bit_cast(h2, ub);
+    h2 pa, pb;
+    if (fast) {
+      pa = __builtin_elementwise_fma(na, vd2, c2);
+      pb = __builtin_elementwise_fma(nb, vd2, c2);
+    } else {
+      pa = (na - k1024) * vd2;
+      pb = (nb - k1024) * vd2;
+    }
+    const h2 wa = pa - vm2, wb = pb - vm2;
+    acc0 = __builtin_amdgcn_fdot2(wa, x.a[i], acc0, false);
+    acc1 = __builtin_amdgcn_fdot2(wb, x.b[i], acc1, false);
+  }
+  return (acc0 + acc1) * x.d;
+}
+
 template <int TYPE>
 using KqRaw = typename std::conditional<TYPE == kTypeQ4K, Q4KRaw, Q6KRaw>::type;
+template <int TYPE>
+using Q8Form = typename std::conditional<TYPE == kTypeQ4K, Q8Halves, Q8Ints>::type;
+
+// Group pairs that share their quant bytes, one load for both: pair p of a
+// row is groups g0 = 2p and 2p + 1 for Q4_K (a qs run's low and high
+// nibbles) and g0 = 8 (p / 4) + p % 4 and g0 + 4 for Q6_K (the same ql and
+// qh bytes; only the scales differ).
+struct Q6KPair {
+  u4 ql0, ql1, qh0, qh1;
+  unsigned sc_a, sc_b, dh;
+};
+template <int TYPE>
+using KqPair = typename std::conditional<TYPE == kTypeQ4K, Q4KRaw, Q6KPair>::type;
+
+template <int TYPE>
+__device__ __forceinline__ int pair_g0(int p) {
+  return TYPE == kTypeQ4K ? 2 * p : 8 * (p >> 2) + (p & 3);
+}
+template <int TYPE>
+__device__ __forceinline__ int pair_g1(int g0) {
+  return TYPE == kTypeQ4K ? g0 + 1 : g0 + 4;
+}
+
+__device__ __forceinline__ void kq_load_pair(const uint8_t *row, int p, Q4KRaw &r) {
+  kq_load(row, 2 * p, r);
+}
+
+__device__ __forceinline__ void kq_load_pair(const uint8_t *row, int p, Q6KPair &r) {
+  const uint8_t *blk = row + (size_t)(p >> 2) * kQ6KBytes;
+  const int n0 = 32 * (p & 3);
+  r.ql0 = load_u4_unaligned(blk + n0);
+  r.ql1 = load_u4_unaligned(blk + n0 + 16);
+  r.qh0 = load_u4_unaligned(blk + 128 + (n0 & 63));
+  r.qh1 = load_u4_unaligned(blk + 128 + (n0 & 63) + 16);
+  r.sc_a = load_u16(blk + 192 + (n0 >> 4));
+  r.sc_b = load_u16(blk + 200 + (n0 >> 4));
+  r.dh = load_u16(blk + 208);
+}
+
+// pair p's two group sums, the first group's added first
+template <int TYPE>
+__device__ __forceinline__ void kq_dot8_pair(const KqPair<TYPE> &raw, int g0,
+                                             const Q8Form<TYPE> &x0, const Q8Form<TYPE> &x1,
+                                             float &acc) {
+  if constexpr (TYPE == kTypeQ4K) {
+    acc += kq_dot8(raw, g0, x0);
+    acc += kq_dot8(raw, g0 + 1, x1);
+  } else {
+    Q6KRaw v;
+    v.ql0 = raw.ql0;
+    v.ql1 = raw.ql1;
+    v.qh0 = raw.qh0;
+    v.qh1 = raw.qh1;
+    v.dh = raw.dh;
+    v.sc2 = raw.sc_a;
+    acc += kq_dot8(v, g0, x0);
+    v.sc2 = raw.sc_b;
+    acc += kq_dot8(v, g0 + 4, x1);
+  }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void q8_form(const unsigned (&blk)[9], Q8Form<TYPE> &x) {
+  if constexpr (TYPE == kTypeQ4K)
+    q8_halves(blk, x);
+  else
+    q8_ints(blk, x);
+}
 
 // R rows per wave, 4 waves per workgroup.
 template <int TYPE, bool XQ8, int R>
-__global__ void __launch_bounds__(256) kquant_matvec_kernel(const uint8_t *W, long row_bytes,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XQ8 ? 4 : 1)))
+kquant_matvec_kernel(const uint8_t *W, long row_bytes,
                                                             const void *x, float *y, int rows,
                                                             int cols) {
   const int lane = threadIdx.x & 63;
@@ -320,27 +507,40 @@ __global__ void __launch_bounds__(256) kquant_matvec_kernel(const uint8_t *W, lo
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
-  for (int g = lane; g < ngroups; g += 64) {
-    KqRaw<TYPE> raw[R];
+  if constexpr (XQ8) {
+    // Q8_0 blocks (fp32 d, 32 int8; 4-byte aligned), the reference's values
+    // d * q (mistral_model.h:662-666) as d times the integers; a lane takes
+    // group pairs
+    const int npairs = ngroups >> 1;
+    for (int p = lane; p < npairs; p += 64) {
+      KqPair<TYPE> raw[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r)  // a row past the end reloads the last row
-      kq_load(W + (size_t)min(row0 + r, rows - 1) * row_bytes, g, raw[r]);
-    float xs[32];
-    if constexpr (XQ8) {
-      // Q8_0 block g (fp32 d, 32 int8; 4-byte aligned): values d * q in fp32
-      // as the reference forms them (mistral_model.h:662-666)
-      const unsigned *blk = reinterpret_cast<const unsigned *>(
-          reinterpret_cast<const uint8_t *>(x) + (size_t)g * 36);
-      unsigned w[9];
+      for (int r = 0; r < R; ++r)  // a row past the end reloads the last row
+        kq_load_pair(W + (size_t)min(row0 + r, rows - 1) * row_bytes, p, raw[r]);
+      const int g0 = pair_g0<TYPE>(p), g1 = pair_g1<TYPE>(g0);
+      const unsigned *b0 = reinterpret_cast<const unsigned *>(
+          reinterpret_cast<const uint8_t *>(x) + (size_t)g0 * 36);
+      const unsigned *b1 = reinterpret_cast<const unsigned *>(
+          reinterpret_cast<const uint8_t *>(x) + (size_t)g1 * 36);
+      unsigned w0[9], w1[9];
 #pragma unroll
-      for (int k = 0; k < 9; ++k) w[k] = blk[k];
-      const float d = __builtin_bit_cast(float, w[0]);
+      for (int k = 0; k < 9; ++k) {
+        w0[k] = b0[k];
+        w1[k] = b1[k];
+      }
+      Q8Form<TYPE> x0, x1;
+      q8_form<TYPE>(w0, x0);
+      q8_form<TYPE>(w1, x1);
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
+      for (int r = 0; r < R; ++r) kq_dot8_pair<TYPE>(raw[r], g0, x0, x1, acc[r]);
+    }
+  } else {
+    for (int g = lane; g < ngroups; g += 64) {
+      KqRaw<TYPE> raw[R];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          xs[4 * k + e] = d * (float)(int)(signed char)((w[1 + k] >> (8 * e)) & 0xFF);
-    } else {
+      for (int r = 0; r < R; ++r)  // a row past the end reloads the last row
+        kq_load(W + (size_t)min(row0 + r, rows - 1) * row_bytes, g, raw[r]);
+      float xs[32];
       const f4 *xv = reinterpret_cast<const f4 *>(reinterpret_cast<const float *>(x) + 32 * g);
       f4 v[8];
 #pragma unroll
@@ -352,15 +552,189 @@ __global__ void __launch_bounds__(256) kquant_matvec_kernel(const uint8_t *W, lo
         xs[4 * k + 2] = v[k].z;
         xs[4 * k + 3] = v[k].w;
       }
-    }
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] += kq_dot(raw[r], g, xs);
+      for (int r = 0; r < R; ++r) acc[r] += kq_dot(raw[r], g, xs);
+    }
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const float v = wave_sum(acc[r]);
     if (lane == 0 && row0 + r < rows) y[row0 + r] = v;
   }
+}
+
+// The decode layer's K-quant matvecs (KqLayerParams): every workgroup of 8
+// waves forms the Q8_0 blocks of its input in LDS while its first weight
+// groups are in flight, then runs kquant_matvec_kernel<TYPE, true, R>'s loop
+// on them.  Thread t loads the input's 4-value groups t + 512k, the groups of
+// rmsnorm_kernel's thread t, so its sum of squares, the wave sums and their
+// fixed combination are rmsnorm_kernel's own.  A workgroup's rows lie in one
+// matrix.
+template <int R, int XP, bool RMS>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
+kq_layer_matvec_kernel(KqLayerParams p) {
+#pragma clang fp contract(off)
+  // the input's Q8_0 blocks twice: as the blocks (Q6_K rows), and as the
+  // fp16 pairs of Q8Halves (Q4_K rows; group g's 16-byte chunk c at 4g +
+  // ((c + g + g / 4) & 3), so that a wave's reads of a chunk are
+  // conflict-free) with the scales apart
+  __shared__ __attribute__((aligned(16))) uint8_t xq_lds[XP * 64 * 36];
+  __shared__ u4 xh_lds[XP * 64 * 4];
+  __shared__ float xd_lds[XP * 64];
+  __shared__ float red[8];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rows01 = p.rows[0] + p.rows[1];
+  const int total = rows01 + p.rows[2];
+  const int row0 = (blockIdx.x * 8 + wave) * R;
+  const int wg_row = blockIdx.x * 8 * R;
+  const int m = wg_row < p.rows[0] ? 0 : (wg_row < rows01 ? 1 : 2);
+  const int ngroups = p.cols >> 5;
+
+  f4 xr[XP], ar[RMS ? XP : 1];
+#pragma unroll
+  for (int k = 0; k < XP; ++k) {
+    const int blk = min(64 * k + (tid >> 3), ngroups - 1);
+    const size_t off = (size_t)blk * 32 + (tid & 7) * 4;
+    xr[k] = *reinterpret_cast<const f4 *>(p.xf + off);
+    if constexpr (RMS) ar[k] = *reinterpret_cast<const f4 *>(p.rms_w + off);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto prologue = [&]() {
+#pragma clang fp contract(off)
+    if constexpr (RMS) {
+      // rmsnorm_vec (mistral_model.h:202-208) of the whole input
+      float ss = 0.0f;
+#pragma unroll
+      for (int k = 0; k < XP; ++k) {
+        const f4 v = xr[k];
+        if (64 * k + (tid >> 3) < ngroups) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) red[wave] = ss;
+      // LDS writes visible; the weight loads stay outstanding
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      ss = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
+      const float scale = 1.0f / sqrtf(ss / (float)p.cols + p.eps);
+#pragma unroll
+      for (int k = 0; k < XP; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xr[k][e] = (xr[k][e] * scale) * ar[k][e];
+    }
+#pragma unroll
+    for (int k = 0; k < XP; ++k) {
+      const int blk = 64 * k + (tid >> 3);
+      if (blk < ngroups)  // whole 8-lane groups
+      {
+        const int sub = tid & 7;
+        f4 q;
+        const float d = q8_block_q(xr[k], q);
+        if (sub == 0) {
+          *reinterpret_cast<float *>(xq_lds + blk * 36) = d;
+          xd_lds[blk] = d;
+        }
+        *reinterpret_cast<unsigned *>(xq_lds + blk * 36 + 4 + 4 * sub) = q8_pack(q);
+        const h2 a = {(_Float16)q[0], (_Float16)q[2]}, b = {(_Float16)q[1], (_Float16)q[3]};
+        const int c = sub >> 1;
+        u2 *dst = reinterpret_cast<u2 *>(&xh_lds[4 * blk + ((c + blk + (blk >> 2)) & 3)]);
+        dst[sub & 1] = u2{__builtin_bit_cast(unsigned, a), __builtin_bit_cast(unsigned, b)};
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+
+  auto body = [&](auto type_tag) {
+#pragma clang fp contract(off)
+    constexpr int TYPE = decltype(type_tag)::value;
+    const long rb = (long)(p.cols / kQKK) * (TYPE == kTypeQ4K ? kQ4KBytes : kQ6KBytes);
+    const uint8_t *wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {  // rows past the end reload the last row
+      const int g = min(row0 + r, total - 1);
+      const void *base;
+      int lr;
+      if (p.swiglu) {
+        base = (g & 1) ? p.w[1] : p.w[0];
+        lr = g >> 1;
+      } else {
+        base = p.w[m];
+        lr = g - (m == 0 ? 0 : (m == 1 ? p.rows[0] : rows01));
+      }
+      wrow[r] = reinterpret_cast<const uint8_t *>(base) + (size_t)lr * rb;
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    // the input's block g in the form the type's dot takes
+    auto lds_form = [&](int g, Q8Form<TYPE> &xf) {
+      if constexpr (TYPE == kTypeQ4K) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const u4 v = xh_lds[4 * g + ((c + g + (g >> 2)) & 3)];
+          // each element through a scalar: __builtin_bit_cast of a vector
+          // element (v.y ...) reads element 0 with this compiler
+          const unsigned e0 = v.x, e1 = v.y, e2 = v.z, e3 = v.w;
+          xf.a[2 * c] = __builtin_bit_cast(h2, e0);
+          xf.b[2 * c] = __builtin_bit_cast(h2, e1);
+          xf.a[2 * c + 1] = __builtin_bit_cast(h2, e2);
+          xf.b[2 * c + 1] = __builtin_bit_cast(h2, e3);
+        }
+        xf.d = xd_lds[g];
+      } else {
+        const unsigned *blk = reinterpret_cast<const unsigned *>(xq_lds + g * 36);
+        unsigned w[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) w[k] = blk[k];
+        q8_ints(w, xf);
+      }
+    };
+    const int npairs = ngroups >> 1;
+    KqPair<TYPE> raw[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) kq_load_pair(wrow[r], min(lane, npairs - 1), raw[r]);
+    __builtin_amdgcn_sched_barrier(0);
+    prologue();
+    for (int pp = lane; pp < npairs; pp += 64) {
+      if (pp != lane) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) kq_load_pair(wrow[r], pp, raw[r]);
+      }
+      const int g0 = pair_g0<TYPE>(pp), g1 = pair_g1<TYPE>(g0);
+      Q8Form<TYPE> x0, x1;
+      lds_form(g0, x0);
+      lds_form(g1, x1);
+#pragma unroll
+      for (int r = 0; r < R; ++r) kq_dot8_pair<TYPE>(raw[r], g0, x0, x1, acc[r]);
+    }
+    float sum[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) sum[r] = wave_sum(acc[r]);
+    if (p.swiglu) {
+      // silu_mul_neon (mistral_model.h:174-199) of row j's gate and up sums
+      if constexpr (R == 2) {
+        if (lane == 0 && row0 < total) {
+          const float gt = sum[0];
+          const float sig = 1.0f / (1.0f + expf(-gt));
+          p.y[0][row0 >> 1] = (gt * sig) * sum[1];
+        }
+      }
+      return;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int g = row0 + r;
+      if (lane == 0 && g < total) {
+        const int mm = g < p.rows[0] ? 0 : (g < rows01 ? 1 : 2);
+        float *y = p.y[mm] + (g - (mm == 0 ? 0 : (mm == 1 ? p.rows[0] : rows01)));
+        *y = p.resid ? p.resid[g] + sum[r] : sum[r];
+      }
+    }
+  };
+  if (p.type[m] == kTypeQ4K)
+    body(std::integral_constant<int, kTypeQ4K>{});
+  else
+    body(std::integral_constant<int, kTypeQ6K>{});
 }
 
 // One thread per group: 32 fp32 weights of a row.
@@ -507,30 +881,48 @@ template <int TYPE, int R>
 void launch_kq_r(const uint8_t *w, long rb, const void *x, bool xq8, float *y, int rows, int cols,
                  hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   const dim3 grid((rows + 4 * R - 1) / (4 * R)), block(256);
-  if (xq8)
-    hipExtLaunchKernelGGL((kquant_matvec_kernel<TYPE, true, R>), grid, block, 0, s, ev0, ev1, 0,
-                          w, rb, x, y, rows, cols);
-  else
+  if (xq8) {
+    if constexpr (R <= 2)  // launch_kq_matvec_t takes 1 or 2 rows per wave for Q8_0 inputs
+      hipExtLaunchKernelGGL((kquant_matvec_kernel<TYPE, true, R>), grid, block, 0, s, ev0, ev1,
+                            0, w, rb, x, y, rows, cols);
+  } else
     hipExtLaunchKernelGGL((kquant_matvec_kernel<TYPE, false, R>), grid, block, 0, s, ev0, ev1, 0,
                           w, rb, x, y, rows, cols);
 }
 
 // Rows per wave, measured on the Mistral shapes: one row per wave while the
 // matrix is small (the most waves in flight), more rows once there are
-// enough waves and the x loads (128 B per lane and row for fp32 x, 36 B for
-// Q8_0 blocks) start to cost.
+// enough waves and the x loads (128 B per lane and row for fp32 x, 72 B per
+// group pair for Q8_0 blocks) start to cost; Q6_K rows on Q8_0 inputs, whose
+// pairs carry 70 bytes each, one row per wave at every size.
 template <int TYPE>
 hipError_t launch_kq_matvec_t(const void *W, long rb, const void *x, bool xq8, float *y,
                               int rows, int cols, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   const uint8_t *w = reinterpret_cast<const uint8_t *>(W);
   const bool large = (long)rows * cols >= (32L << 20);
-  const int R = xq8 ? (large ? 2 : 1) : (rows < 2048 ? 1 : (large ? 4 : 2));
+  const int R = xq8 ? (TYPE == kTypeQ4K && large ? 2 : 1) : (rows < 2048 ? 1 : (large ? 4 : 2));
   if (R == 4)
     launch_kq_r<TYPE, 4>(w, rb, x, xq8, y, rows, cols, s, ev0, ev1);
   else if (R == 2)
     launch_kq_r<TYPE, 2>(w, rb, x, xq8, y, rows, cols, s, ev0, ev1);
   else
     launch_kq_r<TYPE, 1>(w, rb, x, xq8, y, rows, cols, s, ev0, ev1);
+  return hipGetLastError();
+}
+
+template <int R, bool RMS>
+hipError_t launch_kq_layer_r(const KqLayerParams &p, int ngroups, hipStream_t s, hipEvent_t ev0,
+                             hipEvent_t ev1) {
+  const int total = p.rows[0] + p.rows[1] + p.rows[2];
+  const dim3 grid((total + 8 * R - 1) / (8 * R)), block(512);
+  if (ngroups <= 64)
+    hipExtLaunchKernelGGL((kq_layer_matvec_kernel<R, 1, RMS>), grid, block, 0, s, ev0, ev1, 0, p);
+  else if (ngroups <= 128)
+    hipExtLaunchKernelGGL((kq_layer_matvec_kernel<R, 2, RMS>), grid, block, 0, s, ev0, ev1, 0, p);
+  else if (ngroups <= 256)
+    hipExtLaunchKernelGGL((kq_layer_matvec_kernel<R, 4, RMS>), grid, block, 0, s, ev0, ev1, 0, p);
+  else
+    hipExtLaunchKernelGGL((kq_layer_matvec_kernel<R, 8, RMS>), grid, block, 0, s, ev0, ev1, 0, p);
   return hipGetLastError();
 }
 
@@ -571,6 +963,36 @@ hipError_t launch_typed_matvec(const void *W, int type, const void *x, bool x_q8
     case kTypeQ40: return launch_matvec_t<kTypeQ40>(W, rb, x, x_q8, y, rows, cols, s, ev0, ev1);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_kq_layer_matvec(const KqLayerParams &p, hipStream_t s, hipEvent_t ev0,
+                                  hipEvent_t ev1) {
+  if (p.cols <= 0 || p.cols % kQKK || p.cols > kKqLayerMaxCols || !p.xf) return hipErrorInvalidValue;
+  const int nmat = p.swiglu ? 2 : 3;
+  for (int i = 0; i < 3; ++i) {
+    if (p.rows[i] < 0) return hipErrorInvalidValue;
+    if (p.rows[i] == 0) continue;
+    if (i >= nmat || !p.w[i] || (p.type[i] != kTypeQ4K && p.type[i] != kTypeQ6K))
+      return hipErrorInvalidValue;
+  }
+  const int total = p.rows[0] + p.rows[1] + p.rows[2];
+  if (total <= 0) return hipErrorInvalidValue;
+  // rows per wave as launch_typed_matvec picks them for Q8_0 inputs; the
+  // SwiGLU form holds a gate row and its up row per wave
+  const bool large = (long)total * p.cols >= (32L << 20);
+  bool all_q4k = true;
+  for (int i = 0; i < 3; ++i) all_q4k = all_q4k && (p.rows[i] == 0 || p.type[i] == kTypeQ4K);
+  const int R = p.swiglu ? 2 : (all_q4k && large ? 2 : 1);
+  if (p.swiglu && (p.rows[0] != p.rows[1] || p.rows[2] || p.type[0] != p.type[1] || p.resid))
+    return hipErrorInvalidValue;
+  if (!p.swiglu && (p.rows[0] % (8 * R) || (p.rows[0] + p.rows[1]) % (8 * R)))
+    return hipErrorInvalidValue;  // a workgroup would straddle two matrices
+  const int ngroups = p.cols >> 5;
+  if (R == 2)
+    return p.rms_w ? launch_kq_layer_r<2, true>(p, ngroups, s, ev0, ev1)
+                   : launch_kq_layer_r<2, false>(p, ngroups, s, ev0, ev1);
+  return p.rms_w ? launch_kq_layer_r<1, true>(p, ngroups, s, ev0, ev1)
+                 : launch_kq_layer_r<1, false>(p, ngroups, s, ev0, ev1);
 }
 
 hipError_t launch_typed_dequant(const void *W, int type, float *out, int rows, int cols,

@@ -40,32 +40,6 @@ __device__ __forceinline__ int dot4(unsigned a, unsigned b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// One Q8_0 block from an aligned group of 8 lanes holding 4 values each
-// (values 4*sub .. 4*sub+3 of the block).  amax is order-free (max of absolute
-// values), d = amax / 127 and id = 1 / d are IEEE-rounded divides, and
-// q = round-half-even(x * id) saturated to int8, as vcvtnq_s32_f32 + vqmovn.
-// Writes d (lane sub 0) and this lane's 4 int8 to the 36-byte block at ob.
-template <typename Byte>
-__device__ __forceinline__ void q8_block_part(const f4 v, int sub, Byte *ob) {
-  float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  a = fmaxf(a, __shfl_xor(a, 1));
-  a = fmaxf(a, __shfl_xor(a, 2));
-  a = fmaxf(a, __shfl_xor(a, 4));
-  const float d = a / 127.0f;
-  unsigned packed = 0;
-  if (a != 0.0f) {
-    const float id = 1.0f / d;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float r = __builtin_rintf(v[i] * id);
-      r = fminf(fmaxf(r, -128.0f), 127.0f);
-      packed |= ((unsigned)(int)r & 0xFFu) << (8 * i);
-    }
-  }
-  if (sub == 0) *reinterpret_cast<float *>(ob) = d;
-  *reinterpret_cast<unsigned *>(ob + 4 + 4 * sub) = packed;
-}
-
 __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x,
                                                             uint8_t *__restrict__ out,
                                                             int nblocks) {

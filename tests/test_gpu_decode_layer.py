@@ -7,8 +7,9 @@ oracle/q4_oracle.c).
 Bars:
 - The pair matvec: rows within the W4A8 bound of tests/test_gpu_q4.py; the
   fp32-input form bit-identical to quantize + matvec.
-- The all-Q4_0 layer bit-identical to the same steps issued one C-ABI call at
-  a time (the layer's plumbing adds no arithmetic of its own).
+- The all-Q4_0 layer, and layers of Q4_K / Q6_K weights, bit-identical to the
+  same steps issued one C-ABI call at a time (the fused prologues and
+  epilogues add no arithmetic of their own).
 - The layer against the oracle normwise within 1e-2 of the output's scale.
   fp32 reassociation, the attention's fp16 operands and the GPU's exp / sin /
   cos differ from the oracle's by ulps; the layer then re-quantises its
@@ -135,6 +136,72 @@ def test_decode_layer_is_its_steps_call_by_call():
     check(L.mia_silu_mul_f32(hb.ptr, hb2.ptr, hidden, S))
     check(L.mia_quantize_q8_0(hb.ptr, q8.ptr, hidden, S))
     check(L.mia_q4_0_matvec(dev["w2"].ptr, q8.ptr, xb.ptr, dim, hidden, S))
+    check(L.mia_stream_sync(S))
+    want = x1 + xb.download(dim, np.float32)
+    assert np.array_equal(kc_g, dkc.download(kc.shape, np.uint16))
+    assert np.array_equal(vc_g, dvc.download(vc.shape, np.uint16))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+KMIXES = {
+    "q4_k_m": Q4_K_M,
+    "q6_k": {k: O.TYPE_Q6_K for k in O.MATS},
+    # Q / K / V of three runs of types; gate and up of one type, as the
+    # fused K-quant layer needs
+    "kmix": {"wq": O.TYPE_Q6_K, "wk": O.TYPE_Q4_K, "wv": O.TYPE_Q6_K, "wo": O.TYPE_Q6_K,
+             "w1": O.TYPE_Q6_K, "w3": O.TYPE_Q6_K, "w2": O.TYPE_Q4_K},
+}
+
+
+@pytest.mark.parametrize("mix,dim,hidden,nh,nkv", [
+    ("q4_k_m", 512, 1024, 4, 1),      # inputs of 16 and 32 Q8_0 blocks
+    ("q6_k", 1024, 2816, 8, 2),       # 32 and 88
+    ("kmix", 2048, 5632, 16, 4),      # 64 and 176
+])
+def test_kquant_decode_layer_is_its_steps_call_by_call(mix, dim, hidden, nh, nkv):
+    # Q4_K / Q6_K layer == RMSNorm, Q8_0 blocks, a typed matvec per matrix,
+    # mia_decode_step, Q8_0 blocks, Wo, residual, RMSNorm, Q8_0 blocks,
+    # W1, W3, SwiGLU, Q8_0 blocks, W2, residual, issued one call at a time
+    G.say(f"decode layer: {mix} call-by-call composition dim={dim} hidden={hidden}")
+    L = G.lib()
+    M, pos = 64, 45
+    kvd = dim // nh * nkv
+    types = KMIXES[mix]
+    g = np.random.default_rng(dim + hidden)
+    W = _layer(g, types, dim, hidden, nh, nkv)
+    kc, vc = D.ring(g, M, kv_dim=kvd, filled=pos)
+    x = g.standard_normal(dim).astype(np.float32)
+    th = O.theta_inv(D.THETA, 128)
+    got, kc_g, vc_g = _gpu_layer(L, W, types, x, th, kc, vc, dim, hidden, nh, nkv, M, pos)
+
+    dev = {k: DB.from_array(v) for k, v in W.items()}
+    dx, dth, dkc, dvc = DB.from_array(x), DB.from_array(th), DB.from_array(kc), DB.from_array(vc)
+    xb, xb2, q, k, v = DB(dim * 4), DB(dim * 4), DB(dim * 4), DB(kvd * 4), DB(kvd * 4)
+    hb, hb2, q8 = DB(hidden * 4), DB(hidden * 4), DB(hidden // 32 * 36)
+    S = None
+
+    def mv(name, y, rows, cols):
+        check(L.mia_matvec_q8(dev[name].ptr, types[name], q8.ptr, y.ptr, rows, cols, S), name)
+
+    check(L.mia_rmsnorm_f32(xb.ptr, dx.ptr, dev["rms_att"].ptr, dim, 1, 1e-5, S))
+    check(L.mia_quantize_q8_0(xb.ptr, q8.ptr, dim, S))
+    mv("wq", q, dim, dim)
+    mv("wk", k, kvd, dim)
+    mv("wv", v, kvd, dim)
+    check(L.mia_decode_step(q.ptr, k.ptr, v.ptr, dth.ptr, dkc.ptr, dvc.ptr, xb2.ptr, nh, nkv, 128,
+                            M, pos, S))
+    check(L.mia_quantize_q8_0(xb2.ptr, q8.ptr, dim, S))
+    mv("wo", xb, dim, dim)
+    check(L.mia_stream_sync(S))
+    x1 = dx.download(dim, np.float32) + xb.download(dim, np.float32)
+    dx.upload(x1)
+    check(L.mia_rmsnorm_f32(xb.ptr, dx.ptr, dev["rms_ffn"].ptr, dim, 1, 1e-5, S))
+    check(L.mia_quantize_q8_0(xb.ptr, q8.ptr, dim, S))
+    mv("w1", hb, hidden, dim)
+    mv("w3", hb2, hidden, dim)
+    check(L.mia_silu_mul_f32(hb.ptr, hb2.ptr, hidden, S))
+    check(L.mia_quantize_q8_0(hb.ptr, q8.ptr, hidden, S))
+    mv("w2", xb, dim, hidden)
     check(L.mia_stream_sync(S))
     want = x1 + xb.download(dim, np.float32)
     assert np.array_equal(kc_g, dkc.download(kc.shape, np.uint16))
