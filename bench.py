@@ -750,7 +750,9 @@ def decode_layer_leg(lib, dec: "Decode", steps: int, warmup: int) -> dict:
                                   "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                                   "note": "the whole layer's bytes over the step's time "
-                                          "(11-16 launches per layer)"}}
+                                          "(6 launches per layer: 4 matvecs with the "
+                                          "RMSNorms, quantisation, residuals and SwiGLU "
+                                          "inside, the attention and its merge)"}}
         del dl
     return out
 
