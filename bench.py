@@ -685,8 +685,7 @@ def km_weights(lib, seed: int):
 class DecodeLayers:
     """The whole decode layer on the GPU (mia_decode_layer), 32 layers, for the
     token at position 32768 over the headline's full 32768-slot rings: Q4_0
-    weights (3.9 GB, the reference's fused QKV and gate / up dispatches) or
-    Q4_K_M weights (4.45 GB, per-type matvecs); x carried from layer to
+    weights (3.9 GB) or Q4_K_M weights (4.45 GB); x carried from layer to
     layer."""
 
     Q4_SIZES = (("wq", DIM, DIM), ("wk", KV_DIM, DIM), ("wv", KV_DIM, DIM), ("wo", DIM, DIM),
