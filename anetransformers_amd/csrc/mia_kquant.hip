@@ -625,8 +625,7 @@ kq_layer_matvec_kernel(KqLayerParams p) {
 #pragma unroll
     for (int k = 0; k < XP; ++k) {
       const int blk = 64 * k + (tid >> 3);
-      if (blk < ngroups)  // whole 8-lane groups
-      {
+      if (blk < ngroups) {  // whole 8-lane groups
         const int sub = tid & 7;
         f4 q;
         const float d = q8_block_q(xr[k], q);
