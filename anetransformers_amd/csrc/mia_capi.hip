@@ -520,6 +520,34 @@ extern "C" __attribute__((visibility("hidden"))) int mia_internal_set_error(int 
   return set_err(code, "%s", msg);
 }
 
+// Pinned host memory and stream-ordered copies for the drop-in's staging
+// (mia_dropin.c): one transfer each way per call, on the library stream the
+// kernels of a NULL-stream call run on.
+extern "C" __attribute__((visibility("hidden"))) int mia_internal_host_alloc(void **p,
+                                                                             size_t bytes) {
+  if (!p || bytes == 0) return set_err(MIA_ERR_INVALID, "host_alloc: NULL pointer or 0 bytes");
+  HIP_TRY(hipHostMalloc(p, bytes, hipHostMallocDefault));
+  return MIA_OK;
+}
+
+extern "C" __attribute__((visibility("hidden"))) int mia_internal_host_free(void *p) {
+  if (p) HIP_TRY(hipHostFree(p));
+  return MIA_OK;
+}
+
+extern "C" __attribute__((visibility("hidden"))) int mia_internal_copy_async(void *dst,
+                                                                             const void *src,
+                                                                             size_t bytes,
+                                                                             int to_device) {
+  if (bytes == 0) return MIA_OK;
+  if (!dst || !src) return set_err(MIA_ERR_INVALID, "NULL pointer");
+  DevCtx *c;
+  if (int rc = current_ctx(&c)) return rc;
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, to_device ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost,
+                         c->stream));
+  return MIA_OK;
+}
+
 extern "C" {
 
 int mia_version(void) { return 100; }

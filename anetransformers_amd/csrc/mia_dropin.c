@@ -1,9 +1,12 @@
 /*
  * mia_dropin.c -- host C side of the drop-in: the reference's attention-step
  * signatures (include/mia_dropin.h) implemented over the libmiattn C ABI.
- * Host buffers are staged through one device buffer owned by this file;
- * every call is synchronous, like the reference's.  Not re-entrant (neither is
- * the reference: mistral_model.h shares m->q / m->att across calls).
+ * Host buffers are staged through one device buffer owned by this file and
+ * its pinned host mirror: a call copies its inputs into the mirror at their
+ * device offsets, moves them in one transfer, runs its kernels and brings
+ * its outputs back in one transfer, all on the library stream; every call is
+ * synchronous, like the reference's.  Not re-entrant (neither is the
+ * reference: mistral_model.h shares m->q / m->att across calls).
  */
 #include <stdint.h>
 #include <stdio.h>
@@ -12,11 +15,16 @@
 
 #include "../../include/mia_dropin.h"
 
-int mia_internal_set_error(int code, const char *msg); /* mia_capi.hip, not exported */
+/* mia_capi.hip, not exported */
+int mia_internal_set_error(int code, const char *msg);
+int mia_internal_host_alloc(void **p, size_t bytes);
+int mia_internal_host_free(void *p);
+int mia_internal_copy_async(void *dst, const void *src, size_t bytes, int to_device);
 
 static int g_abort = 1;
 static __thread int g_status = 0;
-static char *g_dbuf = NULL;
+static char *g_dbuf = NULL;  /* device staging */
+static char *g_hbuf = NULL;  /* its pinned host mirror, the same size */
 static size_t g_dbuf_bytes = 0;
 
 void mia_dropin_set_abort(int abort_on_error) { g_abort = abort_on_error; }
@@ -40,23 +48,52 @@ static int fail(int rc, const char *what) {
         }                                \
     } while (0)
 
-/* Device staging area of at least `bytes`, carved by the callers. */
+/* Device staging area of at least `bytes` and its pinned host mirror,
+ * carved by the callers (the same offsets in both). */
 static int dbuf(size_t bytes) {
     if (bytes <= g_dbuf_bytes) return MIA_OK;
     if (g_dbuf) {
         int rc = mia_free(g_dbuf);
         if (rc) return rc;
     }
+    if (g_hbuf) {
+        int rc = mia_internal_host_free(g_hbuf);
+        if (rc) return rc;
+    }
     g_dbuf = NULL;
+    g_hbuf = NULL;
     g_dbuf_bytes = 0;
     size_t sz = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
     int rc = mia_malloc((void **)&g_dbuf, sz);
     if (rc) return rc;
+    rc = mia_internal_host_alloc((void **)&g_hbuf, sz);
+    if (rc) {
+        mia_free(g_dbuf);
+        g_dbuf = NULL;
+        return rc;
+    }
     g_dbuf_bytes = sz;
     return MIA_OK;
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+/* Host input -> the mirror at device offset off (NULL src: nothing). */
+static void put(size_t off, const void *src, size_t bytes) {
+    if (src && bytes) memcpy(g_hbuf + off, src, bytes);
+}
+/* The mirror's [0, end) -> the device, one stream-ordered transfer. */
+static int push(size_t end) { return mia_internal_copy_async(g_dbuf, g_hbuf, end, 1); }
+/* The device's [off, off + bytes) -> the mirror, one transfer, then the
+ * stream is synchronised (the kernels before it included). */
+static int pull(size_t off, size_t bytes) {
+    int rc = mia_internal_copy_async(g_hbuf + off, g_dbuf + off, bytes, 0);
+    return rc ? rc : mia_stream_sync(NULL);
+}
+/* The mirror at device offset off -> a host output. */
+static void get(void *dst, size_t off, size_t bytes) {
+    if (dst && bytes) memcpy(dst, g_hbuf + off, bytes);
+}
 
 void mia_dropin_kv_alloc(KVCache *c, int n_layers, int n_kv_heads, int head_dim, int max_seq) {
     g_status = 0;
@@ -113,16 +150,18 @@ void mia_dropin_apply_rope_batch(float *Q, float *K, int start_pos, const float 
     size_t kb = K ? (size_t)S * n_kv_heads * head_dim * sizeof(float) : 0;
     size_t tb = (size_t)(head_dim / 2) * sizeof(float);
     TRY("apply_rope", dbuf(align256(qb) + align256(kb) + align256(tb)));
+    const size_t ko = align256(qb), to = align256(qb) + align256(kb);
     float *dq = Q ? (float *)g_dbuf : NULL;
-    float *dk = K ? (float *)(g_dbuf + align256(qb)) : NULL;
-    float *dt = (float *)(g_dbuf + align256(qb) + align256(kb));
-    TRY("apply_rope", mia_memcpy_h2d(dt, theta_inv, tb));
-    if (Q) TRY("apply_rope", mia_memcpy_h2d(dq, Q, qb));
-    if (K) TRY("apply_rope", mia_memcpy_h2d(dk, K, kb));
+    float *dk = K ? (float *)(g_dbuf + ko) : NULL;
+    float *dt = (float *)(g_dbuf + to);
+    put(0, Q, qb);
+    put(ko, K, kb);
+    put(to, theta_inv, tb);
+    TRY("apply_rope", push(to + tb));
     TRY("apply_rope", mia_rope_f32(dq, dk, S, start_pos, dt, n_heads, n_kv_heads, head_dim, NULL));
-    TRY("apply_rope", mia_stream_sync(NULL));
-    if (Q) TRY("apply_rope", mia_memcpy_d2h(Q, dq, qb));
-    if (K) TRY("apply_rope", mia_memcpy_d2h(K, dk, kb));
+    TRY("apply_rope", pull(0, to));
+    get(Q, 0, qb);
+    get(K, ko, kb);
 }
 
 void mia_dropin_apply_rope(float *q, float *k, int pos, const float *theta_inv, int n_heads,
@@ -143,12 +182,13 @@ void mia_dropin_gqa_attention(float *q, float *att, float *out, _Float16 *kcache
     TRY("gqa_attention", dbuf(2 * align256(nb)));
     float *dq = (float *)g_dbuf;
     float *dout = (float *)(g_dbuf + align256(nb));
-    TRY("gqa_attention", mia_memcpy_h2d(dq, q, nb));
+    put(0, q, nb);
+    TRY("gqa_attention", push(nb));
     TRY("gqa_attention", mia_gqa_attention(dq, dout, (const uint16_t *)kcache_base,
                                            (const uint16_t *)vcache_base, n_heads, heads_per_kv, hd,
                                            max_seq, pos, NULL));
-    TRY("gqa_attention", mia_stream_sync(NULL));
-    TRY("gqa_attention", mia_memcpy_d2h(out, dout, nb));
+    TRY("gqa_attention", pull(align256(nb), nb));
+    get(out, align256(nb), nb);
 }
 
 void mia_dropin_kv_write_batch(KVCache *kv, int layer, int start_pos, const float *K_buf,
@@ -162,8 +202,9 @@ void mia_dropin_kv_write_batch(KVCache *kv, int layer, int start_pos, const floa
     TRY("kv_write_batch", dbuf(2 * align256(nb)));
     float *dk = (float *)g_dbuf;
     float *dv = (float *)(g_dbuf + align256(nb));
-    TRY("kv_write_batch", mia_memcpy_h2d(dk, K_buf, nb));
-    TRY("kv_write_batch", mia_memcpy_h2d(dv, V_buf, nb));
+    put(0, K_buf, nb);
+    put(align256(nb), V_buf, nb);
+    TRY("kv_write_batch", push(align256(nb) + nb));
     size_t lay = (size_t)layer * kv->max_seq * kv->kv_dim;
     TRY("kv_write_batch", mia_kv_write_f32((uint16_t *)(kv->k_cache + lay),
                                            (uint16_t *)(kv->v_cache + lay), dk, dv, S, start_pos,
@@ -189,14 +230,15 @@ void mia_dropin_attention_batch(const float *Q, float *attn_out, const KVCache *
     TRY("attention_batch", dbuf(2 * align256(nb)));
     float *dq = (float *)g_dbuf;
     float *dout = (float *)(g_dbuf + align256(nb));
-    TRY("attention_batch", mia_memcpy_h2d(dq, Q, nb));
+    put(0, Q, nb);
+    TRY("attention_batch", push(nb));
     size_t lay = (size_t)layer * kv->max_seq * kv->kv_dim;
     TRY("attention_batch",
         mia_attention_batch(dq, dout, (const uint16_t *)(kv->k_cache + lay),
                             (const uint16_t *)(kv->v_cache + lay), c->n_heads, c->n_kv_heads,
                             c->head_dim, kv->max_seq, start_pos, S, NULL));
-    TRY("attention_batch", mia_stream_sync(NULL));
-    TRY("attention_batch", mia_memcpy_d2h(attn_out, dout, nb));
+    TRY("attention_batch", pull(align256(nb), nb));
+    get(attn_out, align256(nb), nb);
 }
 
 void mia_dropin_prefill_chunk_attention(KVCache *kv, int layer, const float *Q, const float *K,
@@ -228,17 +270,18 @@ void mia_dropin_prefill_chunk_attention(KVCache *kv, int layer, const float *Q, 
     float *dt = (float *)(g_dbuf + a + 2 * b);
     int *dp = (int *)(g_dbuf + a + 2 * b + t);
     float *dout = (float *)(g_dbuf + a + 2 * b + t + pp);
-    TRY(what, mia_memcpy_h2d(dq, Q, qb));
-    TRY(what, mia_memcpy_h2d(dk, K, kb));
-    TRY(what, mia_memcpy_h2d(dv, V, kb));
-    TRY(what, mia_memcpy_h2d(dt, theta_inv, tb));
-    TRY(what, mia_memcpy_h2d(dp, positions, pb));
+    put(0, Q, qb);
+    put(a, K, kb);
+    put(a + b, V, kb);
+    put(a + 2 * b, theta_inv, tb);
+    put(a + 2 * b + t, positions, pb);
+    TRY(what, push(a + 2 * b + t + pb));
     size_t lay = (size_t)layer * kv->max_seq * kv->kv_dim;
     TRY(what, mia_attention_chunk(dq, dk, dv, dp, dt, (uint16_t *)(kv->k_cache + lay),
                                   (uint16_t *)(kv->v_cache + lay), dout, n_heads, n_kv_heads, hd,
                                   kv->max_seq, chunk_size, NULL));
-    TRY(what, mia_stream_sync(NULL));
-    TRY(what, mia_memcpy_d2h(attn_out, dout, qb));
+    TRY(what, pull(a + 2 * b + t + pp, qb));
+    get(attn_out, a + 2 * b + t + pp, qb);
     /* mistral_model.h:952, per token */
     for (int i = 0; i < chunk_size; i++)
         if (kv->len < kv->max_seq && positions[i] + 1 > kv->len) kv->len = positions[i] + 1;
@@ -297,10 +340,11 @@ static void step_common(const char *what, KVCache *kv, int layer, const float *Q
     float *dv = (float *)(g_dbuf + a + b);
     float *dt = (float *)(g_dbuf + a + 2 * b);
     float *dout = (float *)(g_dbuf + a + 2 * b + t);
-    TRY(what, mia_memcpy_h2d(dq, Q, qb));
-    TRY(what, mia_memcpy_h2d(dk, K, kb));
-    TRY(what, mia_memcpy_h2d(dv, V, kb));
-    TRY(what, mia_memcpy_h2d(dt, theta_inv, tb));
+    put(0, Q, qb);
+    put(a, K, kb);
+    put(a + b, V, kb);
+    put(a + 2 * b, theta_inv, tb);
+    TRY(what, push(a + 2 * b + tb));
     size_t lay = (size_t)layer * kv->max_seq * kv->kv_dim;
     if (staged) {
         size_t rows = (size_t)S * kv->kv_dim;
@@ -315,8 +359,8 @@ static void step_common(const char *what, KVCache *kv, int layer, const float *Q
                                      (uint16_t *)(kv->v_cache + lay), dout, n_heads, n_kv_heads,
                                      hd, kv->max_seq, start_pos, S, NULL));
     }
-    TRY(what, mia_stream_sync(NULL));
-    TRY(what, mia_memcpy_d2h(out, dout, qb));
+    TRY(what, pull(a + 2 * b + t, qb));
+    get(out, a + 2 * b + t, qb);
     if (staged) {
         g_stage_done[layer] = 1;
         return; /* the ring and len change at commit */
@@ -352,10 +396,11 @@ void mia_dropin_quantize_q8_0(const float *x, mia_block_q8_0 *out, int n) {
     TRY("quantize_f32_to_q8_0", dbuf(align256(xb) + align256(qb)));
     float *dx = (float *)g_dbuf;
     void *dq = g_dbuf + align256(xb);
-    TRY("quantize_f32_to_q8_0", mia_memcpy_h2d(dx, x, xb));
+    put(0, x, xb);
+    TRY("quantize_f32_to_q8_0", push(xb));
     TRY("quantize_f32_to_q8_0", mia_quantize_q8_0(dx, dq, n, NULL));
-    TRY("quantize_f32_to_q8_0", mia_stream_sync(NULL));
-    TRY("quantize_f32_to_q8_0", mia_memcpy_d2h(out, dq, qb));
+    TRY("quantize_f32_to_q8_0", pull(align256(xb), qb));
+    get(out, align256(xb), qb);
 }
 
 void mia_dropin_q4_matvec_sdot_parallel_fused_qkv(const void *Wq, const void *Wk, const void *Wv,
@@ -375,13 +420,15 @@ void mia_dropin_q4_matvec_sdot_parallel_fused_qkv(const void *Wq, const void *Wk
     float *dyq = (float *)(g_dbuf + align256(xb));
     float *dyk = kv_dim ? (float *)(g_dbuf + align256(xb) + align256(qb)) : NULL;
     float *dyv = kv_dim ? (float *)(g_dbuf + align256(xb) + align256(qb) + align256(kb)) : NULL;
-    TRY(what, mia_memcpy_h2d(dx, x_q8, xb));
+    put(0, x_q8, xb);
+    TRY(what, push(xb));
     TRY(what, mia_q4_0_matvec_qkv(Wq, Wk, Wv, dx, dyq, dyk, dyv, dim, kv_dim, in_dim, NULL));
-    TRY(what, mia_stream_sync(NULL));
-    TRY(what, mia_memcpy_d2h(yq, dyq, qb));
+    const size_t yo = align256(xb);
+    TRY(what, pull(yo, kv_dim ? align256(qb) + align256(kb) + kb : qb));
+    get(yq, yo, qb);
     if (kv_dim) {
-        TRY(what, mia_memcpy_d2h(yk, dyk, kb));
-        TRY(what, mia_memcpy_d2h(yv, dyv, kb));
+        get(yk, yo + align256(qb), kb);
+        get(yv, yo + align256(qb) + align256(kb), kb);
     }
 }
 
@@ -400,11 +447,12 @@ void mia_dropin_q4_matvec_sdot_parallel_fused_pair(const void *W1, const void *W
     void *dx = g_dbuf;
     float *dy1 = (float *)(g_dbuf + align256(xb));
     float *dy3 = (float *)(g_dbuf + align256(xb) + align256(yb));
-    TRY(what, mia_memcpy_h2d(dx, x_q8, xb));
+    put(0, x_q8, xb);
+    TRY(what, push(xb));
     TRY(what, mia_q4_0_matvec_pair(W1, W3, dx, dy1, dy3, out_dim, in_dim, NULL));
-    TRY(what, mia_stream_sync(NULL));
-    TRY(what, mia_memcpy_d2h(y1, dy1, yb));
-    TRY(what, mia_memcpy_d2h(y3, dy3, yb));
+    TRY(what, pull(align256(xb), align256(yb) + yb));
+    get(y1, align256(xb), yb);
+    get(y3, align256(xb) + align256(yb), yb);
 }
 
 void mia_dropin_q4_matvec_sdot_parallel(const void *W, uint32_t type, const mia_block_q8_0 *x_q8,
@@ -427,10 +475,11 @@ void mia_dropin_q4_matvec_sdot_parallel(const void *W, uint32_t type, const mia_
     TRY(what, dbuf(align256(xb) + align256(yb)));
     void *dx = g_dbuf;
     float *dy = (float *)(g_dbuf + align256(xb));
-    TRY(what, mia_memcpy_h2d(dx, x_q8, xb));
+    put(0, x_q8, xb);
+    TRY(what, push(xb));
     TRY(what, mia_matvec_q8(W, (int)type, dx, dy, out_dim, in_dim, NULL));
-    TRY(what, mia_stream_sync(NULL));
-    TRY(what, mia_memcpy_d2h(y, dy, yb));
+    TRY(what, pull(align256(xb), yb));
+    get(y, align256(xb), yb);
 }
 
 void mia_dropin_verify_stage(KVCache *kv, int layer, const float *Q, const float *K, const float *V,
