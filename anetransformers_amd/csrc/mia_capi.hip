@@ -2,7 +2,7 @@
 // Host code only: validation, per-device context (stream, split-K scratch,
 // work buffers) and launch planning.
 #include <hip/hip_runtime.h>
-#include <rocblas/rocblas.h>
+#include <hipblaslt/hipblaslt.h>
 
 #include <climits>
 #include <cstdarg>
@@ -33,6 +33,16 @@ constexpr int kMaxSeq = 1 << 22;  // ring capacity limit; in-layer offsets are 6
 // token takes its slot by scanning them (S^2 / 2 reads); longer chunks use a
 // per-slot area instead (one more launch, linear in S).
 constexpr int kChunkScanMax = 64;
+// The fp16 GEMMs of the weight types other than Q4_0 (hipBLASLt): workspace
+// size, algorithms timed on a shape's first call, shapes remembered.
+constexpr size_t kLtWorkspace = size_t(64) << 20;
+constexpr int kLtCandidates = 4;
+constexpr size_t kLtMaxShapes = 64;
+
+struct LtPick {
+  int m, n, k;
+  hipblasLtMatmulAlgo_t algo;
+};
 
 struct DevCtx {
   bool ready = false;
@@ -54,11 +64,14 @@ struct DevCtx {
   int *owner = nullptr;  // long chunks of mia_attention_chunk: last token per ring slot, -1 at rest
   int owner_slots = 0;
   // Weight types other than Q4_0 in the GEMM: the weights' fp16 planes and
-  // the partial products, multiplied by rocBLAS gemm_ex (handle created on
-  // first use).
+  // the partial products, multiplied by hipBLASLt (handle and workspace
+  // created on first use, the algorithm of each GEMM shape picked on its
+  // first call: lt_gemm).
   float *wbuf = nullptr;
   size_t wbuf_bytes = 0;
-  rocblas_handle blas = nullptr;
+  hipblasLtHandle_t lt = nullptr;
+  void *lt_ws = nullptr;
+  std::vector<LtPick> lt_picks;
   void *dl_work = nullptr;  // mia_decode_layer's vectors
   size_t dl_work_bytes = 0;
   // Opt-in kernel timing: an event pair around the main kernel of each call
@@ -206,14 +219,113 @@ int ensure_dl_work(DevCtx *c, size_t bytes) {
   return MIA_OK;
 }
 
-int ensure_blas(DevCtx *c) {
-  if (c->blas == nullptr) {
-    rocblas_handle h = nullptr;
-    const rocblas_status st = rocblas_create_handle(&h);
-    if (st != rocblas_status_success)
-      return set_err(MIA_ERR_HIP, "rocblas_create_handle: %s", rocblas_status_to_string(st));
-    c->blas = h;
+int ensure_lt(DevCtx *c) {
+  if (c->lt_ws == nullptr) HIP_TRY(hipMalloc(&c->lt_ws, kLtWorkspace));
+  if (c->lt == nullptr) {
+    hipblasLtHandle_t h = nullptr;
+    const hipblasStatus_t st = hipblasLtCreate(&h);
+    if (st != HIPBLAS_STATUS_SUCCESS) return set_err(MIA_ERR_HIP, "hipblasLtCreate: status %d", (int)st);
+    c->lt = h;
   }
+  return MIA_OK;
+}
+
+// The descriptors of C = A^T B: A the fp16 weights (column-major k x m, i.e.
+// m rows of k values), B the fp16 activations (k x n: n rows of k), C fp32
+// column-major m x n (n rows of m outputs), fp32 accumulation.
+struct LtDesc {
+  hipblasLtMatmulDesc_t md = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+  hipblasStatus_t st = HIPBLAS_STATUS_SUCCESS;
+  LtDesc(int m, int n, int k) {
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    st = hipblasLtMatmulDescCreate(&md, HIPBLAS_COMPUTE_32F, HIP_R_32F);
+    if (st == HIPBLAS_STATUS_SUCCESS)
+      st = hipblasLtMatmulDescSetAttribute(md, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta));
+    if (st == HIPBLAS_STATUS_SUCCESS)
+      st = hipblasLtMatmulDescSetAttribute(md, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb));
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&la, HIP_R_16F, k, m, k);
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&lb, HIP_R_16F, k, n, k);
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&lc, HIP_R_32F, m, n, m);
+  }
+  ~LtDesc() {
+    if (lc) hipblasLtMatrixLayoutDestroy(lc);
+    if (lb) hipblasLtMatrixLayoutDestroy(lb);
+    if (la) hipblasLtMatrixLayoutDestroy(la);
+    if (md) hipblasLtMatmulDescDestroy(md);
+  }
+};
+
+// C = A^T B (LtDesc) on stream s.  The algorithm of a shape is picked on its
+// first call: the heuristic's first kLtCandidates algorithms are each run
+// once, then timed over three calls on s (the host waits for s once per
+// candidate), and the fastest is kept for every later call of that shape in
+// this process, so repeated calls of a shape give identical results.  Another
+// process may keep another algorithm: its sums differ in rounding only (fp32
+// accumulation either way).  Beyond kLtMaxShapes shapes the heuristic's
+// first algorithm is used untimed.
+int lt_gemm(DevCtx *c, int m, int n, int k, const _Float16 *A, const _Float16 *B, float *C,
+            hipStream_t s) {
+  LtDesc d(m, n, k);
+  if (d.st != HIPBLAS_STATUS_SUCCESS)
+    return set_err(MIA_ERR_HIP, "hipBLASLt descriptors (%d x %d x %d): status %d", m, n, k, (int)d.st);
+  const float one = 1.0f, zero = 0.0f;
+  auto run = [&](const hipblasLtMatmulAlgo_t &algo) {
+    return hipblasLtMatmul(c->lt, d.md, &one, A, d.la, B, d.lb, &zero, C, d.lc, C, d.lc, &algo,
+                           c->lt_ws, kLtWorkspace, s);
+  };
+  for (const LtPick &p : c->lt_picks) {
+    if (p.m != m || p.n != n || p.k != k) continue;
+    const hipblasStatus_t st = run(p.algo);
+    if (st != HIPBLAS_STATUS_SUCCESS) return set_err(MIA_ERR_HIP, "hipblasLtMatmul: status %d", (int)st);
+    return MIA_OK;
+  }
+  hipblasLtMatmulPreference_t pref = nullptr;
+  hipblasStatus_t st = hipblasLtMatmulPreferenceCreate(&pref);
+  const uint64_t ws = kLtWorkspace;
+  if (st == HIPBLAS_STATUS_SUCCESS)
+    st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
+                                               sizeof(ws));
+  hipblasLtMatmulHeuristicResult_t res[kLtCandidates];
+  int got = 0;
+  if (st == HIPBLAS_STATUS_SUCCESS)
+    st = hipblasLtMatmulAlgoGetHeuristic(c->lt, d.md, d.la, d.lb, d.lc, d.lc, pref, kLtCandidates, res,
+                                         &got);
+  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+  if (st != HIPBLAS_STATUS_SUCCESS || got < 1)
+    return set_err(MIA_ERR_HIP, "hipBLASLt: no algorithm for %d x %d x %d (status %d)", m, n, k, (int)st);
+  int best = -1;
+  const bool remember = c->lt_picks.size() < kLtMaxShapes;
+  if (remember && got > 1) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t he = hipEventCreate(&e0);
+    if (he == hipSuccess) he = hipEventCreate(&e1);
+    float best_ms = 0.0f;
+    for (int i = 0; he == hipSuccess && i < got; ++i) {
+      if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kLtWorkspace) continue;
+      if (run(res[i].algo) != HIPBLAS_STATUS_SUCCESS) continue;
+      he = hipEventRecord(e0, s);
+      bool ok = true;
+      for (int r = 0; r < 3 && ok; ++r) ok = run(res[i].algo) == HIPBLAS_STATUS_SUCCESS;
+      if (he == hipSuccess) he = hipEventRecord(e1, s);
+      if (he == hipSuccess) he = hipEventSynchronize(e1);
+      float ms = 0.0f;
+      if (he == hipSuccess) he = hipEventElapsedTime(&ms, e0, e1);
+      if (he == hipSuccess && ok && (best < 0 || ms < best_ms)) {
+        best = i;
+        best_ms = ms;
+      }
+    }
+    if (e1) (void)hipEventDestroy(e1);
+    if (e0) (void)hipEventDestroy(e0);
+    if (he != hipSuccess) return set_err(MIA_ERR_HIP, "timing the GEMM algorithms: %s", hipGetErrorString(he));
+  }
+  for (int i = 0; best < 0 && i < got; ++i)
+    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= kLtWorkspace) best = i;
+  if (best < 0) return set_err(MIA_ERR_HIP, "hipBLASLt: no usable algorithm for %d x %d x %d", m, n, k);
+  if (remember) c->lt_picks.push_back(LtPick{m, n, k, res[best].algo});
+  st = run(res[best].algo);
+  if (st != HIPBLAS_STATUS_SUCCESS) return set_err(MIA_ERR_HIP, "hipblasLtMatmul: status %d", (int)st);
   return MIA_OK;
 }
 
@@ -1178,7 +1290,7 @@ static int typed_gemm_impl(DevCtx *c, const void *W, int type, const float *X, f
   const size_t bc1 = al256((size_t)2 * S * N * 4), bc2 = al256((size_t)S * N * 4);
   if (int rc = ensure_wbuf(c, bp + bc1 + (lo ? bc2 : 0))) return rc;
   if (int rc = ensure_split_work(c, (size_t)2 * S * K * sizeof(_Float16))) return rc;
-  if (int rc = ensure_blas(c)) return rc;
+  if (int rc = ensure_lt(c)) return rc;
   char *w = reinterpret_cast<char *>(c->wbuf);
   char *planes = packed ? reinterpret_cast<char *>(const_cast<void *>(W)) : w;
   const size_t bw = al256((size_t)N * K * 2);
@@ -1191,20 +1303,9 @@ static int typed_gemm_impl(DevCtx *c, const void *W, int type, const float *X, f
   if (!packed) HIP_TRY(mia::launch_typed_split(W, type, whi, wlo, rs, N, K, s));
   if (!reuse_x)
     HIP_TRY(mia::launch_split_hilo(X, (long)S * K, xhi, xhi + (size_t)S * K, c->num_cus, s));
-  const float one = 1.0f, zero = 0.0f;
-  rocblas_status st = rocblas_set_stream(c->blas, s);
-  if (st == rocblas_status_success)
-    st = rocblas_gemm_ex(c->blas, rocblas_operation_transpose, rocblas_operation_none, N, 2 * S,
-                         K, &one, whi, rocblas_datatype_f16_r, K, xhi, rocblas_datatype_f16_r, K,
-                         &zero, C1, rocblas_datatype_f32_r, N, C1, rocblas_datatype_f32_r, N,
-                         rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-  if (st == rocblas_status_success && lo)
-    st = rocblas_gemm_ex(c->blas, rocblas_operation_transpose, rocblas_operation_none, N, S, K,
-                         &one, wlo, rocblas_datatype_f16_r, K, xhi, rocblas_datatype_f16_r, K,
-                         &zero, C2, rocblas_datatype_f32_r, N, C2, rocblas_datatype_f32_r, N,
-                         rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-  if (st != rocblas_status_success)
-    return set_err(MIA_ERR_HIP, "rocblas_gemm_ex: %s", rocblas_status_to_string(st));
+  if (int rc = lt_gemm(c, N, 2 * S, K, whi, xhi, C1, s)) return rc;
+  if (lo)
+    if (int rc = lt_gemm(c, N, S, K, wlo, xhi, C2, s)) return rc;
   HIP_TRY(mia::launch_hilo_combine(C1, C2, rs, Y, S, N, add, s));
   return MIA_OK;
 }

@@ -892,7 +892,8 @@ def typed_leg(lib, steps: int, warmup: int) -> dict:
             "workload": "mia_prefill_layer_typed_packed x 32, S 512 after 1536 cached: the "
                         "weights in the GEMM operand form made once at set-up (mia_gemm_pack: "
                         "fp16 values of Q4_K, row-scaled hi + lo halves of Q6_K, 18 GB), fp16 "
-                        "MFMA GEMMs (rocBLAS gemm_ex) on the activations' hi + lo halves",
+                        "MFMA GEMMs (hipBLASLt, each shape's algorithm picked by timing on its first "
+                        "call, in the warm-up) on the activations' hi + lo halves",
             "value": round(N_LAYERS * layer_flop / (pf_ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
             "ms_per_step": round(pf_ms, 3), "flop_per_layer": layer_flop,
             "per_call_conversion_ms_per_step": round(pf_conv_ms, 3),

@@ -363,7 +363,10 @@ int mia_matvec_q8(const void *W, int type, const void *x_q8, float *y, int out_d
 /* tiled_q4_gemm for every type (mistral/mistral_ane_prefill.h:1018-1042):
  * Y[S][out_dim] = X[S][in_dim] . W^T, fp32 X and Y (dev, 16-byte aligned).
  * Q4_0 is mia_q4_0_gemm_f32.  The other types multiply on fp16 MFMA with fp32
- * accumulation (rocBLAS gemm_ex), within fp32 rounding of the reference's
+ * accumulation (hipBLASLt; the algorithm of each GEMM shape is timed and
+ * picked on the shape's first call in the process, which therefore waits for
+ * the stream once; later calls of the shape reuse it, so repeated calls give
+ * bit-identical results), within fp32 rounding of the reference's
  * dequantise + cblas_sgemm: X is split into fp16 hi + lo halves, as for Q4_0;
  * Q4_K and F16 weights are fp16 values and enter exactly; Q6_K and F32
  * weights are scaled per row by a power of two and split into hi + lo halves

@@ -265,6 +265,29 @@ def test_gemm_rows_of_every_magnitude(t):
         assert np.all(got[:, 5] == 0)
 
 
+@pytest.mark.parametrize("t,N,K", [
+    (O.TYPE_Q4_K, 4096, 4096), (O.TYPE_Q4_K, 1024, 4096), (O.TYPE_Q6_K, 1024, 4096),
+    (O.TYPE_Q4_K, 14336, 4096), (O.TYPE_Q6_K, 4096, 14336),
+])
+def test_gemm_f32_prefill_shapes_sampled(t, N, K):
+    # The Q4_K_M prefill layer's GEMMs at S = 512 (each shape's GEMM algorithm
+    # is picked on its first call): 64 sampled output columns against a
+    # float64 product of the oracle's dequantised rows, and a second call
+    # bit-identical to the first.
+    S = 512
+    G.say(f"kquant: gemm {NAMES[t]} S={S} {N}x{K}, sampled columns")
+    g = np.random.default_rng(800 + N + K + t)
+    W = O.make_typed(g, t, N, K, d_scale=0.07)
+    X = g.standard_normal((S, K)).astype(np.float32)
+    got = gpu_gemm(W, t, X, N, K)
+    again = gpu_gemm(W, t, X, N, K)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    rows = np.sort(g.choice(N, 64, replace=False))
+    Wd = O.dequant_typed(np.ascontiguousarray(W[rows]), t, 64, K)
+    ref = X.astype(np.float64) @ Wd.astype(np.float64).T
+    _assert_close(got[:, rows], ref, _bound(Wd, X), f"gemm {NAMES[t]} S={S} {N}x{K}")
+
+
 def gpu_pack(W, t, N, K):
     L = G.lib()
     dw = DB.from_array(W)
