@@ -371,7 +371,8 @@ int mia_matvec_q8(const void *W, int type, const void *x_q8, float *y, int out_d
  * Q4_K and F16 weights are fp16 values and enter exactly; Q6_K and F32
  * weights are scaled per row by a power of two and split into hi + lo halves
  * (2^-22 relative).  Per-device work areas: out_dim * in_dim * 2 bytes
- * (twice that for Q6_K / F32) and 12 * S * out_dim bytes.  Range as
+ * (twice that for Q6_K / F32), 12 * S * out_dim bytes and a 64 MiB GEMM
+ * workspace.  Range as
  * mia_q4_0_gemm_f32's: every |x| below 65504, below 2^-3 carried to 2^-25
  * absolute. */
 int mia_gemm_f32(const void *W, int type, const float *X, float *Y, int out_dim, int in_dim,
@@ -380,7 +381,8 @@ int mia_gemm_f32(const void *W, int type, const float *X, float *Y, int out_dim,
 /* The same weights converted once, at load time, into the GEMM's operand form
  * (no reference counterpart; the reference dequantises per call,
  * mistral/mistral_ane_prefill.h:1018-1042), so that the per-call conversion
- * drops out: results are bit-identical to mia_gemm_f32's.  Q4_0 is
+ * drops out: results are bit-identical to mia_gemm_f32's in the same process
+ * (the same GEMM algorithm for the shape).  Q4_0 is
  * mia_q4_0_pack_gemm's tile layout (out_dim and in_dim multiples of 64, the
  * size of the GGUF form); Q4_K and F16 become their fp16 values [out_dim]
  * [in_dim] (4x / 1x the Q4_K / F16 bytes); Q6_K and F32 the row-scaled fp16
