@@ -288,6 +288,24 @@ def test_gemm_f32_prefill_shapes_sampled(t, N, K):
     _assert_close(got[:, rows], ref, _bound(Wd, X), f"gemm {NAMES[t]} S={S} {N}x{K}")
 
 
+def test_gemm_f32_many_shapes():
+    # More GEMM shapes than the library remembers algorithms for (64): every
+    # batch size from 1 to 80 on one Q4_K and one Q6_K matrix, each against
+    # the oracle; the shapes past the limit run the heuristic's first
+    # algorithm untimed.
+    G.say("kquant: gemm at 80 batch sizes x 2 types")
+    g = np.random.default_rng(910)
+    N, K = 96, 512
+    for t in (O.TYPE_Q4_K, O.TYPE_Q6_K):
+        W = O.make_typed(g, t, N, K, d_scale=0.07)
+        Wd = O.dequant_typed(W, t, N, K)
+        for S in range(1, 81):
+            X = g.standard_normal((S, K)).astype(np.float32)
+            got = gpu_gemm(W, t, X, N, K)
+            ref = X.astype(np.float64) @ Wd.astype(np.float64).T
+            _assert_close(got, ref, _bound(Wd, X), f"gemm {NAMES[t]} S={S}")
+
+
 def gpu_pack(W, t, N, K):
     L = G.lib()
     dw = DB.from_array(W)
